@@ -1,0 +1,168 @@
+/*
+ * vflorence_amd.h -- C ABI of the MI355X (gfx950) decode-step attention library.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, and a
+ * hipStream_t passed as `void *` (NULL = the legacy default stream).  No entry point
+ * allocates device memory: scratch space is passed in by the caller, sized by
+ * vfl_get_scheduler_metadata().  All work is enqueued asynchronously on `stream`,
+ * in call order, so a caller that issues copy_blocks -> reshape_and_cache ->
+ * attention_with_kv_cache on one stream gets the reference's ordering.
+ *
+ * Return value: VFL_OK (0) or a negative VFL_E_* code; vfl_last_error() then holds
+ * a message for the calling thread.  Arguments are validated on the host before
+ * any launch; out-of-range block ids or slots found on the device are skipped
+ * rather than dereferenced (see each entry point).
+ *
+ * Cache layout (the reference's logical layout, vflorence/engine/model_runner.py:66-77):
+ *   cache[num_blocks][num_heads][block_size][head_dim], contiguous, one tensor per
+ *   layer and per K / V.  Token t of block b, head h lives at
+ *   ((b * num_heads + h) * block_size + t) * head_dim.
+ */
+#ifndef VFLORENCE_AMD_H
+#define VFLORENCE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of caches, queries and outputs */
+enum vfl_dtype { VFL_FLOAT32 = 0, VFL_BFLOAT16 = 1, VFL_FLOAT16 = 2 };
+
+/* status codes */
+enum vfl_status {
+  VFL_OK = 0,
+  VFL_E_INVALID = -1,     /* bad argument (shape, dtype, alignment, size)   */
+  VFL_E_UNSUPPORTED = -2, /* valid but not built (head_dim, block_size ...) */
+  VFL_E_LAUNCH = -3,      /* HIP reported an error at launch                */
+  VFL_E_WORKSPACE = -4    /* workspace missing or too small                 */
+};
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *vfl_last_error(void);
+
+/* Library version, major * 10000 + minor * 100 + patch. */
+int vfl_version(void);
+
+/*
+ * Replaces vllm_cpu_attn.get_isa(dtype, block_size, head_dim)
+ * (vflorence/engine/model_runner.py:38).  There is one code path, so this returns
+ * the GPU target the library was built for ("gfx950"), or NULL when the
+ * (dtype, block_size, head_dim) combination has no kernel.
+ */
+const char *vfl_get_isa(int dtype, int block_size, int head_dim);
+
+/*
+ * Replaces vllm_cpu_attn.reshape_and_cache(key, value, k_cache, v_cache,
+ * slot_mapping, isa=) (vflorence/layers/attention.py:55-57 and
+ * vflorence/engine/model_runner.py:252-259):
+ *
+ *   for t < num_tokens with 0 <= slot_mapping[t] < num_blocks * block_size:
+ *     k_cache[slot / bs][h][slot % bs][:] = key[t][h][:]      (same for value)
+ *
+ * key / value are [num_tokens][num_heads][head_dim] with arbitrary token and head
+ * strides (in elements) and a contiguous last dimension -- the strided views a
+ * fused qkv projection produces.  Negative slots are skipped (padding tokens), as
+ * are slots past the end of the pool.  Bit-exact copy.
+ */
+int vfl_reshape_and_cache(const void *key, const void *value,
+                          int64_t key_stride_token, int64_t key_stride_head,
+                          int64_t value_stride_token, int64_t value_stride_head,
+                          void *k_cache, void *v_cache, const int64_t *slot_mapping,
+                          int64_t num_tokens, int num_heads, int head_dim,
+                          int block_size, int64_t num_blocks, int dtype, void *stream);
+
+/*
+ * Split plan for vfl_attention_with_kv_cache.  Replaces
+ * vllm_cpu_attn.get_scheduler_metadata(...) (vflorence/layers/attention.py:18-29,
+ * vflorence/engine/model_runner.py:308-319): the CPU work partition becomes a
+ * GPU grid shape plus the size of the split-K scratch.
+ */
+typedef struct vfl_sched_meta {
+  int64_t num_rows;           /* query rows the plan was made for                  */
+  int32_t num_heads;          /* heads the plan was made for                       */
+  int32_t head_dim;           /* head size the plan was made for                   */
+  int32_t max_blocks_per_seq; /* block-table width; longer contexts are clamped    */
+  int32_t partition_blocks;   /* KV blocks handled by one workgroup                */
+  int32_t max_partitions;     /* ceil(max_blocks_per_seq / partition_blocks)       */
+  int32_t max_group_size;     /* query rows that share one block-table row (beams) */
+  int32_t heads_per_workgroup;/* one wave per head                                 */
+  size_t workspace_bytes;     /* scratch the call needs (0 if max_partitions == 1) */
+} vfl_sched_meta;
+
+/*
+ * num_rows:           query rows (sequences, beams included)
+ * num_groups:         row groups sharing a block-table row (== num_rows when no
+ *                     rows are grouped)
+ * max_blocks_per_seq: width of the block table
+ * partition_blocks:   0 picks the library default, otherwise forces a size
+ */
+int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_heads,
+                               int head_dim, int block_size,
+                               int64_t max_blocks_per_seq, int max_group_size,
+                               int dtype, int partition_blocks,
+                               vfl_sched_meta *meta);
+
+/*
+ * Replaces vllm_cpu_attn.attention_with_kv_cache(query, k_cache, v_cache, out,
+ * query_start_loc, seq_lens, scale=, causal=, block_table=, scheduler_metadata=)
+ * on its decode path (vflorence/layers/attention.py:61-72 for self-attention,
+ * :98-109 for cross-attention): one query row per sequence,
+ *
+ *   out[r][h][:] = softmax_j(scale * <query[r][h], K_r[j][h]>) V_r[j][h]
+ *
+ * over j < seq_lens[r], where token j of row r lives in block
+ * block_table[r][j / block_size] at offset j % block_size.  Decode queries sit at
+ * the end of their context, so the reference's causal flag changes nothing here.
+ *
+ * Row groups (cross-attention beams): when group_start is non-NULL, group g owns
+ * rows group_start[g] .. group_start[g+1]-1, which must share one block-table row
+ * and one length; the kernel reads that row's K/V once for the whole group.  With
+ * group_start NULL every row is its own group (num_groups == num_rows).
+ *
+ * query: [num_rows][num_heads][head_dim], token / head strides in elements.
+ * out:   [num_rows][num_heads][head_dim], contiguous.
+ * block_table: int32, row stride block_table_stride >= meta->max_blocks_per_seq;
+ *   only entries below min(ceil(seq_lens[r] / bs), meta->max_blocks_per_seq) are
+ *   read (longer contexts are clamped to the table width).
+ * Block ids outside [0, num_blocks) contribute nothing.  seq_lens[r] <= 0 gives a
+ * zero output row.  Accumulation is fp32 for every element type.
+ * meta: from vfl_get_scheduler_metadata for the same num_rows, num_heads and
+ *   head_dim (checked).
+ * workspace: meta->workspace_bytes of device memory (may be NULL when 0); its
+ *   contents need no initialisation and are dead after the call.
+ */
+int vfl_attention_with_kv_cache(const void *query, int64_t query_stride_token,
+                                int64_t query_stride_head, const void *k_cache,
+                                const void *v_cache, void *out,
+                                const int32_t *seq_lens, const int32_t *block_table,
+                                int64_t block_table_stride,
+                                const int32_t *group_start, int64_t num_rows,
+                                int64_t num_groups, int num_heads, int head_dim,
+                                int block_size, int64_t num_blocks, float scale,
+                                int dtype, const vfl_sched_meta *meta,
+                                void *workspace, size_t workspace_bytes,
+                                void *stream);
+
+/*
+ * Replaces ModelRunner._copy_blocks (vflorence/engine/model_runner.py:162-167):
+ * for every cache c < num_caches and pair p < num_pairs,
+ *   caches[c][dst[p]] = caches[c][src[p]]          (block_bytes bytes per block)
+ * with the reference's gather-then-scatter semantics: every source is read before
+ * any destination is written when `staging` is non-NULL (staging must hold
+ * num_caches * num_pairs * block_bytes bytes); with staging NULL the caller
+ * guarantees that no dst block is also a src block.  `caches` is a DEVICE array of
+ * num_caches cache base pointers.  Pairs with an id outside [0, num_blocks) are
+ * skipped.  block_bytes must be a multiple of 16 and every cache 16-byte aligned.
+ */
+int vfl_copy_blocks(void *const *caches, int num_caches, const int64_t *src,
+                    const int64_t *dst, int64_t num_pairs, int64_t block_bytes,
+                    int64_t num_blocks, void *staging, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VFLORENCE_AMD_H */

@@ -1,0 +1,146 @@
+"""The C-ABI library loads, exports what include/vflorence_amd.h declares, and its
+host-side planning and argument checks behave (no GPU work is launched here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vflorence_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vfl_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from vflorence_amd import _lib
+
+    declared = declared_functions()
+    assert declared, "no declarations found"
+    assert sorted(_lib.EXPORTED_SYMBOLS) == declared
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared:
+        assert hasattr(raw, name), name
+
+
+def test_version_and_isa():
+    from vflorence_amd import hip_attn
+    from vflorence_amd._lib import lib
+
+    assert lib.vfl_version() >= 100
+    import torch
+
+    assert hip_attn.get_isa(torch.bfloat16, 16, 64) == "gfx950"
+    assert hip_attn.get_isa(torch.float32, 16, 128) == "gfx950"
+    with pytest.raises(ValueError):
+        hip_attn.get_isa(torch.bfloat16, 32, 64)
+    with pytest.raises(ValueError):
+        hip_attn.get_isa(torch.bfloat16, 16, 80)
+
+
+def plan(rows, groups, heads, dim, max_blocks, gmax=1, pb=0, dtype=1):
+    from vflorence_amd._lib import SchedMeta, lib
+
+    meta = SchedMeta()
+    rc = lib.vfl_get_scheduler_metadata(rows, groups, heads, dim, 16, max_blocks, gmax, dtype, pb,
+                                        ctypes.byref(meta))
+    return rc, meta
+
+
+def test_scheduler_metadata_plan():
+    rc, m = plan(256, 256, 16, 64, 64)
+    assert rc == 0
+    assert m.partition_blocks > 0
+    assert m.max_partitions * m.partition_blocks >= 64
+    assert m.max_partitions == -(-64 // m.partition_blocks)
+    if m.max_partitions > 1:
+        acc = 256 * 16 * m.max_partitions * 64 * 4
+        acc = (acc + 255) // 256 * 256
+        assert m.workspace_bytes == acc + 256 * 16 * m.max_partitions * 8
+    rc, m = plan(10, 10, 16, 64, 3, pb=16)
+    assert rc == 0 and m.max_partitions == 1 and m.workspace_bytes == 0
+    rc, m = plan(8, 2, 12, 64, 40, gmax=4, pb=8)
+    assert rc == 0 and m.max_partitions == 5 and m.max_group_size == 4
+
+
+@pytest.mark.parametrize(
+    "kwargs",
+    [
+        dict(gmax=9),  # beams per group above the compiled maximum
+        dict(gmax=0),
+        dict(dim=80),  # no kernel
+        dict(groups=300),  # more groups than rows
+    ],
+)
+def test_scheduler_metadata_rejects(kwargs):
+    args = dict(rows=256, groups=256, heads=16, dim=64, max_blocks=64)
+    args.update(kwargs)
+    rc, _ = plan(**args)
+    assert rc != 0
+
+
+def test_attention_validates_before_launch():
+    """Bad calls return an error code and a message; nothing is enqueued."""
+    from vflorence_amd._lib import SchedMeta, lib
+
+    rc, meta = plan(4, 4, 16, 64, 8, pb=4)
+    assert rc == 0 and meta.workspace_bytes > 0
+    fake = ctypes.c_void_p(0x1000)
+    # workspace missing
+    rc = lib.vfl_attention_with_kv_cache(fake, 3072, 64, fake, fake, fake, fake, fake, 8, None, 4,
+                                         4, 16, 64, 16, 100, 0.125, 1, ctypes.byref(meta), None, 0,
+                                         None)
+    assert rc == -4
+    assert b"workspace" in lib.vfl_last_error()
+    # metadata made for other sizes
+    rc = lib.vfl_attention_with_kv_cache(fake, 3072, 64, fake, fake, fake, fake, fake, 8, None, 5,
+                                         5, 16, 64, 16, 100, 0.125, 1, ctypes.byref(meta), None, 0,
+                                         None)
+    assert rc == -1
+    # table narrower than the plan
+    rc = lib.vfl_attention_with_kv_cache(fake, 3072, 64, fake, fake, fake, fake, fake, 4, None, 4,
+                                         4, 16, 64, 16, 100, 0.125, 1, ctypes.byref(meta), None, 0,
+                                         None)
+    assert rc == -1
+    # unsupported head size
+    rc = lib.vfl_attention_with_kv_cache(fake, 3072, 64, fake, fake, fake, fake, fake, 8, None, 4,
+                                         4, 16, 96, 16, 100, 0.125, 1, ctypes.byref(meta), None, 0,
+                                         None)
+    assert rc == -2
+    # zero rows is a no-op
+    rc0, meta0 = plan(0, 0, 16, 64, 8)
+    assert rc0 == 0
+    assert lib.vfl_attention_with_kv_cache(None, 0, 0, None, None, None, None, None, 8, None, 0, 0,
+                                           16, 64, 16, 100, 0.125, 1, ctypes.byref(meta0), None, 0,
+                                           None) == 0
+
+
+def test_reshape_and_copy_validate_before_launch():
+    from vflorence_amd._lib import lib
+
+    # bad dtype / head_dim not a multiple of the 16-byte vector
+    assert lib.vfl_reshape_and_cache(None, None, 0, 0, 0, 0, None, None, None, 4, 16, 64, 16, 10,
+                                     7, None) == -1
+    assert lib.vfl_reshape_and_cache(None, None, 0, 0, 0, 0, None, None, None, 4, 16, 60, 16, 10,
+                                     1, None) == -2
+    assert lib.vfl_reshape_and_cache(None, None, 0, 0, 0, 0, None, None, None, 0, 16, 64, 16, 10,
+                                     1, None) == 0
+    assert lib.vfl_copy_blocks(None, 24, None, None, 5, 1000, 10, None, None) == -1  # not /16
+    assert lib.vfl_copy_blocks(None, 24, None, None, 0, 1024, 10, None, None) == 0
+    assert lib.vfl_copy_blocks(None, 24, None, None, 5, 1024, 10, None, None) == -1  # nulls
+
+
+def test_cpu_tensors_are_rejected():
+    import torch
+
+    from vflorence_amd import hip_attn
+
+    k = torch.zeros(4, 2, 16, 64, dtype=torch.bfloat16)
+    x = torch.zeros(3, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        hip_attn.reshape_and_cache(x, x, k, k, torch.zeros(3, dtype=torch.int64))

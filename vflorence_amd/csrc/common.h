@@ -1,0 +1,208 @@
+// Shared device helpers for the gfx950 decode-attention kernels: element traits,
+// 16-byte vector moves, bf16/f16 dot products on the dot2 units, row-local DPP
+// reductions and the C-ABI error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/vflorence_amd.h"
+
+namespace vfl {
+
+// ---------------------------------------------------------------------------
+// error reporting for the C ABI
+// ---------------------------------------------------------------------------
+void set_error(const char *fmt, ...);
+void clear_error();
+int launch_status(const char *what);
+
+// ---------------------------------------------------------------------------
+// element traits: every kernel moves data in 16-byte chunks (one dwordx4 per lane)
+// ---------------------------------------------------------------------------
+template <int DT> struct Elem;
+template <> struct Elem<VFL_FLOAT32> {
+  using T = float;
+  static constexpr int VEC = 4;
+};
+template <> struct Elem<VFL_BFLOAT16> {
+  using T = uint16_t;
+  static constexpr int VEC = 8;
+};
+template <> struct Elem<VFL_FLOAT16> {
+  using T = uint16_t;
+  static constexpr int VEC = 8;
+};
+
+inline int elem_bytes(int dtype) { return dtype == VFL_FLOAT32 ? 4 : 2; }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// fp32 -> bf16 with round-to-nearest-even; NaN becomes the canonical quiet NaN 0x7fc0
+// (the same bits torch's float -> bfloat16 conversion produces).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// <q, k> over one 16-byte chunk, fp32 accumulation.
+template <int DT> __device__ __forceinline__ float dot16(const uint4 &q, const uint4 &k);
+
+template <> __device__ __forceinline__ float dot16<VFL_BFLOAT16>(const uint4 &q, const uint4 &k) {
+  float s = 0.f;
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q.x),
+                                      __builtin_bit_cast(bf16x2_t, k.x), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q.y),
+                                      __builtin_bit_cast(bf16x2_t, k.y), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q.z),
+                                      __builtin_bit_cast(bf16x2_t, k.z), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q.w),
+                                      __builtin_bit_cast(bf16x2_t, k.w), s, false);
+  return s;
+}
+
+template <> __device__ __forceinline__ float dot16<VFL_FLOAT16>(const uint4 &q, const uint4 &k) {
+  float s = 0.f;
+  s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q.x), __builtin_bit_cast(f16x2_t, k.x), s,
+                             false);
+  s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q.y), __builtin_bit_cast(f16x2_t, k.y), s,
+                             false);
+  s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q.z), __builtin_bit_cast(f16x2_t, k.z), s,
+                             false);
+  s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q.w), __builtin_bit_cast(f16x2_t, k.w), s,
+                             false);
+  return s;
+}
+
+template <> __device__ __forceinline__ float dot16<VFL_FLOAT32>(const uint4 &q, const uint4 &k) {
+  float s = __uint_as_float(q.x) * __uint_as_float(k.x);
+  s = fmaf(__uint_as_float(q.y), __uint_as_float(k.y), s);
+  s = fmaf(__uint_as_float(q.z), __uint_as_float(k.z), s);
+  s = fmaf(__uint_as_float(q.w), __uint_as_float(k.w), s);
+  return s;
+}
+
+// Unpack one 16-byte chunk into VEC floats.
+template <int DT> __device__ __forceinline__ void unpack16(const uint4 &v, float *f);
+
+template <> __device__ __forceinline__ void unpack16<VFL_BFLOAT16>(const uint4 &v, float *f) {
+  f[0] = bf16lo(v.x); f[1] = bf16hi(v.x);
+  f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
+  f[4] = bf16lo(v.z); f[5] = bf16hi(v.z);
+  f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
+}
+
+template <> __device__ __forceinline__ void unpack16<VFL_FLOAT16>(const uint4 &v, float *f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f16x2_t h = __builtin_bit_cast(f16x2_t, w[i]);
+    f[2 * i] = (float)h.x;
+    f[2 * i + 1] = (float)h.y;
+  }
+}
+
+template <> __device__ __forceinline__ void unpack16<VFL_FLOAT32>(const uint4 &v, float *f) {
+  f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+  f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+}
+
+// Pack VEC floats into one 16-byte chunk of element type DT (round to nearest even).
+template <int DT> __device__ __forceinline__ uint4 pack16(const float *f);
+
+template <> __device__ __forceinline__ uint4 pack16<VFL_BFLOAT16>(const float *f) {
+  uint4 r;
+  r.x = f32_to_bf16(f[0]) | (f32_to_bf16(f[1]) << 16);
+  r.y = f32_to_bf16(f[2]) | (f32_to_bf16(f[3]) << 16);
+  r.z = f32_to_bf16(f[4]) | (f32_to_bf16(f[5]) << 16);
+  r.w = f32_to_bf16(f[6]) | (f32_to_bf16(f[7]) << 16);
+  return r;
+}
+
+template <> __device__ __forceinline__ uint4 pack16<VFL_FLOAT16>(const float *f) {
+  uint4 r;
+  r.x = f32_to_f16(f[0]) | (f32_to_f16(f[1]) << 16);
+  r.y = f32_to_f16(f[2]) | (f32_to_f16(f[3]) << 16);
+  r.z = f32_to_f16(f[4]) | (f32_to_f16(f[5]) << 16);
+  r.w = f32_to_f16(f[6]) | (f32_to_f16(f[7]) << 16);
+  return r;
+}
+
+template <> __device__ __forceinline__ uint4 pack16<VFL_FLOAT32>(const float *f) {
+  uint4 r;
+  r.x = __float_as_uint(f[0]); r.y = __float_as_uint(f[1]);
+  r.z = __float_as_uint(f[2]); r.w = __float_as_uint(f[3]);
+  return r;
+}
+
+// Load 16 bytes from an address that may be only element-aligned.
+template <int DT>
+__device__ __forceinline__ uint4 load16_unaligned(const typename Elem<DT>::T *p) {
+  if constexpr (DT == VFL_FLOAT32) {
+    uint4 r;
+    r.x = __float_as_uint(p[0]); r.y = __float_as_uint(p[1]);
+    r.z = __float_as_uint(p[2]); r.w = __float_as_uint(p[3]);
+    return r;
+  } else {
+    uint4 r;
+    r.x = (uint32_t)p[0] | ((uint32_t)p[1] << 16);
+    r.y = (uint32_t)p[2] | ((uint32_t)p[3] << 16);
+    r.z = (uint32_t)p[4] | ((uint32_t)p[5] << 16);
+    r.w = (uint32_t)p[6] | ((uint32_t)p[7] << 16);
+    return r;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store16_unaligned(typename Elem<DT>::T *p, const uint4 &v) {
+  if constexpr (DT == VFL_FLOAT32) {
+    p[0] = __uint_as_float(v.x); p[1] = __uint_as_float(v.y);
+    p[2] = __uint_as_float(v.z); p[3] = __uint_as_float(v.w);
+  } else {
+    p[0] = (uint16_t)v.x; p[1] = (uint16_t)(v.x >> 16);
+    p[2] = (uint16_t)v.y; p[3] = (uint16_t)(v.y >> 16);
+    p[4] = (uint16_t)v.z; p[5] = (uint16_t)(v.z >> 16);
+    p[6] = (uint16_t)v.w; p[7] = (uint16_t)(v.w >> 16);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------
+template <int CTRL> __device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+
+// Sum over aligned groups of N consecutive lanes (N = 1..64, power of two); every
+// lane of a group ends with the group's sum.  Within a 16-lane row the partners come
+// from DPP (no LDS traffic): after the quad sums, half-row mirroring pairs each
+// quad with the other quad of its half-row, and row mirroring pairs the halves.
+template <int N> __device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp<DPP_QUAD_XOR1>(x);
+  if constexpr (N >= 4) x += dpp<DPP_QUAD_XOR2>(x);
+  if constexpr (N >= 8) x += dpp<DPP_ROW_HALF_MIRROR>(x);
+  if constexpr (N >= 16) x += dpp<DPP_ROW_MIRROR>(x);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace vfl

@@ -1,0 +1,243 @@
+// KV-cache data movement on gfx950: the slot_mapping scatter that writes new K/V
+// rows into the paged pools, and the batched copy-on-write block copy.  Both are
+// bit-exact byte moves; every lane moves 16-byte chunks so a wave covers 1 KiB per
+// instruction.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "common.h"
+
+namespace vfl {
+
+static thread_local char g_error[512];
+
+void set_error(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_error[0] = '\0'; }
+
+int launch_status(const char *what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(err));
+    return VFL_E_LAUNCH;
+  }
+  return VFL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// reshape_and_cache: one thread per 16-byte chunk of a (token, head) row.
+// ---------------------------------------------------------------------------
+template <int DT, bool ALIGNED>
+__global__ __launch_bounds__(256) void reshape_and_cache_kernel(
+    const typename Elem<DT>::T *__restrict__ key, const typename Elem<DT>::T *__restrict__ value,
+    int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh, typename Elem<DT>::T *__restrict__ kc,
+    typename Elem<DT>::T *__restrict__ vc, const int64_t *__restrict__ slots, int64_t num_tokens,
+    int num_heads, int chunks_per_row, int block_size, int64_t num_slots) {
+  using T = typename Elem<DT>::T;
+  constexpr int VEC = Elem<DT>::VEC;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = num_tokens * num_heads * chunks_per_row;
+  if (idx >= total) return;
+  const int c = (int)(idx % chunks_per_row);
+  const int64_t row = idx / chunks_per_row;
+  const int h = (int)(row % num_heads);
+  const int64_t t = row / num_heads;
+  const int64_t slot = slots[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t blk = slot / block_size;
+  const int off = (int)(slot % block_size);
+  const int head_dim = chunks_per_row * VEC;
+  const int64_t dst = ((blk * num_heads + h) * block_size + off) * head_dim + c * VEC;
+  const T *ks = key + t * k_st + h * k_sh + c * VEC;
+  const T *vs = value + t * v_st + h * v_sh + c * VEC;
+  if constexpr (ALIGNED) {
+    const uint4 kv = *reinterpret_cast<const uint4 *>(ks);
+    const uint4 vv = *reinterpret_cast<const uint4 *>(vs);
+    *reinterpret_cast<uint4 *>(kc + dst) = kv;
+    *reinterpret_cast<uint4 *>(vc + dst) = vv;
+  } else {
+    store16_unaligned<DT>(kc + dst, load16_unaligned<DT>(ks));
+    store16_unaligned<DT>(vc + dst, load16_unaligned<DT>(vs));
+  }
+}
+
+template <int DT>
+static void launch_reshape(bool aligned, const void *key, const void *value, int64_t k_st,
+                           int64_t k_sh, int64_t v_st, int64_t v_sh, void *kc, void *vc,
+                           const int64_t *slots, int64_t T, int H, int D, int BS,
+                           int64_t num_blocks, hipStream_t stream) {
+  using E = typename Elem<DT>::T;
+  const int cpr = D / Elem<DT>::VEC;
+  const int64_t total = T * H * cpr;
+  const int threads = 256;
+  const int64_t blocks = (total + threads - 1) / threads;
+  if (aligned)
+    reshape_and_cache_kernel<DT, true><<<dim3((unsigned)blocks), dim3(threads), 0, stream>>>(
+        (const E *)key, (const E *)value, k_st, k_sh, v_st, v_sh, (E *)kc, (E *)vc, slots, T, H,
+        cpr, BS, num_blocks * BS);
+  else
+    reshape_and_cache_kernel<DT, false><<<dim3((unsigned)blocks), dim3(threads), 0, stream>>>(
+        (const E *)key, (const E *)value, k_st, k_sh, v_st, v_sh, (E *)kc, (E *)vc, slots, T, H,
+        cpr, BS, num_blocks * BS);
+}
+
+// ---------------------------------------------------------------------------
+// copy_blocks: one workgroup per (chunk of a block, pair, cache).  Each thread
+// moves CPT 16-byte chunks, issuing all loads before the stores.
+// mode 0: src -> dst; mode 1: src -> staging; mode 2: staging -> dst.
+// ---------------------------------------------------------------------------
+constexpr int COPY_THREADS = 256;
+constexpr int COPY_CPT = 4;
+constexpr int64_t COPY_BYTES_PER_WG = (int64_t)COPY_THREADS * COPY_CPT * 16;
+
+__global__ __launch_bounds__(COPY_THREADS) void copy_blocks_kernel(
+    void *const *__restrict__ caches, const int64_t *__restrict__ src,
+    const int64_t *__restrict__ dst, int64_t num_pairs, int64_t block_bytes, int64_t num_blocks,
+    int mode, uint8_t *__restrict__ staging) {
+  const int64_t p = blockIdx.y;
+  const int c = blockIdx.z;
+  const int64_t s = src[p], d = dst[p];
+  if (s < 0 || s >= num_blocks || d < 0 || d >= num_blocks) return;
+  uint8_t *base = (uint8_t *)caches[c];
+  const uint8_t *from;
+  uint8_t *to;
+  if (mode == 0) {
+    from = base + s * block_bytes;
+    to = base + d * block_bytes;
+  } else if (mode == 1) {
+    from = base + s * block_bytes;
+    to = staging + ((int64_t)c * num_pairs + p) * block_bytes;
+  } else {
+    from = staging + ((int64_t)c * num_pairs + p) * block_bytes;
+    to = base + d * block_bytes;
+  }
+  const int64_t chunk0 = (int64_t)blockIdx.x * COPY_BYTES_PER_WG / 16 + threadIdx.x;
+  const int64_t nchunks = block_bytes / 16;
+  uint4 v[COPY_CPT];
+#pragma unroll
+  for (int i = 0; i < COPY_CPT; ++i) {
+    const int64_t ch = chunk0 + (int64_t)i * COPY_THREADS;
+    if (ch < nchunks) v[i] = reinterpret_cast<const uint4 *>(from)[ch];
+  }
+#pragma unroll
+  for (int i = 0; i < COPY_CPT; ++i) {
+    const int64_t ch = chunk0 + (int64_t)i * COPY_THREADS;
+    if (ch < nchunks) reinterpret_cast<uint4 *>(to)[ch] = v[i];
+  }
+}
+
+}  // namespace vfl
+
+using namespace vfl;
+
+extern "C" const char *vfl_last_error(void) { return g_error; }
+
+extern "C" int vfl_version(void) { return 100; }
+
+static bool supported_dtype(int dtype) {
+  return dtype == VFL_FLOAT32 || dtype == VFL_BFLOAT16 || dtype == VFL_FLOAT16;
+}
+
+extern "C" int vfl_reshape_and_cache(const void *key, const void *value,
+                                     int64_t key_stride_token, int64_t key_stride_head,
+                                     int64_t value_stride_token, int64_t value_stride_head,
+                                     void *k_cache, void *v_cache, const int64_t *slot_mapping,
+                                     int64_t num_tokens, int num_heads, int head_dim,
+                                     int block_size, int64_t num_blocks, int dtype,
+                                     void *stream) {
+  clear_error();
+  if (!supported_dtype(dtype)) {
+    set_error("reshape_and_cache: unsupported dtype code %d", dtype);
+    return VFL_E_INVALID;
+  }
+  if (num_tokens < 0 || num_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks < 0) {
+    set_error("reshape_and_cache: bad sizes (tokens %lld heads %d head_dim %d block_size %d "
+              "blocks %lld)",
+              (long long)num_tokens, num_heads, head_dim, block_size, (long long)num_blocks);
+    return VFL_E_INVALID;
+  }
+  const int vec = 16 / elem_bytes(dtype);
+  if (head_dim % vec != 0) {
+    set_error("reshape_and_cache: head_dim %d must be a multiple of %d", head_dim, vec);
+    return VFL_E_UNSUPPORTED;
+  }
+  if (num_tokens == 0) return VFL_OK;
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping) {
+    set_error("reshape_and_cache: null pointer argument");
+    return VFL_E_INVALID;
+  }
+  // 16-byte vector path when every source and destination chunk is 16-byte aligned.
+  const uintptr_t align_bits = (uintptr_t)key | (uintptr_t)value | (uintptr_t)k_cache |
+                               (uintptr_t)v_cache;
+  const bool aligned = (align_bits % 16 == 0) && (key_stride_token % vec == 0) &&
+                       (key_stride_head % vec == 0) && (value_stride_token % vec == 0) &&
+                       (value_stride_head % vec == 0);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case VFL_FLOAT32:
+      launch_reshape<VFL_FLOAT32>(aligned, key, value, key_stride_token, key_stride_head,
+                                  value_stride_token, value_stride_head, k_cache, v_cache,
+                                  slot_mapping, num_tokens, num_heads, head_dim, block_size,
+                                  num_blocks, s);
+      break;
+    case VFL_BFLOAT16:
+      launch_reshape<VFL_BFLOAT16>(aligned, key, value, key_stride_token, key_stride_head,
+                                   value_stride_token, value_stride_head, k_cache, v_cache,
+                                   slot_mapping, num_tokens, num_heads, head_dim, block_size,
+                                   num_blocks, s);
+      break;
+    default:
+      launch_reshape<VFL_FLOAT16>(aligned, key, value, key_stride_token, key_stride_head,
+                                  value_stride_token, value_stride_head, k_cache, v_cache,
+                                  slot_mapping, num_tokens, num_heads, head_dim, block_size,
+                                  num_blocks, s);
+      break;
+  }
+  return launch_status("reshape_and_cache");
+}
+
+extern "C" int vfl_copy_blocks(void *const *caches, int num_caches, const int64_t *src,
+                               const int64_t *dst, int64_t num_pairs, int64_t block_bytes,
+                               int64_t num_blocks, void *staging, void *stream) {
+  clear_error();
+  if (num_caches < 0 || num_pairs < 0 || block_bytes <= 0 || block_bytes % 16 != 0) {
+    set_error("copy_blocks: bad sizes (caches %d pairs %lld block_bytes %lld)", num_caches,
+              (long long)num_pairs, (long long)block_bytes);
+    return VFL_E_INVALID;
+  }
+  if (num_caches == 0 || num_pairs == 0) return VFL_OK;
+  if (!caches || !src || !dst) {
+    set_error("copy_blocks: null pointer argument");
+    return VFL_E_INVALID;
+  }
+  if (num_pairs > 65535 || num_caches > 65535) {
+    set_error("copy_blocks: at most 65535 pairs and 65535 caches per call (got %lld, %d)",
+              (long long)num_pairs, num_caches);
+    return VFL_E_INVALID;
+  }
+  if (staging && ((uintptr_t)staging % 16) != 0) {
+    set_error("copy_blocks: staging buffer must be 16-byte aligned");
+    return VFL_E_INVALID;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  const unsigned gx = (unsigned)((block_bytes + COPY_BYTES_PER_WG - 1) / COPY_BYTES_PER_WG);
+  const dim3 grid(gx, (unsigned)num_pairs, (unsigned)num_caches);
+  if (!staging) {
+    copy_blocks_kernel<<<grid, COPY_THREADS, 0, s>>>(caches, src, dst, num_pairs, block_bytes,
+                                                     num_blocks, 0, nullptr);
+  } else {
+    copy_blocks_kernel<<<grid, COPY_THREADS, 0, s>>>(caches, src, dst, num_pairs, block_bytes,
+                                                     num_blocks, 1, (uint8_t *)staging);
+    int st = launch_status("copy_blocks");
+    if (st != VFL_OK) return st;
+    copy_blocks_kernel<<<grid, COPY_THREADS, 0, s>>>(caches, src, dst, num_pairs, block_bytes,
+                                                     num_blocks, 2, (uint8_t *)staging);
+  }
+  return launch_status("copy_blocks");
+}

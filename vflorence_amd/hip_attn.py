@@ -1,0 +1,354 @@
+"""Torch-facing wrappers of the gfx950 C ABI: the counterpart of ``vllm_cpu_attn``.
+
+The reference reaches its attention arithmetic through four functions of the external
+``vllm_cpu_attn`` package (vflorence/layers/attention.py:18,55,61,98;
+vflorence/engine/model_runner.py:38,252,308).  This module offers the same four names
+with the same keyword arguments, plus ``copy_blocks`` for the copy-on-write loop of
+vflorence/engine/model_runner.py:162-167.  Every call validates shapes on the host,
+then enqueues HIP kernels on torch's current stream of the tensors' device.  CPU
+tensors are rejected: there is no host implementation behind these names.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from ._lib import SchedMeta, check, lib
+
+_DTYPE_CODES = {
+    torch.float32: _lib.VFL_FLOAT32,
+    torch.bfloat16: _lib.VFL_BFLOAT16,
+    torch.float16: _lib.VFL_FLOAT16,
+}
+
+# Head sizes with a compiled kernel (the reference accepts more, for its CPU ISAs:
+# vflorence/layers/attention.py:6).  BART and Florence-2 use 64.
+SUPPORTED_HEAD_DIMS = frozenset({64, 128})
+SUPPORTED_BLOCK_SIZES = frozenset({16})
+MAX_GROUP_SIZE = 8
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; use float32, bfloat16 or float16") from None
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "vflorence_amd kernels need HIP device tensors; got a tensor on "
+                f"{t.device} (there is no CPU path)"
+            )
+        if t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def get_isa(dtype: torch.dtype, block_size: int, head_dim: int) -> str:
+    """The GPU target whose kernel serves (dtype, block_size, head_dim).
+
+    Counterpart of ``vllm_cpu_attn.get_isa`` (vflorence/engine/model_runner.py:38);
+    raises ValueError where the reference would have no ISA either.
+    """
+    isa = lib.vfl_get_isa(_dtype_code(dtype), int(block_size), int(head_dim))
+    if isa is None:
+        raise ValueError(
+            f"no gfx950 kernel for dtype={dtype} block_size={block_size} head_dim={head_dim}; "
+            f"supported head_dim {sorted(SUPPORTED_HEAD_DIMS)}, block_size "
+            f"{sorted(SUPPORTED_BLOCK_SIZES)}"
+        )
+    return isa.decode()
+
+
+def reshape_and_cache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    isa: str | None = None,
+) -> None:
+    """``cache[slot // bs, h, slot % bs, :] = key[t, h, :]`` for K and V.
+
+    Counterpart of ``vllm_cpu_attn.reshape_and_cache`` (vflorence/layers/attention.py:55-57,
+    vflorence/engine/model_runner.py:252-259).  key/value are [T, H, D] with any token and
+    head strides and a contiguous last dim; caches are contiguous [NB, H, bs, D]; slots
+    are int64 [T].  Negative slots are skipped.  ``isa`` is accepted and ignored.
+    """
+    dev = _require_gpu(key, value, k_cache, v_cache, slot_mapping)
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError(f"key/value must be [T, H, D] of one shape, got {key.shape}, {value.shape}")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must be [num_blocks, H, block_size, D] of one shape")
+    num_blocks, num_heads, block_size, head_dim = k_cache.shape
+    if key.shape[1:] != (num_heads, head_dim):
+        raise ValueError(f"key is {tuple(key.shape)} but caches hold H={num_heads}, D={head_dim}")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    if key.stride(-1) != 1 or value.stride(-1) != 1:
+        raise ValueError("key/value need a contiguous last dimension")
+    if not (key.dtype == value.dtype == k_cache.dtype == v_cache.dtype):
+        raise ValueError("key, value and caches must share one dtype")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.shape != (key.shape[0],):
+        raise ValueError(f"slot_mapping must be int64 [{key.shape[0]}], got "
+                         f"{slot_mapping.dtype} {tuple(slot_mapping.shape)}")
+    if not slot_mapping.is_contiguous():
+        slot_mapping = slot_mapping.contiguous()
+    check(
+        lib.vfl_reshape_and_cache(
+            key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), value.stride(0),
+            value.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(),
+            key.shape[0], num_heads, head_dim, block_size, num_blocks, _dtype_code(key.dtype),
+            _stream(dev),
+        )
+    )
+
+
+@dataclass(eq=False)
+class SchedulerMetadata:
+    """Work plan for ``attention_with_kv_cache``: the GPU stand-in for the opaque
+    tensor ``vllm_cpu_attn.get_scheduler_metadata`` returns.
+
+    ``group_start`` (device int32 [num_groups + 1]) lists row groups that share one
+    block-table row -- the beams of a request in cross-attention -- so their K/V is
+    read once.  The grid itself is sized at call time from the block table's width,
+    which the host always knows, so no device value is ever read back.  The scratch
+    buffer is reused by every call made with this object; calls on one stream are
+    ordered, so that is safe for the decoder's layer loop.
+    """
+
+    num_heads: int
+    head_dim: int
+    block_size: int
+    dtype: torch.dtype
+    group_start: torch.Tensor | None = None
+    num_groups: int | None = None
+    max_group_size: int = 1
+    partition_blocks: int = 0
+    _plans: dict = field(default_factory=dict, repr=False)
+    _workspace: torch.Tensor | None = field(default=None, repr=False)
+
+    def plan(self, num_rows: int, max_blocks: int) -> SchedMeta:
+        key = (num_rows, max_blocks)
+        meta = self._plans.get(key)
+        if meta is None:
+            meta = SchedMeta()
+            groups = num_rows if self.group_start is None else self.num_groups
+            check(
+                lib.vfl_get_scheduler_metadata(
+                    num_rows, groups, self.num_heads, self.head_dim, self.block_size,
+                    max_blocks, self.max_group_size, _dtype_code(self.dtype),
+                    self.partition_blocks, ctypes.byref(meta),
+                )
+            )
+            self._plans[key] = meta
+        return meta
+
+    def workspace(self, nbytes: int, device: torch.device) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        ws = self._workspace
+        if ws is None or ws.numel() < nbytes or ws.device != device:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            self._workspace = ws
+        return ws
+
+
+def get_scheduler_metadata(
+    *,
+    num_reqs: int,
+    num_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    seq_lens: torch.Tensor | None = None,
+    dtype: torch.dtype,
+    query_start_loc: torch.Tensor | None = None,
+    causal: bool = False,
+    isa: str | None = None,
+    block_size: int,
+    group_start: torch.Tensor | None = None,
+    max_group_size: int = 1,
+    partition_blocks: int = 0,
+) -> SchedulerMetadata:
+    """Counterpart of ``vllm_cpu_attn.get_scheduler_metadata`` (keyword names from
+    vflorence/layers/attention.py:18-29 and vflorence/engine/model_runner.py:308-319).
+
+    ``group_start``/``max_group_size`` are this library's additions: row groups that
+    share K/V pages.  ``seq_lens``, ``query_start_loc``, ``causal`` and ``isa`` are
+    accepted for signature compatibility; the plan does not need them.
+    """
+    if num_kv_heads != num_heads:
+        raise ValueError("grouped-query attention is not supported (num_kv_heads != num_heads)")
+    if head_dim not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim {head_dim} has no gfx950 kernel ({sorted(SUPPORTED_HEAD_DIMS)})")
+    if block_size not in SUPPORTED_BLOCK_SIZES:
+        raise ValueError(f"block_size {block_size} has no gfx950 kernel")
+    if not 1 <= max_group_size <= MAX_GROUP_SIZE:
+        raise ValueError(f"max_group_size must be in [1, {MAX_GROUP_SIZE}]")
+    num_groups = None
+    if group_start is not None:
+        if group_start.dtype != torch.int32 or group_start.dim() != 1:
+            raise ValueError("group_start must be a 1-D int32 tensor")
+        num_groups = group_start.numel() - 1
+    return SchedulerMetadata(
+        num_heads=num_heads,
+        head_dim=head_dim,
+        block_size=block_size,
+        dtype=dtype,
+        group_start=group_start,
+        num_groups=num_groups,
+        max_group_size=max_group_size,
+        partition_blocks=partition_blocks,
+    )
+
+
+def attention_with_kv_cache(
+    query: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    out: torch.Tensor,
+    query_start_loc: torch.Tensor | None,
+    seq_lens: torch.Tensor,
+    *,
+    scale: float,
+    causal: bool = False,
+    block_table: torch.Tensor,
+    scheduler_metadata: SchedulerMetadata | None = None,
+) -> None:
+    """One-query-per-sequence paged attention, written into ``out`` in place.
+
+    Counterpart of ``vllm_cpu_attn.attention_with_kv_cache`` as the reference calls it
+    (vflorence/layers/attention.py:61-72 and :98-109): row r attends to the first
+    ``seq_lens[r]`` tokens of the pages ``block_table[r]`` lists.  ``query_start_loc``
+    must describe one query per sequence (the reference always passes
+    ``arange(N + 1)``, vflorence/engine/model_runner.py:306); with one query at the end of
+    its context ``causal`` changes nothing.
+    """
+    dev = _require_gpu(query, k_cache, v_cache, out, seq_lens, block_table)
+    if query.dim() != 3 or query.stride(-1) != 1:
+        raise ValueError("query must be [N, H, D] with a contiguous last dimension")
+    num_rows, num_heads, head_dim = query.shape
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must be [num_blocks, H, block_size, D] of one shape")
+    num_blocks, cache_heads, block_size, cache_dim = k_cache.shape
+    if (cache_heads, cache_dim) != (num_heads, head_dim):
+        raise ValueError(
+            f"query has H={num_heads}, D={head_dim} but the cache holds H={cache_heads}, "
+            f"D={cache_dim}"
+        )
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    if not (query.dtype == k_cache.dtype == v_cache.dtype == out.dtype):
+        raise ValueError("query, caches and out must share one dtype")
+    if out.shape != query.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of query's shape")
+    if seq_lens.dtype != torch.int32 or seq_lens.shape != (num_rows,):
+        raise ValueError(f"seq_lens must be int32 [{num_rows}], got {seq_lens.dtype} "
+                         f"{tuple(seq_lens.shape)}")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != num_rows:
+        raise ValueError(f"block_table must be int32 [{num_rows}, max_blocks], got "
+                         f"{block_table.dtype} {tuple(block_table.shape)}")
+    if query_start_loc is not None and query_start_loc.numel() != num_rows + 1:
+        raise ValueError("query_start_loc must hold num_seqs + 1 offsets (one query per sequence)")
+    if block_table.stride(1) != 1:
+        block_table = block_table.contiguous()
+    if not seq_lens.is_contiguous():
+        seq_lens = seq_lens.contiguous()
+    sm = scheduler_metadata
+    if sm is None:
+        sm = get_scheduler_metadata(
+            num_reqs=num_rows, num_heads=num_heads, num_kv_heads=num_heads, head_dim=head_dim,
+            dtype=query.dtype, block_size=block_size,
+        )
+    group_start = sm.group_start
+    if group_start is not None:
+        _require_gpu(query, group_start)
+    num_groups = num_rows if group_start is None else sm.num_groups
+    meta = sm.plan(num_rows, block_table.shape[1])
+    ws = sm.workspace(meta.workspace_bytes, dev)
+    check(
+        lib.vfl_attention_with_kv_cache(
+            query.data_ptr(), query.stride(0), query.stride(1), k_cache.data_ptr(),
+            v_cache.data_ptr(), out.data_ptr(), seq_lens.data_ptr(), block_table.data_ptr(),
+            block_table.stride(0), None if group_start is None else group_start.data_ptr(),
+            num_rows, num_groups, num_heads, head_dim, block_size, num_blocks, float(scale),
+            _dtype_code(query.dtype), ctypes.byref(meta),
+            None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+            _stream(dev),
+        )
+    )
+
+
+def cache_pointer_table(caches: list[torch.Tensor]) -> torch.Tensor:
+    """Device int64 tensor of cache base addresses, the ``caches`` argument of copy_blocks."""
+    if not caches:
+        raise ValueError("no caches")
+    dev = _require_gpu(*caches)
+    shape, dtype = caches[0].shape, caches[0].dtype
+    for c in caches:
+        if c.shape != shape or c.dtype != dtype or not c.is_contiguous():
+            raise ValueError("caches must be contiguous tensors of one shape and dtype")
+    return torch.tensor([c.data_ptr() for c in caches], dtype=torch.int64, device=dev)
+
+
+def copy_blocks(
+    caches: list[torch.Tensor],
+    src: torch.Tensor,
+    dst: torch.Tensor,
+    pointer_table: torch.Tensor | None = None,
+    staged: bool = False,
+) -> None:
+    """``cache[dst[p]] = cache[src[p]]`` for every cache and pair, in one launch.
+
+    Counterpart of ModelRunner._copy_blocks (vflorence/engine/model_runner.py:162-167),
+    which runs ``index_copy_(0, dst, index_select(0, src))`` per cache: every source is
+    read before any destination is written.  The caller holds the pairs on the host
+    and passes ``staged=copy_pairs_need_staging(pairs)``: when a destination block is
+    also a source, the copy goes through a staging buffer to keep that order;
+    otherwise it is a single direct pass.
+    """
+    if not caches:
+        return
+    dev = _require_gpu(*caches, src, dst)
+    if src.dtype != torch.int64 or dst.dtype != torch.int64 or src.shape != dst.shape or src.dim() != 1:
+        raise ValueError("src/dst must be int64 vectors of one length")
+    if src.numel() == 0:
+        return
+    if pointer_table is None:
+        pointer_table = cache_pointer_table(caches)
+    elif pointer_table.dtype != torch.int64 or pointer_table.numel() != len(caches):
+        raise ValueError("pointer_table must be int64 with one entry per cache")
+    num_blocks = caches[0].shape[0]
+    block_bytes = caches[0][0].numel() * caches[0].element_size()
+    src = src.contiguous()
+    dst = dst.contiguous()
+    staging = None
+    if staged:
+        staging = torch.empty(len(caches) * src.numel() * block_bytes, dtype=torch.uint8, device=dev)
+    check(
+        lib.vfl_copy_blocks(
+            pointer_table.data_ptr(), len(caches), src.data_ptr(), dst.data_ptr(), src.numel(),
+            block_bytes, num_blocks, None if staging is None else staging.data_ptr(),
+            _stream(dev),
+        )
+    )
+
+
+def copy_pairs_need_staging(pairs: list[tuple[int, int]]) -> bool:
+    """True when a destination block is also a source block; raises on repeated dsts."""
+    dsts = [d for _, d in pairs]
+    if len(set(dsts)) != len(dsts):
+        raise ValueError("copy-on-write pairs repeat a destination block")
+    return not set(dsts).isdisjoint(s for s, _ in pairs)

@@ -1,0 +1,170 @@
+"""Decoder attention custom ops backed by the gfx950 kernels.
+
+Drop-in for vflorence/layers/attention.py: the two opaque ``torch.library`` ops keep
+their names, schemas, mutation annotations and fakes
+(``vflorence::self_attention`` :42-85, ``vflorence::cross_attention`` :88-115), and
+``stage_cross`` (:9-39) keeps its arguments and per-layer tuple layout, so model code
+and ``torch.compile`` of the decoder are unchanged.  The op bodies read the step's
+Context at call time and enqueue HIP kernels on the current stream; nothing runs on
+the CPU.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import hip_attn
+from ..utils.context import get_context
+
+# Head sizes with a gfx950 kernel (the reference lists its CPU ISAs' sizes at :6).
+HEAD_DIMS = set(hip_attn.SUPPORTED_HEAD_DIMS)
+
+
+def beam_groups(pages, enc_lens, max_group: int = hip_attn.MAX_GROUP_SIZE) -> list[int]:
+    """Start offsets of runs of consecutive rows that read the same encoder pages.
+
+    The runner repeats one page tensor for every beam of a request and keeps a
+    request's beams adjacent (vflorence/engine/scheduler.py:121-126), so a run is one
+    request.  Runs are cut at ``max_group`` rows.  Returns ``[0, ..., len(pages)]``.
+    """
+    starts = [0]
+    for i in range(1, len(pages)):
+        same = enc_lens[i] == enc_lens[i - 1] and (
+            pages[i] is pages[i - 1]
+            or (pages[i].shape == pages[i - 1].shape and torch.equal(pages[i], pages[i - 1]))
+        )
+        if not same or i - starts[-1] >= max_group:
+            starts.append(i)
+    starts.append(len(pages))
+    return starts
+
+
+def stage_cross(layers, pages, enc_lens, block_size: int, isa: str):
+    """Point this step's sequences at their encoder K/V pages in each layer's pool.
+
+    ``pages[i]`` (int32 tensor) and ``enc_lens[i]`` belong to running sequence i; beams
+    of one request repeat its pages.  Nothing is copied: the padded block table,
+    lengths and beam groups go to the device once and every layer shares them.
+    """
+    attn = layers[0].encoder_attn
+    device = attn.k_cache.device
+    block_table = torch.nn.utils.rnn.pad_sequence(
+        [p.to(torch.int32).cpu() for p in pages], batch_first=True
+    )
+    starts = beam_groups(pages, enc_lens)
+    max_group = max(b - a for a, b in zip(starts, starts[1:]))
+    n, width, ng = len(pages), block_table.shape[1], len(starts)
+    # One host->device copy: [seq_lens (n) | group starts (ng) | block table (n*width)].
+    host = torch.cat(
+        [
+            torch.tensor(enc_lens, dtype=torch.int32),
+            torch.tensor(starts, dtype=torch.int32),
+            block_table.flatten(),
+        ]
+    )
+    dev = host.to(device)
+    seq_lens = dev[:n]
+    group_start = dev[n : n + ng] if max_group > 1 else None
+    block_table = dev[n + ng :].view(n, width)
+    metadata = hip_attn.get_scheduler_metadata(
+        num_reqs=n,
+        num_heads=attn.num_heads,
+        num_kv_heads=attn.num_heads,
+        head_dim=attn.head_dim,
+        seq_lens=seq_lens,
+        dtype=attn.k_cache.dtype,
+        causal=False,
+        isa=isa,
+        block_size=block_size,
+        group_start=group_start,
+        max_group_size=max_group,
+    )
+    return [
+        (
+            layer.encoder_attn.k_cache,
+            layer.encoder_attn.v_cache,
+            block_table,
+            seq_lens,
+            metadata,
+        )
+        for layer in layers
+    ]
+
+
+def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping, isa=None) -> None:
+    """KV slot write into a paged pool (the runner's encoder path uses it directly)."""
+    hip_attn.reshape_and_cache(key, value, k_cache, v_cache, slot_mapping, isa=isa)
+
+
+@torch.library.custom_op("vflorence::self_attention", mutates_args={"k_cache", "v_cache"})
+def decoder_self_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    scale: float,
+) -> torch.Tensor:
+    """Write new K/V into the paged cache and run self-attention."""
+    ctx = get_context()
+    hip_attn.reshape_and_cache(key, value, k_cache, v_cache, ctx.slot_mapping, isa=ctx.isa)
+    out = query.new_empty(query.shape)
+    # One query per sequence, the newest token; the cache holds nothing after it, so
+    # attending to the whole context is the causal result.
+    hip_attn.attention_with_kv_cache(
+        query,
+        k_cache,
+        v_cache,
+        out,
+        ctx.query_start_loc,
+        ctx.context_lens,
+        scale=scale,
+        causal=False,
+        block_table=ctx.block_tables,
+        scheduler_metadata=ctx.self_metadata,
+    )
+    return out
+
+
+@decoder_self_attention.register_fake
+def _(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    scale: float,
+) -> torch.Tensor:
+    # The op returns a contiguous tensor (for the reference's strided q views,
+    # empty_like gives the same layout).
+    return query.new_empty(query.shape)
+
+
+@torch.library.custom_op("vflorence::cross_attention", mutates_args={})
+def decoder_cross_attention(
+    query: torch.Tensor,
+    layer_idx: int,
+    scale: float,
+) -> torch.Tensor:
+    """Run cross-attention over the staged encoder K/V for decoder layer ``layer_idx``."""
+    ctx = get_context()
+    k_cache, v_cache, block_table, seq_lens, metadata = ctx.cross_staged[layer_idx]
+    out = query.new_empty(query.shape)
+    hip_attn.attention_with_kv_cache(
+        query,
+        k_cache,
+        v_cache,
+        out,
+        ctx.query_start_loc,
+        seq_lens,
+        scale=scale,
+        causal=False,
+        block_table=block_table,
+        scheduler_metadata=metadata,
+    )
+    return out
+
+
+@decoder_cross_attention.register_fake
+def _(query: torch.Tensor, layer_idx: int, scale: float) -> torch.Tensor:
+    return query.new_empty(query.shape)
