@@ -3,10 +3,11 @@
  *
  * Every entry point takes plain device pointers, element strides and sizes, and a
  * hipStream_t passed as `void *` (NULL = the legacy default stream).  No entry point
- * allocates device memory: scratch space is passed in by the caller, sized by
- * vfl_get_scheduler_metadata().  All work is enqueued asynchronously on `stream`,
- * in call order, so a caller that issues copy_blocks -> reshape_and_cache ->
- * attention_with_kv_cache on one stream gets the reference's ordering.
+ * allocates device memory; the one that needs scratch space (vfl_copy_blocks with
+ * overlapping pairs) takes it from the caller.  All work is enqueued asynchronously
+ * on `stream`, in call order, so a caller that issues copy_blocks ->
+ * reshape_and_cache -> attention_with_kv_cache on one stream gets the reference's
+ * ordering.
  *
  * Return value: VFL_OK (0) or a negative VFL_E_* code; vfl_last_error() then holds
  * a message for the calling thread.  Arguments are validated on the host before
@@ -36,8 +37,7 @@ enum vfl_status {
   VFL_OK = 0,
   VFL_E_INVALID = -1,     /* bad argument (shape, dtype, alignment, size)   */
   VFL_E_UNSUPPORTED = -2, /* valid but not built (head_dim, block_size ...) */
-  VFL_E_LAUNCH = -3,      /* HIP reported an error at launch                */
-  VFL_E_WORKSPACE = -4    /* workspace missing or too small                 */
+  VFL_E_LAUNCH = -3       /* HIP reported an error at launch                */
 };
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -75,34 +75,34 @@ int vfl_reshape_and_cache(const void *key, const void *value,
                           int block_size, int64_t num_blocks, int dtype, void *stream);
 
 /*
- * Split plan for vfl_attention_with_kv_cache.  Replaces
+ * Launch plan for vfl_attention_with_kv_cache.  Replaces
  * vllm_cpu_attn.get_scheduler_metadata(...) (vflorence/layers/attention.py:18-29,
- * vflorence/engine/model_runner.py:308-319): the CPU work partition becomes a
- * GPU grid shape plus the size of the split-K scratch.
+ * vflorence/engine/model_runner.py:308-319): the CPU work partition becomes the
+ * number of waves that split one (row group, head) context inside a workgroup.
+ * Pure host computation; no device memory is touched.
  */
 typedef struct vfl_sched_meta {
-  int64_t num_rows;           /* query rows the plan was made for                  */
-  int32_t num_heads;          /* heads the plan was made for                       */
-  int32_t head_dim;           /* head size the plan was made for                   */
-  int32_t max_blocks_per_seq; /* block-table width; longer contexts are clamped    */
-  int32_t partition_blocks;   /* KV blocks handled by one workgroup                */
-  int32_t max_partitions;     /* ceil(max_blocks_per_seq / partition_blocks)       */
-  int32_t max_group_size;     /* query rows that share one block-table row (beams) */
-  int32_t heads_per_workgroup;/* one wave per head                                 */
-  size_t workspace_bytes;     /* scratch the call needs (0 if max_partitions == 1) */
+  int64_t num_rows;            /* query rows the plan was made for                  */
+  int64_t num_groups;          /* row groups the plan was made for                  */
+  int32_t num_heads;           /* heads the plan was made for                       */
+  int32_t head_dim;            /* head size the plan was made for                   */
+  int32_t max_blocks_per_seq;  /* block-table width; longer contexts are clamped    */
+  int32_t waves_per_workgroup; /* waves splitting one (group, head) context: 1..8   */
+  int32_t max_group_size;      /* query rows sharing one block-table row (beams)    */
 } vfl_sched_meta;
 
 /*
- * num_rows:           query rows (sequences, beams included)
- * num_groups:         row groups sharing a block-table row (== num_rows when no
- *                     rows are grouped)
- * max_blocks_per_seq: width of the block table
- * partition_blocks:   0 picks the library default, otherwise forces a size
+ * num_rows:            query rows (sequences, beams included)
+ * num_groups:          row groups sharing a block-table row (== num_rows when no
+ *                      rows are grouped)
+ * max_blocks_per_seq:  width of the block table
+ * max_group_size:      largest group, 1..8
+ * waves_per_workgroup: 0 picks the library default, else 1, 2, 4 or 8
  */
 int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_heads,
                                int head_dim, int block_size,
                                int64_t max_blocks_per_seq, int max_group_size,
-                               int dtype, int partition_blocks,
+                               int dtype, int waves_per_workgroup,
                                vfl_sched_meta *meta);
 
 /*
@@ -121,6 +121,8 @@ int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_hea
  * rows group_start[g] .. group_start[g+1]-1, which must share one block-table row
  * and one length; the kernel reads that row's K/V once for the whole group.  With
  * group_start NULL every row is its own group (num_groups == num_rows).
+ * group_order (optional, int32 [num_groups]): a permutation of the groups giving
+ * the dispatch order (longest first balances the tail); NULL = natural order.
  *
  * query: [num_rows][num_heads][head_dim], token / head strides in elements.
  * out:   [num_rows][num_heads][head_dim], contiguous.
@@ -128,22 +130,20 @@ int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_hea
  *   only entries below min(ceil(seq_lens[r] / bs), meta->max_blocks_per_seq) are
  *   read (longer contexts are clamped to the table width).
  * Block ids outside [0, num_blocks) contribute nothing.  seq_lens[r] <= 0 gives a
- * zero output row.  Accumulation is fp32 for every element type.
- * meta: from vfl_get_scheduler_metadata for the same num_rows, num_heads and
- *   head_dim (checked).
- * workspace: meta->workspace_bytes of device memory (may be NULL when 0); its
- *   contents need no initialisation and are dead after the call.
+ * zero output row.  Accumulation is fp32 for every element type.  One kernel
+ * launch; no scratch memory.
+ * meta: from vfl_get_scheduler_metadata for the same num_rows, num_groups,
+ *   num_heads and head_dim (checked).
  */
 int vfl_attention_with_kv_cache(const void *query, int64_t query_stride_token,
                                 int64_t query_stride_head, const void *k_cache,
                                 const void *v_cache, void *out,
                                 const int32_t *seq_lens, const int32_t *block_table,
                                 int64_t block_table_stride,
-                                const int32_t *group_start, int64_t num_rows,
-                                int64_t num_groups, int num_heads, int head_dim,
-                                int block_size, int64_t num_blocks, float scale,
-                                int dtype, const vfl_sched_meta *meta,
-                                void *workspace, size_t workspace_bytes,
+                                const int32_t *group_start, const int32_t *group_order,
+                                int64_t num_rows, int64_t num_groups, int num_heads,
+                                int head_dim, int block_size, int64_t num_blocks,
+                                float scale, int dtype, const vfl_sched_meta *meta,
                                 void *stream);
 
 /*

@@ -176,7 +176,7 @@ def make_case(lens, H=16, D=64, bs=16, NB=None, dtype=torch.bfloat16, seed=0, st
     return q, kc, vc, torch.tensor(lens, dtype=torch.int32), table
 
 
-def run_gpu(q, kc, vc, lens, table, scale, partition_blocks=0, group_start=None, gmax=1):
+def run_gpu(q, kc, vc, lens, table, scale, waves=0, group_start=None, gmax=1, order=False):
     hip_attn = hip()
     qd = q.to(DEV) if q.is_contiguous() else None
     if qd is None:  # keep the strided layout on the device
@@ -188,8 +188,9 @@ def run_gpu(q, kc, vc, lens, table, scale, partition_blocks=0, group_start=None,
     out = torch.empty(q.shape, dtype=q.dtype, device=DEV)
     meta = hip_attn.get_scheduler_metadata(
         num_reqs=q.shape[0], num_heads=q.shape[1], num_kv_heads=q.shape[1], head_dim=q.shape[2],
-        dtype=q.dtype, block_size=kc.shape[2], partition_blocks=partition_blocks,
+        dtype=q.dtype, block_size=kc.shape[2], waves_per_workgroup=waves,
         group_start=None if group_start is None else group_start.to(DEV), max_group_size=gmax,
+        group_order=group_order(lens, group_start) if order else None,
     )
     hip_attn.attention_with_kv_cache(
         qd, kd, vd, out, torch.arange(q.shape[0] + 1, dtype=torch.int32, device=DEV),
@@ -200,6 +201,12 @@ def run_gpu(q, kc, vc, lens, table, scale, partition_blocks=0, group_start=None,
     return out.cpu()
 
 
+def group_order(lens, group_start):
+    firsts = lens.tolist() if group_start is None else [lens[i].item() for i in group_start[:-1]]
+    order = hip().longest_first(firsts)
+    return torch.tensor(order, dtype=torch.int32, device=DEV)
+
+
 def check(out, q, kc, vc, lens, table, scale):
     want = orc.paged_attention(as_f64(q), as_f64(kc), as_f64(vc), lens.numpy(), table.numpy(),
                                scale)
@@ -208,12 +215,12 @@ def check(out, q, kc, vc, lens, table, scale):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("partition_blocks", [1, 3, 16, 0])
-def test_self_attention_matches_oracle(dtype, head_dim, partition_blocks):
+@pytest.mark.parametrize("waves", [1, 2, 4, 8, 0])
+def test_self_attention_matches_oracle(dtype, head_dim, waves):
     lens = [1, 2, 15, 16, 17, 31, 32, 33, 100, 255, 256, 257, 511, 700, 1024, 64]
     q, kc, vc, L, table = make_case(lens, D=head_dim, dtype=dtype, seed=1)
     scale = head_dim**-0.5
-    out = run_gpu(q, kc, vc, L, table, scale, partition_blocks=partition_blocks)
+    out = run_gpu(q, kc, vc, L, table, scale, waves=waves, order=waves == 4)
     check(out, q, kc, vc, L, table, scale)
 
 
@@ -222,7 +229,7 @@ def test_self_attention_head_counts(H):
     """Florence-2-base has 12 heads; 5 leaves a partly filled workgroup."""
     lens = [40, 300, 1, 129]
     q, kc, vc, L, table = make_case(lens, H=H, seed=2)
-    out = run_gpu(q, kc, vc, L, table, 0.125, partition_blocks=4)
+    out = run_gpu(q, kc, vc, L, table, 0.125, waves=4)
     check(out, q, kc, vc, L, table, 0.125)
 
 
@@ -237,7 +244,7 @@ def test_one_token_context_returns_value_exactly():
 def test_zero_length_rows_give_zeros():
     lens = [0, 50, 0, 7]
     q, kc, vc, L, table = make_case(lens, seed=4)
-    out = run_gpu(q, kc, vc, L, table, 0.125, partition_blocks=2)
+    out = run_gpu(q, kc, vc, L, table, 0.125, waves=2)
     assert not out[0].any() and not out[2].any()
     check(out, q, kc, vc, L, table, 0.125)
 
@@ -321,13 +328,13 @@ def grouped_case(group_sizes, enc_lens, H=16, D=64, dtype=torch.bfloat16, seed=0
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("group_sizes", [[4] * 6, [1, 2, 3, 4], [8, 8, 1], [3] * 5, [2, 7, 5]])
-@pytest.mark.parametrize("partition_blocks", [2, 0])
-def test_grouped_attention_matches_oracle(dtype, group_sizes, partition_blocks):
+@pytest.mark.parametrize("waves", [1, 8, 0])
+def test_grouped_attention_matches_oracle(dtype, group_sizes, waves):
     enc = [256 + 97 * i for i in range(len(group_sizes))]
     q, kc, vc, L, table, starts = grouped_case(group_sizes, enc, dtype=dtype, seed=9)
     gmax = max(group_sizes)
-    out = run_gpu(q, kc, vc, L, table, 0.125, partition_blocks=partition_blocks,
-                  group_start=starts, gmax=gmax)
+    out = run_gpu(q, kc, vc, L, table, 0.125, waves=waves, group_start=starts, gmax=gmax,
+                  order=waves == 0)
     check(out, q, kc, vc, L, table, 0.125)
 
 

@@ -43,11 +43,11 @@ def test_version_and_isa():
         hip_attn.get_isa(torch.bfloat16, 16, 80)
 
 
-def plan(rows, groups, heads, dim, max_blocks, gmax=1, pb=0, dtype=1):
+def plan(rows, groups, heads, dim, max_blocks, gmax=1, nw=0, dtype=1):
     from vflorence_amd._lib import SchedMeta, lib
 
     meta = SchedMeta()
-    rc = lib.vfl_get_scheduler_metadata(rows, groups, heads, dim, 16, max_blocks, gmax, dtype, pb,
+    rc = lib.vfl_get_scheduler_metadata(rows, groups, heads, dim, 16, max_blocks, gmax, dtype, nw,
                                         ctypes.byref(meta))
     return rc, meta
 
@@ -55,17 +55,19 @@ def plan(rows, groups, heads, dim, max_blocks, gmax=1, pb=0, dtype=1):
 def test_scheduler_metadata_plan():
     rc, m = plan(256, 256, 16, 64, 64)
     assert rc == 0
-    assert m.partition_blocks > 0
-    assert m.max_partitions * m.partition_blocks >= 64
-    assert m.max_partitions == -(-64 // m.partition_blocks)
-    if m.max_partitions > 1:
-        acc = 256 * 16 * m.max_partitions * 64 * 4
-        acc = (acc + 255) // 256 * 256
-        assert m.workspace_bytes == acc + 256 * 16 * m.max_partitions * 8
-    rc, m = plan(10, 10, 16, 64, 3, pb=16)
-    assert rc == 0 and m.max_partitions == 1 and m.workspace_bytes == 0
-    rc, m = plan(8, 2, 12, 64, 40, gmax=4, pb=8)
-    assert rc == 0 and m.max_partitions == 5 and m.max_group_size == 4
+    assert (m.num_rows, m.num_groups, m.num_heads, m.head_dim) == (256, 256, 16, 64)
+    assert m.max_blocks_per_seq == 64 and m.max_group_size == 1
+    assert m.waves_per_workgroup in (1, 2, 4, 8)
+    # 4096 workgroups: two waves each reach the 8192-wave target
+    assert m.waves_per_workgroup == 2
+    # cross-attention of 64 requests x 4 beams: 1024 workgroups -> 8 waves
+    rc, m = plan(256, 64, 16, 64, 64, gmax=4)
+    assert rc == 0 and m.waves_per_workgroup == 8 and m.max_group_size == 4
+    # never more waves than blocks in the longest context
+    rc, m = plan(4, 4, 16, 64, 1)
+    assert rc == 0 and m.waves_per_workgroup == 1
+    rc, m = plan(8, 2, 12, 64, 40, gmax=4, nw=4)
+    assert rc == 0 and m.waves_per_workgroup == 4
 
 
 @pytest.mark.parametrize(
@@ -75,6 +77,8 @@ def test_scheduler_metadata_plan():
         dict(gmax=0),
         dict(dim=80),  # no kernel
         dict(groups=300),  # more groups than rows
+        dict(nw=3),  # not a power of two
+        dict(nw=16),
     ],
 )
 def test_scheduler_metadata_rejects(kwargs):
@@ -86,37 +90,35 @@ def test_scheduler_metadata_rejects(kwargs):
 
 def test_attention_validates_before_launch():
     """Bad calls return an error code and a message; nothing is enqueued."""
-    from vflorence_amd._lib import SchedMeta, lib
+    from vflorence_amd._lib import lib
 
-    rc, meta = plan(4, 4, 16, 64, 8, pb=4)
-    assert rc == 0 and meta.workspace_bytes > 0
+    rc, meta = plan(4, 4, 16, 64, 8, nw=4)
+    assert rc == 0
     fake = ctypes.c_void_p(0x1000)
-    # workspace missing
-    rc = lib.vfl_attention_with_kv_cache(fake, 3072, 64, fake, fake, fake, fake, fake, 8, None, 4,
-                                         4, 16, 64, 16, 100, 0.125, 1, ctypes.byref(meta), None, 0,
-                                         None)
-    assert rc == -4
-    assert b"workspace" in lib.vfl_last_error()
+
+    def call(rows=4, groups=4, dim=64, stride=8, meta_=meta, q=fake, kc=fake, group_start=None):
+        return lib.vfl_attention_with_kv_cache(q, 3072, 64, kc, fake, fake, fake, fake, stride,
+                                               group_start, None, rows, groups, 16, dim, 16, 100,
+                                               0.125, 1, ctypes.byref(meta_), None)
+
     # metadata made for other sizes
-    rc = lib.vfl_attention_with_kv_cache(fake, 3072, 64, fake, fake, fake, fake, fake, 8, None, 5,
-                                         5, 16, 64, 16, 100, 0.125, 1, ctypes.byref(meta), None, 0,
-                                         None)
-    assert rc == -1
+    assert call(rows=5, groups=5) == -1
+    assert b"metadata" in lib.vfl_last_error()
     # table narrower than the plan
-    rc = lib.vfl_attention_with_kv_cache(fake, 3072, 64, fake, fake, fake, fake, fake, 4, None, 4,
-                                         4, 16, 64, 16, 100, 0.125, 1, ctypes.byref(meta), None, 0,
-                                         None)
-    assert rc == -1
+    assert call(stride=4) == -1
     # unsupported head size
-    rc = lib.vfl_attention_with_kv_cache(fake, 3072, 64, fake, fake, fake, fake, fake, 8, None, 4,
-                                         4, 16, 96, 16, 100, 0.125, 1, ctypes.byref(meta), None, 0,
-                                         None)
-    assert rc == -2
+    assert call(dim=96) == -2
+    # grouped counts without a group table
+    rc2, meta2 = plan(4, 2, 16, 64, 8)
+    assert call(groups=2, meta_=meta2) == -1
+    # null / misaligned pointers
+    assert call(q=None) == -1
+    assert call(kc=ctypes.c_void_p(0x1008)) == -1
     # zero rows is a no-op
     rc0, meta0 = plan(0, 0, 16, 64, 8)
     assert rc0 == 0
-    assert lib.vfl_attention_with_kv_cache(None, 0, 0, None, None, None, None, None, 8, None, 0, 0,
-                                           16, 64, 16, 100, 0.125, 1, ctypes.byref(meta0), None, 0,
+    assert lib.vfl_attention_with_kv_cache(None, 0, 0, None, None, None, None, None, 8, None, None,
+                                           0, 0, 16, 64, 16, 100, 0.125, 1, ctypes.byref(meta0),
                                            None) == 0
 
 

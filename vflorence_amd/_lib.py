@@ -34,24 +34,16 @@ class SchedMeta(ctypes.Structure):
 
     _fields_ = [
         ("num_rows", ctypes.c_int64),
+        ("num_groups", ctypes.c_int64),
         ("num_heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
         ("max_blocks_per_seq", ctypes.c_int32),
-        ("partition_blocks", ctypes.c_int32),
-        ("max_partitions", ctypes.c_int32),
+        ("waves_per_workgroup", ctypes.c_int32),
         ("max_group_size", ctypes.c_int32),
-        ("heads_per_workgroup", ctypes.c_int32),
-        ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
-_i64, _i32, _vp, _f32, _sz = (
-    ctypes.c_int64,
-    ctypes.c_int,
-    ctypes.c_void_p,
-    ctypes.c_float,
-    ctypes.c_size_t,
-)
+_i64, _i32, _vp, _f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float
 
 _SIGNATURES = {
     "vfl_last_error": (ctypes.c_char_p, []),
@@ -68,8 +60,8 @@ _SIGNATURES = {
     ),
     "vfl_attention_with_kv_cache": (
         ctypes.c_int,
-        [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _i32,
-         _i64, _f32, _i32, ctypes.POINTER(SchedMeta), _vp, _sz, _vp],
+        [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _i32,
+         _i64, _f32, _i32, ctypes.POINTER(SchedMeta), _vp],
     ),
     "vfl_copy_blocks": (
         ctypes.c_int,

@@ -4,31 +4,23 @@
 // so a request's beams share one read of its pages).
 //
 // Work decomposition
-//   grid = (partition, row group, head group); one wave per head, NW heads per
-//   workgroup, so a workgroup reads NW adjacent 2 KiB head slices of each block.
-//   A partition covers `part_blocks` consecutive blocks of the group's context.
-//   Groups with one partition write the output directly; longer ones write fp32
-//   partials (unnormalised accumulator, running max, running sum) that
-//   paged_decode_reduce_kernel merges.
+//   grid = (head, row group); the workgroup's NW waves split the group's context
+//   into NW contiguous runs of blocks and merge their softmax states through LDS at
+//   the end, so each (group, head) is one workgroup and one launch does the whole
+//   op (no partial buffers, no second kernel).  An optional host-computed order
+//   dispatches the longest groups first.
 //
 // Lane layout inside a wave (bf16, head_dim 64): a 16-byte load per lane covers
-//   8 token rows x 64 dims (1 KiB, fully coalesced).  Lane = tok * LPT + c holds
-//   dims [c*VEC, c*VEC+VEC) of token row `tok`.  Scores are summed over the LPT
-//   lanes of a row with DPP; each of the TPL token rows keeps its own online
-//   softmax state, merged across rows once at the end (no cross-row traffic in the
-//   loop).
+//   8 token rows x 64 dims (1 KiB, fully coalesced); a block's 2 KiB head slice is
+//   two loads.  Lane = tok * LPT + c holds dims [c*VEC, c*VEC+VEC) of token row
+//   `tok`.  Scores are summed over the LPT lanes of a row with DPP; each of the TPL
+//   token rows keeps its own online-softmax state, merged across rows once at the
+//   end (no cross-row traffic in the loop).
 #include "common.h"
 
 namespace vfl {
 
 constexpr float NEG_INF = -__builtin_huge_valf();
-
-template <int DT, int D, int BS, int G> struct DecodeState {
-  static constexpr int VEC = Elem<DT>::VEC;
-  float m[G];
-  float l[G];
-  float acc[G][VEC];
-};
 
 // Fold NT loaded token rows (K chunks kr, V chunks vr) into the running state of
 // every live row of the group.  MASKED selects per-lane validity `valid[j]`.
@@ -78,15 +70,23 @@ __device__ __forceinline__ void consume(const uint4 (&qv)[G], const uint4 *kr, c
   }
 }
 
+template <int DT> __device__ __forceinline__ typename Elem<DT>::T to_elem(float v) {
+  if constexpr (DT == VFL_FLOAT32)
+    return v;
+  else if constexpr (DT == VFL_BFLOAT16)
+    return (typename Elem<DT>::T)f32_to_bf16(v);
+  else
+    return (typename Elem<DT>::T)f32_to_f16(v);
+}
+
 template <int DT, int D, int BS, int G, int NW, int U>
 __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
     const typename Elem<DT>::T *__restrict__ q, int64_t q_st, int64_t q_sh,
     const typename Elem<DT>::T *__restrict__ kc, const typename Elem<DT>::T *__restrict__ vc,
-    typename Elem<DT>::T *__restrict__ out, float *__restrict__ ws_acc,
-    float2 *__restrict__ ws_ml, const int32_t *__restrict__ seq_lens,
+    typename Elem<DT>::T *__restrict__ out, const int32_t *__restrict__ seq_lens,
     const int32_t *__restrict__ bt, int64_t bt_stride, int max_blocks,
-    const int32_t *__restrict__ group_start, int64_t num_rows, int H, int64_t num_blocks,
-    int part_blocks, int max_parts, float scale_log2) {
+    const int32_t *__restrict__ group_start, const int32_t *__restrict__ group_order,
+    int64_t num_rows, int64_t num_groups, int H, int64_t num_blocks, float scale_log2) {
   using T = typename Elem<DT>::T;
   constexpr int VEC = Elem<DT>::VEC;
   constexpr int LPT = D / VEC;   // lanes per token row
@@ -94,18 +94,23 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
   constexpr int NLD = BS / TPL;  // loads per block per head
   static_assert(D % VEC == 0 && 64 % LPT == 0 && BS % TPL == 0, "unsupported tile");
 
+  // Per-wave softmax states for the cross-wave merge.
+  __shared__ float s_acc[NW > 1 ? NW : 1][G][D];
+  __shared__ float s_ml[NW > 1 ? NW : 1][G][2];
+
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int h = blockIdx.z * NW + wave;
-  if (h >= H) return;
-  const int g = blockIdx.y;
-  const int p = blockIdx.x;
+  // 1-D grid, head fastest: a group's heads are dispatched together.
+  const int h = (int)(blockIdx.x % (unsigned)H);
+  int g = (int)(blockIdx.x / (unsigned)H);
+  if (group_order) g = group_order[g];
+  // Workgroup-uniform exits only (before any barrier).
+  if (g < 0 || g >= num_groups || h >= H) return;
   int row0 = g, nrows = 1;
   if (group_start) {
     row0 = group_start[g];
     nrows = min(group_start[g + 1] - row0, G);
   }
-  // A malformed group table must not send the kernel outside the rows it was given.
   if (row0 < 0 || row0 >= num_rows) return;
   nrows = (int)min((int64_t)nrows, num_rows - row0);
   if (nrows <= 0) return;
@@ -117,17 +122,17 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
   const int c = lane % LPT;
 
   if (nblk == 0) {
-    if (p == 0 && tok == 0) {
-      const uint4 z = make_uint4(0, 0, 0, 0);
-      for (int gi = 0; gi < nrows; ++gi)
-        *reinterpret_cast<uint4 *>(out + ((int64_t)(row0 + gi) * H + h) * D + c * VEC) = z;
+    for (int i = threadIdx.x; i < nrows * D; i += NW * 64) {
+      const int gi = i / D, d = i % D;
+      out[((int64_t)(row0 + gi) * H + h) * D + d] = to_elem<DT>(0.f);
     }
     return;
   }
-  const int b0 = p * part_blocks;
-  if (b0 >= nblk) return;
-  const int b1 = min(nblk, b0 + part_blocks);
-  const int nparts = (nblk + part_blocks - 1) / part_blocks;
+
+  // This wave's run of blocks.
+  const int chunk = (nblk + NW - 1) / NW;
+  const int b0 = min(nblk, wave * chunk);
+  const int b1 = min(nblk, b0 + chunk);
 
   uint4 qv[G];
 #pragma unroll
@@ -219,145 +224,110 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
     }
   }
 
-  if (tok != 0) return;
+  if constexpr (NW == 1) {
+    if (tok != 0) return;
 #pragma unroll
-  for (int gi = 0; gi < G; ++gi) {
-    if (gi >= nrows) break;
-    const int64_t rh = (int64_t)(row0 + gi) * H + h;
-    if (nparts == 1) {
+    for (int gi = 0; gi < G; ++gi) {
+      if (gi >= nrows) break;
       const float inv = l[gi] > 0.f ? 1.f / l[gi] : 0.f;
       float o[VEC];
 #pragma unroll
       for (int d = 0; d < VEC; ++d) o[d] = acc[gi][d] * inv;
-      *reinterpret_cast<uint4 *>(out + rh * D + c * VEC) = pack16<DT>(o);
-    } else {
-      float *dst = ws_acc + (rh * max_parts + p) * D + c * VEC;
-#pragma unroll
-      for (int d = 0; d < VEC; d += 4)
-        *reinterpret_cast<float4 *>(dst + d) =
-            make_float4(acc[gi][d], acc[gi][d + 1], acc[gi][d + 2], acc[gi][d + 3]);
-      if (c == 0) ws_ml[rh * max_parts + p] = make_float2(m[gi], l[gi]);
+      *reinterpret_cast<uint4 *>(out + ((int64_t)(row0 + gi) * H + h) * D + c * VEC) =
+          pack16<DT>(o);
     }
-  }
-}
-
-// Merge the partitions of every group that needed more than one.
-template <int DT, int D, int BS, int G, int NW>
-__global__ __launch_bounds__(NW * 64) void paged_decode_reduce_kernel(
-    typename Elem<DT>::T *__restrict__ out, const float *__restrict__ ws_acc,
-    const float2 *__restrict__ ws_ml, const int32_t *__restrict__ seq_lens,
-    const int32_t *__restrict__ group_start, int64_t num_rows, int H, int max_blocks,
-    int part_blocks, int max_parts) {
-  using T = typename Elem<DT>::T;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int h = blockIdx.y * NW + wave;
-  if (h >= H) return;
-  const int g = blockIdx.x;
-  int row0 = g, nrows = 1;
-  if (group_start) {
-    row0 = group_start[g];
-    nrows = min(group_start[g + 1] - row0, G);
-  }
-  if (row0 < 0 || row0 >= num_rows) return;
-  nrows = (int)min((int64_t)nrows, num_rows - row0);
-  const int L = seq_lens[row0];
-  int nblk = L > 0 ? (L + BS - 1) / BS : 0;
-  nblk = min(nblk, max_blocks);
-  const int nparts = (nblk + part_blocks - 1) / part_blocks;
-  if (nparts <= 1) return;
-  for (int gi = 0; gi < nrows; ++gi) {
-    const int64_t rh = (int64_t)(row0 + gi) * H + h;
-    const float2 *ml = ws_ml + rh * max_parts;
-    float M = NEG_INF;
-    for (int pp = 0; pp < nparts; ++pp) M = fmaxf(M, ml[pp].x);
-    const float Ms = (M == NEG_INF) ? 0.f : M;
-    float Ls = 0.f;
-    float o[(D + 63) / 64];
+  } else {
+    // Cross-wave merge through LDS.
+    if (tok == 0) {
 #pragma unroll
-    for (int k = 0; k < (D + 63) / 64; ++k) o[k] = 0.f;
-    for (int pp = 0; pp < nparts; ++pp) {
-      const float2 mlp = ml[pp];
-      const float w = fast_exp2(mlp.x - Ms);
-      Ls = fmaf(mlp.y, w, Ls);
-      const float *a = ws_acc + (rh * max_parts + pp) * D;
+      for (int gi = 0; gi < G; ++gi) {
+        if (gi >= nrows) break;
 #pragma unroll
-      for (int k = 0; k < (D + 63) / 64; ++k) {
-        const int d = lane + 64 * k;
-        if (d < D) o[k] = fmaf(a[d], w, o[k]);
+        for (int d = 0; d < VEC; ++d) s_acc[wave][gi][c * VEC + d] = acc[gi][d];
+        if (c == 0) {
+          s_ml[wave][gi][0] = m[gi];
+          s_ml[wave][gi][1] = l[gi];
+        }
       }
     }
-    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+    __syncthreads();
+    for (int i = threadIdx.x; i < nrows * D; i += NW * 64) {
+      const int gi = i / D, d = i % D;
+      float M = NEG_INF;
 #pragma unroll
-    for (int k = 0; k < (D + 63) / 64; ++k) {
-      const int d = lane + 64 * k;
-      if (d >= D) continue;
-      const float v = o[k] * inv;
-      if constexpr (DT == VFL_FLOAT32)
-        out[rh * D + d] = v;
-      else if constexpr (DT == VFL_BFLOAT16)
-        out[rh * D + d] = (T)f32_to_bf16(v);
-      else
-        out[rh * D + d] = (T)f32_to_f16(v);
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_ml[w][gi][0]);
+      const float Ms = (M == NEG_INF) ? 0.f : M;
+      float S = 0.f, o = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float f = fast_exp2(s_ml[w][gi][0] - Ms);
+        S = fmaf(s_ml[w][gi][1], f, S);
+        o = fmaf(s_acc[w][gi][d], f, o);
+      }
+      out[((int64_t)(row0 + gi) * H + h) * D + d] = to_elem<DT>(S > 0.f ? o / S : 0.f);
     }
   }
 }
 
-constexpr int NW_HEADS = 4;  // heads (waves) per workgroup
-constexpr int UNROLL = 2;    // whole blocks per fast-path step
+// Whole blocks per fast-path step: about four 16-byte K loads (and four V loads)
+// in flight per lane, so fp32 and head_dim 128 (more loads per block) unroll less.
+template <int DT, int D> constexpr int unroll_blocks() {
+  constexpr int nld = 16 / (64 / (D / Elem<DT>::VEC));
+  return nld >= 4 ? 1 : 4 / nld;
+}
 
 struct AttnArgs {
   const void *q;
   int64_t q_st, q_sh;
   const void *kc, *vc;
   void *out;
-  float *ws_acc;
-  float2 *ws_ml;
   const int32_t *seq_lens, *bt;
   int64_t bt_stride;
   int max_blocks;
-  const int32_t *group_start;
+  const int32_t *group_start, *group_order;
   int64_t num_rows, num_groups;
   int H;
   int64_t num_blocks;
-  int part_blocks, max_parts;
   float scale_log2;
   hipStream_t stream;
 };
 
-template <int DT, int D, int G>
+template <int DT, int D, int G, int NW>
 static int launch_attention(const AttnArgs &a) {
   using T = typename Elem<DT>::T;
   constexpr int BS = 16;
-  const dim3 block(NW_HEADS * 64);
-  const unsigned hz = (unsigned)((a.H + NW_HEADS - 1) / NW_HEADS);
-  const dim3 grid((unsigned)a.max_parts, (unsigned)a.num_groups, hz);
-  paged_decode_kernel<DT, D, BS, G, NW_HEADS, UNROLL><<<grid, block, 0, a.stream>>>(
-      (const T *)a.q, a.q_st, a.q_sh, (const T *)a.kc, (const T *)a.vc, (T *)a.out, a.ws_acc,
-      a.ws_ml, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start, a.num_rows, a.H,
-      a.num_blocks, a.part_blocks, a.max_parts, a.scale_log2);
-  int st = launch_status("attention_with_kv_cache");
-  if (st != VFL_OK || a.max_parts <= 1) return st;
-  const dim3 rgrid((unsigned)a.num_groups, hz);
-  paged_decode_reduce_kernel<DT, D, BS, G, NW_HEADS><<<rgrid, block, 0, a.stream>>>(
-      (T *)a.out, a.ws_acc, a.ws_ml, a.seq_lens, a.group_start, a.num_rows, a.H, a.max_blocks,
-      a.part_blocks, a.max_parts);
-  return launch_status("attention_with_kv_cache (reduce)");
+  const dim3 grid((unsigned)(a.num_groups * a.H));
+  paged_decode_kernel<DT, D, BS, G, NW, unroll_blocks<DT, D>()><<<grid, dim3(NW * 64), 0,
+                                                                    a.stream>>>(
+      (const T *)a.q, a.q_st, a.q_sh, (const T *)a.kc, (const T *)a.vc, (T *)a.out, a.seq_lens,
+      a.bt, a.bt_stride, a.max_blocks, a.group_start, a.group_order, a.num_rows, a.num_groups,
+      a.H, a.num_blocks, a.scale_log2);
+  return launch_status("attention_with_kv_cache");
+}
+
+template <int DT, int D, int G>
+static int dispatch_waves(const AttnArgs &a, int nw) {
+  switch (nw) {
+    case 1: return launch_attention<DT, D, G, 1>(a);
+    case 2: return launch_attention<DT, D, G, 2>(a);
+    case 4: return launch_attention<DT, D, G, 4>(a);
+    default: return launch_attention<DT, D, G, 8>(a);
+  }
 }
 
 template <int DT, int D>
-static int dispatch_group(const AttnArgs &a, int gmax) {
-  if (gmax <= 1) return launch_attention<DT, D, 1>(a);
-  if (gmax <= 2) return launch_attention<DT, D, 2>(a);
-  if (gmax <= 4) return launch_attention<DT, D, 4>(a);
-  return launch_attention<DT, D, 8>(a);
+static int dispatch_group(const AttnArgs &a, int gmax, int nw) {
+  if (gmax <= 1) return dispatch_waves<DT, D, 1>(a, nw);
+  if (gmax <= 2) return dispatch_waves<DT, D, 2>(a, nw);
+  if (gmax <= 4) return dispatch_waves<DT, D, 4>(a, nw);
+  return dispatch_waves<DT, D, 8>(a, nw);
 }
 
 template <int DT>
-static int dispatch_dim(const AttnArgs &a, int head_dim, int gmax) {
+static int dispatch_dim(const AttnArgs &a, int head_dim, int gmax, int nw) {
   switch (head_dim) {
-    case 64: return dispatch_group<DT, 64>(a, gmax);
-    case 128: return dispatch_group<DT, 128>(a, gmax);
+    case 64: return dispatch_group<DT, 64>(a, gmax, nw);
+    case 128: return dispatch_group<DT, 128>(a, gmax, nw);
     default: break;
   }
   set_error("attention_with_kv_cache: head_dim %d has no kernel (built: 64, 128)", head_dim);
@@ -369,15 +339,19 @@ static bool kernel_exists(int dtype, int block_size, int head_dim) {
          block_size == 16 && (head_dim == 64 || head_dim == 128);
 }
 
-static size_t workspace_for(int64_t rows, int H, int D, int max_parts) {
-  if (max_parts <= 1) return 0;
-  const size_t parts = (size_t)rows * H * max_parts;
-  size_t acc_bytes = parts * D * sizeof(float);
-  acc_bytes = (acc_bytes + 255) & ~(size_t)255;
-  return acc_bytes + parts * sizeof(float2);
-}
-
 constexpr int MAX_GROUP = 8;
+constexpr int MAX_WAVES = 8;
+// Waves the default plan aims to have in flight: 256 CUs x 32 wave slots.
+constexpr int64_t TARGET_WAVES = 256 * 32;
+
+static int default_waves(int64_t num_groups, int num_heads, int64_t max_blocks) {
+  const int64_t wgs = num_groups * num_heads;
+  int nw = 1;
+  while (nw < MAX_WAVES && wgs * nw < TARGET_WAVES) nw *= 2;
+  // No more waves than blocks in the longest context.
+  while (nw > 1 && nw / 2 >= max_blocks) nw /= 2;
+  return nw;
+}
 
 }  // namespace vfl
 
@@ -390,14 +364,15 @@ extern "C" const char *vfl_get_isa(int dtype, int block_size, int head_dim) {
 extern "C" int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_heads,
                                           int head_dim, int block_size,
                                           int64_t max_blocks_per_seq, int max_group_size,
-                                          int dtype, int partition_blocks, vfl_sched_meta *meta) {
+                                          int dtype, int waves_per_workgroup,
+                                          vfl_sched_meta *meta) {
   clear_error();
   if (!meta) {
     set_error("get_scheduler_metadata: meta is NULL");
     return VFL_E_INVALID;
   }
   if (num_rows < 0 || num_groups < 0 || num_groups > num_rows || num_heads <= 0 ||
-      max_blocks_per_seq < 0 || max_blocks_per_seq > (1 << 30) || partition_blocks < 0) {
+      num_heads > 65535 || max_blocks_per_seq < 0 || max_blocks_per_seq > (1 << 30)) {
     set_error("get_scheduler_metadata: bad sizes (rows %lld groups %lld heads %d blocks %lld)",
               (long long)num_rows, (long long)num_groups, num_heads,
               (long long)max_blocks_per_seq);
@@ -413,24 +388,23 @@ extern "C" int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, 
               MAX_GROUP);
     return VFL_E_UNSUPPORTED;
   }
-  int pb = partition_blocks;
-  if (pb == 0) pb = 16;
-  const int64_t mb = max_blocks_per_seq > 0 ? max_blocks_per_seq : 1;
-  const int64_t parts = (mb + pb - 1) / pb;
-  if (parts > 65535 || num_groups > 65535) {
-    set_error("get_scheduler_metadata: grid too large (%lld partitions, %lld groups)",
-              (long long)parts, (long long)num_groups);
+  int nw = waves_per_workgroup;
+  if (nw == 0) nw = default_waves(num_groups, num_heads, max_blocks_per_seq);
+  if (nw != 1 && nw != 2 && nw != 4 && nw != 8) {
+    set_error("get_scheduler_metadata: waves_per_workgroup %d not in {0, 1, 2, 4, 8}", nw);
+    return VFL_E_UNSUPPORTED;
+  }
+  if (num_groups * num_heads > 2147483647LL) {
+    set_error("get_scheduler_metadata: too many groups x heads for one grid");
     return VFL_E_UNSUPPORTED;
   }
   meta->num_rows = num_rows;
+  meta->num_groups = num_groups;
   meta->num_heads = num_heads;
   meta->head_dim = head_dim;
   meta->max_blocks_per_seq = (int32_t)max_blocks_per_seq;
-  meta->partition_blocks = pb;
-  meta->max_partitions = (int32_t)parts;
+  meta->waves_per_workgroup = nw;
   meta->max_group_size = max_group_size;
-  meta->heads_per_workgroup = NW_HEADS;
-  meta->workspace_bytes = workspace_for(num_rows, num_heads, head_dim, (int)parts);
   return VFL_OK;
 }
 
@@ -438,9 +412,9 @@ extern "C" int vfl_attention_with_kv_cache(
     const void *query, int64_t query_stride_token, int64_t query_stride_head,
     const void *k_cache, const void *v_cache, void *out, const int32_t *seq_lens,
     const int32_t *block_table, int64_t block_table_stride, const int32_t *group_start,
-    int64_t num_rows, int64_t num_groups, int num_heads, int head_dim, int block_size,
-    int64_t num_blocks, float scale, int dtype, const vfl_sched_meta *meta, void *workspace,
-    size_t workspace_bytes, void *stream) {
+    const int32_t *group_order, int64_t num_rows, int64_t num_groups, int num_heads,
+    int head_dim, int block_size, int64_t num_blocks, float scale, int dtype,
+    const vfl_sched_meta *meta, void *stream) {
   clear_error();
   if (!meta) {
     set_error("attention_with_kv_cache: meta is NULL");
@@ -455,12 +429,12 @@ extern "C" int vfl_attention_with_kv_cache(
     set_error("attention_with_kv_cache: bad sizes");
     return VFL_E_INVALID;
   }
-  if (meta->num_rows != num_rows || meta->num_heads != num_heads ||
-      meta->head_dim != head_dim) {
-    set_error("attention_with_kv_cache: metadata was made for rows %lld heads %d head_dim %d, "
-              "call has rows %lld heads %d head_dim %d",
-              (long long)meta->num_rows, meta->num_heads, meta->head_dim, (long long)num_rows,
-              num_heads, head_dim);
+  if (meta->num_rows != num_rows || meta->num_groups != num_groups ||
+      meta->num_heads != num_heads || meta->head_dim != head_dim) {
+    set_error("attention_with_kv_cache: metadata was made for rows %lld groups %lld heads %d "
+              "head_dim %d, call has rows %lld groups %lld heads %d head_dim %d",
+              (long long)meta->num_rows, (long long)meta->num_groups, meta->num_heads,
+              meta->head_dim, (long long)num_rows, (long long)num_groups, num_heads, head_dim);
     return VFL_E_INVALID;
   }
   if (group_start == nullptr && num_groups != num_rows) {
@@ -469,13 +443,15 @@ extern "C" int vfl_attention_with_kv_cache(
               (long long)num_groups, (long long)num_rows);
     return VFL_E_INVALID;
   }
-  if (num_groups < 0 || num_groups > num_rows || num_groups > 65535) {
-    set_error("attention_with_kv_cache: num_groups %lld out of range", (long long)num_groups);
+  if (num_groups < 0 || num_groups > num_rows || num_groups * num_heads > 2147483647LL ||
+      num_heads > 65535) {
+    set_error("attention_with_kv_cache: num_groups %lld / num_heads %d out of range",
+              (long long)num_groups, num_heads);
     return VFL_E_INVALID;
   }
-  if (meta->partition_blocks <= 0 || meta->max_partitions < 1 ||
-      (int64_t)meta->max_partitions * meta->partition_blocks < meta->max_blocks_per_seq ||
-      meta->max_group_size < 1 || meta->max_group_size > MAX_GROUP) {
+  const int nw = meta->waves_per_workgroup;
+  if (meta->max_group_size < 1 || meta->max_group_size > MAX_GROUP ||
+      (nw != 1 && nw != 2 && nw != 4 && nw != 8) || meta->max_blocks_per_seq < 0) {
     set_error("attention_with_kv_cache: inconsistent metadata");
     return VFL_E_INVALID;
   }
@@ -484,7 +460,7 @@ extern "C" int vfl_attention_with_kv_cache(
               (long long)block_table_stride, meta->max_blocks_per_seq);
     return VFL_E_INVALID;
   }
-  if (num_rows == 0) return VFL_OK;
+  if (num_rows == 0 || num_groups == 0) return VFL_OK;
   if (!query || !k_cache || !v_cache || !out || !seq_lens || !block_table) {
     set_error("attention_with_kv_cache: null pointer argument");
     return VFL_E_INVALID;
@@ -493,14 +469,6 @@ extern "C" int vfl_attention_with_kv_cache(
     set_error("attention_with_kv_cache: caches and out must be 16-byte aligned");
     return VFL_E_INVALID;
   }
-  const size_t need = workspace_for(num_rows, num_heads, head_dim, meta->max_partitions);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need ||
-                   ((uintptr_t)workspace % 256) != 0)) {
-    set_error("attention_with_kv_cache: workspace of %zu bytes (256-byte aligned) required, "
-              "got %zu",
-              need, workspace ? workspace_bytes : (size_t)0);
-    return VFL_E_WORKSPACE;
-  }
   AttnArgs a;
   a.q = query;
   a.q_st = query_stride_token;
@@ -508,30 +476,22 @@ extern "C" int vfl_attention_with_kv_cache(
   a.kc = k_cache;
   a.vc = v_cache;
   a.out = out;
-  a.ws_acc = (float *)workspace;
-  a.ws_ml = nullptr;
-  if (need > 0) {
-    size_t acc_bytes = (size_t)num_rows * num_heads * meta->max_partitions * head_dim * 4;
-    acc_bytes = (acc_bytes + 255) & ~(size_t)255;
-    a.ws_ml = (float2 *)((uint8_t *)workspace + acc_bytes);
-  }
   a.seq_lens = seq_lens;
   a.bt = block_table;
   a.bt_stride = block_table_stride;
   a.max_blocks = meta->max_blocks_per_seq;
   a.group_start = group_start;
+  a.group_order = group_order;
   a.num_rows = num_rows;
   a.num_groups = num_groups;
   a.H = num_heads;
   a.num_blocks = num_blocks;
-  a.part_blocks = meta->partition_blocks;
-  a.max_parts = meta->max_partitions;
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
   a.stream = (hipStream_t)stream;
   const int gmax = meta->max_group_size;
   switch (dtype) {
-    case VFL_FLOAT32: return dispatch_dim<VFL_FLOAT32>(a, head_dim, gmax);
-    case VFL_BFLOAT16: return dispatch_dim<VFL_BFLOAT16>(a, head_dim, gmax);
-    default: return dispatch_dim<VFL_FLOAT16>(a, head_dim, gmax);
+    case VFL_FLOAT32: return dispatch_dim<VFL_FLOAT32>(a, head_dim, gmax, nw);
+    case VFL_BFLOAT16: return dispatch_dim<VFL_BFLOAT16>(a, head_dim, gmax, nw);
+    default: return dispatch_dim<VFL_FLOAT16>(a, head_dim, gmax, nw);
   }
 }

@@ -118,15 +118,14 @@ def reshape_and_cache(
 
 @dataclass(eq=False)
 class SchedulerMetadata:
-    """Work plan for ``attention_with_kv_cache``: the GPU stand-in for the opaque
+    """Launch plan for ``attention_with_kv_cache``: the GPU stand-in for the opaque
     tensor ``vllm_cpu_attn.get_scheduler_metadata`` returns.
 
     ``group_start`` (device int32 [num_groups + 1]) lists row groups that share one
     block-table row -- the beams of a request in cross-attention -- so their K/V is
-    read once.  The grid itself is sized at call time from the block table's width,
-    which the host always knows, so no device value is ever read back.  The scratch
-    buffer is reused by every call made with this object; calls on one stream are
-    ordered, so that is safe for the decoder's layer loop.
+    read once.  ``group_order`` (device int32 [num_groups]) is the dispatch order,
+    longest context first.  The launch shape is fixed at call time from the block
+    table's width, which the host always knows, so no device value is read back.
     """
 
     num_heads: int
@@ -134,11 +133,11 @@ class SchedulerMetadata:
     block_size: int
     dtype: torch.dtype
     group_start: torch.Tensor | None = None
+    group_order: torch.Tensor | None = None
     num_groups: int | None = None
     max_group_size: int = 1
-    partition_blocks: int = 0
+    waves_per_workgroup: int = 0
     _plans: dict = field(default_factory=dict, repr=False)
-    _workspace: torch.Tensor | None = field(default=None, repr=False)
 
     def plan(self, num_rows: int, max_blocks: int) -> SchedMeta:
         key = (num_rows, max_blocks)
@@ -150,20 +149,17 @@ class SchedulerMetadata:
                 lib.vfl_get_scheduler_metadata(
                     num_rows, groups, self.num_heads, self.head_dim, self.block_size,
                     max_blocks, self.max_group_size, _dtype_code(self.dtype),
-                    self.partition_blocks, ctypes.byref(meta),
+                    self.waves_per_workgroup, ctypes.byref(meta),
                 )
             )
             self._plans[key] = meta
         return meta
 
-    def workspace(self, nbytes: int, device: torch.device) -> torch.Tensor | None:
-        if nbytes == 0:
-            return None
-        ws = self._workspace
-        if ws is None or ws.numel() < nbytes or ws.device != device:
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
-            self._workspace = ws
-        return ws
+
+def longest_first(lengths) -> list[int]:
+    """Group indices sorted by descending length (stable): the dispatch order that
+    starts the longest contexts first so the short ones fill the tail."""
+    return sorted(range(len(lengths)), key=lambda i: -int(lengths[i]))
 
 
 def get_scheduler_metadata(
@@ -179,15 +175,17 @@ def get_scheduler_metadata(
     isa: str | None = None,
     block_size: int,
     group_start: torch.Tensor | None = None,
+    group_order: torch.Tensor | None = None,
     max_group_size: int = 1,
-    partition_blocks: int = 0,
+    waves_per_workgroup: int = 0,
 ) -> SchedulerMetadata:
     """Counterpart of ``vllm_cpu_attn.get_scheduler_metadata`` (keyword names from
     vflorence/layers/attention.py:18-29 and vflorence/engine/model_runner.py:308-319).
 
-    ``group_start``/``max_group_size`` are this library's additions: row groups that
-    share K/V pages.  ``seq_lens``, ``query_start_loc``, ``causal`` and ``isa`` are
-    accepted for signature compatibility; the plan does not need them.
+    ``group_start``/``group_order``/``max_group_size``/``waves_per_workgroup`` are this
+    library's additions.  ``seq_lens``, ``query_start_loc``, ``causal`` and ``isa`` are
+    accepted for signature compatibility; the plan does not need them (callers that
+    know the lengths on the host pass ``group_order`` instead).
     """
     if num_kv_heads != num_heads:
         raise ValueError("grouped-query attention is not supported (num_kv_heads != num_heads)")
@@ -197,20 +195,26 @@ def get_scheduler_metadata(
         raise ValueError(f"block_size {block_size} has no gfx950 kernel")
     if not 1 <= max_group_size <= MAX_GROUP_SIZE:
         raise ValueError(f"max_group_size must be in [1, {MAX_GROUP_SIZE}]")
-    num_groups = None
+    if waves_per_workgroup not in (0, 1, 2, 4, 8):
+        raise ValueError("waves_per_workgroup must be 0 (default), 1, 2, 4 or 8")
+    num_groups = num_reqs
     if group_start is not None:
         if group_start.dtype != torch.int32 or group_start.dim() != 1:
             raise ValueError("group_start must be a 1-D int32 tensor")
         num_groups = group_start.numel() - 1
+    if group_order is not None:
+        if group_order.dtype != torch.int32 or group_order.shape != (num_groups,):
+            raise ValueError(f"group_order must be int32 [{num_groups}]")
     return SchedulerMetadata(
         num_heads=num_heads,
         head_dim=head_dim,
         block_size=block_size,
         dtype=dtype,
         group_start=group_start,
+        group_order=group_order,
         num_groups=num_groups,
         max_group_size=max_group_size,
-        partition_blocks=partition_blocks,
+        waves_per_workgroup=waves_per_workgroup,
     )
 
 
@@ -272,21 +276,21 @@ def attention_with_kv_cache(
             num_reqs=num_rows, num_heads=num_heads, num_kv_heads=num_heads, head_dim=head_dim,
             dtype=query.dtype, block_size=block_size,
         )
-    group_start = sm.group_start
-    if group_start is not None:
-        _require_gpu(query, group_start)
-    num_groups = num_rows if group_start is None else sm.num_groups
+    if sm.group_start is not None:
+        _require_gpu(query, sm.group_start)
+    if sm.group_order is not None:
+        _require_gpu(query, sm.group_order)
+    num_groups = num_rows if sm.group_start is None else sm.num_groups
     meta = sm.plan(num_rows, block_table.shape[1])
-    ws = sm.workspace(meta.workspace_bytes, dev)
     check(
         lib.vfl_attention_with_kv_cache(
             query.data_ptr(), query.stride(0), query.stride(1), k_cache.data_ptr(),
             v_cache.data_ptr(), out.data_ptr(), seq_lens.data_ptr(), block_table.data_ptr(),
-            block_table.stride(0), None if group_start is None else group_start.data_ptr(),
+            block_table.stride(0),
+            None if sm.group_start is None else sm.group_start.data_ptr(),
+            None if sm.group_order is None else sm.group_order.data_ptr(),
             num_rows, num_groups, num_heads, head_dim, block_size, num_blocks, float(scale),
-            _dtype_code(query.dtype), ctypes.byref(meta),
-            None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
-            _stream(dev),
+            _dtype_code(query.dtype), ctypes.byref(meta), _stream(dev),
         )
     )
 

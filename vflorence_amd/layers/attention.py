@@ -53,19 +53,24 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str):
     )
     starts = beam_groups(pages, enc_lens)
     max_group = max(b - a for a, b in zip(starts, starts[1:]))
-    n, width, ng = len(pages), block_table.shape[1], len(starts)
-    # One host->device copy: [seq_lens (n) | group starts (ng) | block table (n*width)].
+    n, width, ng = len(pages), block_table.shape[1], len(starts) - 1
+    order = hip_attn.longest_first([enc_lens[a] for a in starts[:-1]])
+    # One host->device copy:
+    # [seq_lens (n) | group starts (ng + 1) | group order (ng) | block table (n * width)].
     host = torch.cat(
         [
             torch.tensor(enc_lens, dtype=torch.int32),
             torch.tensor(starts, dtype=torch.int32),
+            torch.tensor(order, dtype=torch.int32),
             block_table.flatten(),
         ]
     )
     dev = host.to(device)
     seq_lens = dev[:n]
-    group_start = dev[n : n + ng] if max_group > 1 else None
-    block_table = dev[n + ng :].view(n, width)
+    grouped = max_group > 1
+    group_start = dev[n : n + ng + 1] if grouped else None
+    group_order = dev[n + ng + 1 : n + 2 * ng + 1]
+    block_table = dev[n + 2 * ng + 1 :].view(n, width)
     metadata = hip_attn.get_scheduler_metadata(
         num_reqs=n,
         num_heads=attn.num_heads,
@@ -77,6 +82,7 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str):
         isa=isa,
         block_size=block_size,
         group_start=group_start,
+        group_order=group_order,
         max_group_size=max_group,
     )
     return [

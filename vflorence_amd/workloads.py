@@ -190,3 +190,88 @@ def cross_attention_bytes(enc_lens_per_group: list[int], num_rows: int, num_head
     kv = sum(2 * E * row for E in enc_lens_per_group)
     return (kv + 2 * num_rows * row
             + sum(4 * math.ceil(E / block_size) for E in enc_lens_per_group) + 4 * num_rows)
+
+
+@dataclass
+class DecodeStepPlan:
+    """Host-side metadata of one decode step of the beam-search workload."""
+
+    block_tables: list[list[int]]  # per row, unpadded
+    context_lens: list[int]  # per row (position + 1)
+    slot_mapping: list[int]  # per row
+    copies: list[tuple[int, int]]  # copy-on-write pairs, copied before the KV write
+
+
+def beam_decode_schedule(
+    num_requests: int = 64,
+    beams: int = 4,
+    steps: int = 128,
+    block_size: int = 16,
+    num_blocks: int | None = None,
+    cow_fraction: float = 0.10,
+    seed: int = 0,
+) -> list[DecodeStepPlan]:
+    """Synthetic beam search driven through the real BlockManager.
+
+    Every step each row feeds one token (ModelRunner._prepare, model_runner.py:288-300)
+    after the scheduler's ensure_capacity pass (scheduler.py:124-134).  After the step,
+    ``round(cow_fraction * blocks_in_use)`` beams (at most beams - 1 per request) are
+    replaced by forks of a surviving sibling, as beam search re-ranks hypotheses
+    (scheduler.py:193-199): the fork shares the parent's blocks, so the next step's
+    write into the shared partial block produces one copy-on-write pair.  Beams of a
+    request stay adjacent.
+    """
+    import random
+
+    from .engine.block_manager import BlockManager
+    from .engine.sequence import Sequence
+    from .sampling_params import SamplingParams
+
+    rng = random.Random(seed)
+    n_rows = num_requests * beams
+    if num_blocks is None:
+        num_blocks = n_rows * math.ceil(steps / block_size)
+    bm = BlockManager(num_blocks, block_size)
+    params = SamplingParams(max_tokens=steps, num_beams=beams)
+    rows = [Sequence(r, [0], [0], params) for r in range(num_requests) for _ in range(beams)]
+    plans = []
+    for t in range(steps):
+        if bm.required_new_blocks(rows) > bm.num_free_blocks:
+            raise RuntimeError("KV cache is full; increase num_blocks")
+        copies = [c for seq in rows if (c := bm.ensure_capacity(seq)) is not None]
+        tables, lens, slots = [], [], []
+        for seq in rows:
+            pos = seq.num_cached_tokens
+            tables.append(list(seq.block_table))
+            lens.append(pos + 1)
+            slots.append(seq.block_table[pos // block_size] * block_size + pos % block_size)
+        plans.append(DecodeStepPlan(tables, lens, slots, copies))
+        for seq in rows:
+            seq.num_cached_tokens += 1
+            seq.token_ids.append(0)
+        if t == steps - 1:
+            break
+        in_use = num_blocks - bm.num_free_blocks
+        forks = min(round(cow_fraction * in_use), num_requests * (beams - 1))
+        per_request = [0] * num_requests
+        for _ in range(forks):
+            candidates = [r for r in range(num_requests) if per_request[r] < beams - 1]
+            if not candidates:
+                break
+            per_request[rng.choice(candidates)] += 1
+        for r, m in enumerate(per_request):
+            if m == 0:
+                continue
+            group = rows[r * beams : (r + 1) * beams]
+            order = list(range(beams))
+            rng.shuffle(order)
+            victims, parents = order[:m], order[m:]
+            for v in victims:
+                parent = group[rng.choice(parents)]
+                child = parent.fork(0, 0.0)
+                child.num_cached_tokens = parent.num_cached_tokens
+                bm.fork(parent, child)
+                bm.deallocate(group[v])
+                group[v] = child
+            rows[r * beams : (r + 1) * beams] = group
+    return plans
