@@ -299,8 +299,13 @@ def cpu_baseline(torch, wl, budget_s: float):
     def host_bits(t):
         return t.cpu().view(torch.int16).numpy().view(np.uint16)
 
-    kc, vc = host_bits(L0.self_attn.k_cache), host_bits(L0.self_attn.v_cache)
-    ck, cv = host_bits(L0.encoder_attn.k_cache), host_bits(L0.encoder_attn.v_cache)
+    from vflorence_amd import hip_attn
+
+    # the oracle reads V in logical (token, dim) order
+    kc = host_bits(L0.self_attn.k_cache)
+    vc = host_bits(hip_attn.v_cache_logical(L0.self_attn.v_cache).contiguous())
+    ck = host_bits(L0.encoder_attn.k_cache)
+    cv = host_bits(hip_attn.v_cache_logical(L0.encoder_attn.v_cache).contiguous())
     qkv = host_bits(wl["qkv"][0])
     rows = REQUESTS * BEAMS
     E = NUM_HEADS * HEAD_DIM

@@ -55,7 +55,7 @@ def test_reshape_and_cache_bit_exact(dtype, head_dim):
     vc = torch.randn(NB, H, bs, head_dim, generator=g).to(dtype)
     slots = torch.randperm(NB * bs, generator=g)[:T].to(torch.int64)
     slots[5] = -1  # padding token
-    kd, vd = kc.to(DEV), vc.to(DEV)
+    kd, vd = kc.to(DEV), hip().v_cache_from_logical(vc).to(DEV)
     fd = fused.to(DEV)
     keyd = fd[:, H * head_dim : 2 * H * head_dim].reshape(T, H, head_dim)
     vald = fd[:, 2 * H * head_dim :].reshape(T, H, head_dim)
@@ -64,7 +64,7 @@ def test_reshape_and_cache_bit_exact(dtype, head_dim):
     ko, vo = raw_bits(kc), raw_bits(vc)
     orc.reshape_and_cache(raw_bits(key), raw_bits(value), ko, vo, slots.numpy())
     assert np.array_equal(raw_bits(kd), ko)
-    assert np.array_equal(raw_bits(vd), vo)
+    assert np.array_equal(raw_bits(hip().v_cache_logical(vd)), vo)
 
 
 def test_reshape_and_cache_unaligned_source():
@@ -79,9 +79,10 @@ def test_reshape_and_cache_unaligned_source():
     slots = torch.tensor([3, 100, 17, 250, 0, 319, 16, 15, 200], dtype=torch.int64, device=DEV)
     hip().reshape_and_cache(key, value, kc, vc, slots)
     torch.cuda.synchronize()
+    vl = hip().v_cache_logical(vc)
     for t, s in enumerate(slots.tolist()):
         assert torch.equal(kc[s // bs, :, s % bs], key[t])
-        assert torch.equal(vc[s // bs, :, s % bs], value[t])
+        assert torch.equal(vl[s // bs, :, s % bs], value[t])
 
 
 def test_reshape_and_cache_large_encoder_write():
@@ -99,7 +100,8 @@ def test_reshape_and_cache_large_encoder_write():
     torch.cuda.synchronize()
     ko, vo = raw_bits(kc), raw_bits(vc)
     orc.reshape_and_cache(raw_bits(key), raw_bits(value), ko, vo, slots.numpy())
-    assert np.array_equal(raw_bits(kd), ko) and np.array_equal(raw_bits(vd), vo)
+    assert np.array_equal(raw_bits(kd), ko)
+    assert np.array_equal(raw_bits(hip().v_cache_logical(vd)), vo)
 
 
 # ---------------------------------------------------------------------------
@@ -184,7 +186,7 @@ def run_gpu(q, kc, vc, lens, table, scale, waves=0, group_start=None, gmax=1, or
         fused = torch.empty(q.shape[0], q.stride(0), dtype=q.dtype)
         fused.copy_(base)
         qd = fused.to(DEV).as_strided(q.shape, q.stride(), 0)
-    kd, vd = kc.to(DEV), vc.to(DEV)
+    kd, vd = kc.to(DEV), hip_attn.v_cache_from_logical(vc).to(DEV)
     out = torch.empty(q.shape, dtype=q.dtype, device=DEV)
     meta = hip_attn.get_scheduler_metadata(
         num_reqs=q.shape[0], num_heads=q.shape[1], num_kv_heads=q.shape[1], head_dim=q.shape[2],
@@ -353,8 +355,8 @@ def test_config_self_attention_256_ragged_sequences():
     from vflorence_amd import workloads
 
     case = workloads.self_attention_case(device=DEV, seed=0)
-    kc0, vc0 = raw_bits(case.k_cache), raw_bits(case.v_cache)
     hip_attn = hip()
+    kc0, vc0 = raw_bits(case.k_cache), raw_bits(hip_attn.v_cache_logical(case.v_cache))
     hip_attn.reshape_and_cache(case.key, case.value, case.k_cache, case.v_cache, case.slot_mapping)
     out = torch.empty(case.query.shape, dtype=case.query.dtype, device=DEV)
     hip_attn.attention_with_kv_cache(
@@ -365,7 +367,7 @@ def test_config_self_attention_256_ragged_sequences():
     orc.reshape_and_cache(raw_bits(case.key), raw_bits(case.value), kc0, vc0,
                           case.slot_mapping.cpu().numpy())
     assert np.array_equal(raw_bits(case.k_cache), kc0)
-    assert np.array_equal(raw_bits(case.v_cache), vc0)
+    assert np.array_equal(raw_bits(hip_attn.v_cache_logical(case.v_cache)), vc0)
     table = case.block_tables.cpu().numpy()
     used, remapped = np.unique(table, return_inverse=True)
     want = orc.paged_attention(

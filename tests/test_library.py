@@ -58,11 +58,13 @@ def test_scheduler_metadata_plan():
     assert (m.num_rows, m.num_groups, m.num_heads, m.head_dim) == (256, 256, 16, 64)
     assert m.max_blocks_per_seq == 64 and m.max_group_size == 1
     assert m.waves_per_workgroup in (1, 2, 4, 8)
-    # 4096 workgroups: two waves each reach the 8192-wave target
-    assert m.waves_per_workgroup == 2
-    # cross-attention of 64 requests x 4 beams: 1024 workgroups -> 8 waves
+    # measured best for 256 ragged rows (4096 workgroups) and 64 x 4 beams (1024)
+    assert m.waves_per_workgroup == 4
     rc, m = plan(256, 64, 16, 64, 64, gmax=4)
-    assert rc == 0 and m.waves_per_workgroup == 8 and m.max_group_size == 4
+    assert rc == 0 and m.waves_per_workgroup == 4 and m.max_group_size == 4
+    # few workgroups: more waves each
+    rc, m = plan(8, 8, 16, 64, 64)
+    assert rc == 0 and m.waves_per_workgroup == 8
     # never more waves than blocks in the longest context
     rc, m = plan(4, 4, 16, 64, 1)
     assert rc == 0 and m.waves_per_workgroup == 1

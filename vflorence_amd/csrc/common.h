@@ -205,4 +205,41 @@ template <int N> __device__ __forceinline__ float group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+constexpr float NEG_INF_F = -__builtin_huge_valf();
+
+// Online-softmax maxima are lazy references: scores are exponentiated against the
+// reference and it only moves (rescaling the accumulators) when a block max exceeds
+// it by more than this many log2 units, so weights stay <= 2^8 and most blocks skip
+// the rescale.  The final normalisation makes the result exact in exact arithmetic.
+constexpr float RESCALE_SLACK_LOG2 = 8.0f;
+
+// V pools of 16-bit element type hold every [block][head] slice transposed
+// ([head_dim][block_size]) so the matrix-core kernel can feed tokens along the
+// reduction dimension; fp32 pools keep the logical [block_size][head_dim] order.
+inline bool v_tile_transposed(int dtype) { return dtype != VFL_FLOAT32; }
+
+// A wave's block ids, 64 at a time in one VGPR (lane i holds the id of block
+// base + i), read back with readlane: no scalar load sits between one block's
+// K/V loads and the next.
+struct WaveBlockIds {
+  const int32_t *row;
+  int end, base, reg;
+
+  __device__ __forceinline__ void fetch(int b) {
+    base = b;
+    const int lane = __lane_id();
+    reg = (b + lane < end) ? row[b + lane] : -1;
+  }
+  __device__ __forceinline__ void init(const int32_t *r, int b0, int b1) {
+    row = r;
+    end = b1;
+    fetch(b0);
+  }
+  // b is wave-uniform and b0 <= b < b1.
+  __device__ __forceinline__ int get(int b) {
+    if (b - base >= 64) fetch(b);
+    return __builtin_amdgcn_readlane(reg, b - base);
+  }
+};
+
 }  // namespace vfl

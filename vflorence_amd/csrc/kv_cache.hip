@@ -33,7 +33,9 @@ int launch_status(const char *what) {
 // ---------------------------------------------------------------------------
 // reshape_and_cache: one thread per 16-byte chunk of a (token, head) row.
 // ---------------------------------------------------------------------------
-template <int DT, bool ALIGNED>
+// VT: the V pool stores each [block][head] slice transposed ([head_dim][block_size],
+// 16-bit pools); the token's head_dim values then land block_size elements apart.
+template <int DT, bool ALIGNED, bool VT>
 __global__ __launch_bounds__(256) void reshape_and_cache_kernel(
     const typename Elem<DT>::T *__restrict__ key, const typename Elem<DT>::T *__restrict__ value,
     int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh, typename Elem<DT>::T *__restrict__ kc,
@@ -56,14 +58,26 @@ __global__ __launch_bounds__(256) void reshape_and_cache_kernel(
   const int64_t dst = ((blk * num_heads + h) * block_size + off) * head_dim + c * VEC;
   const T *ks = key + t * k_st + h * k_sh + c * VEC;
   const T *vs = value + t * v_st + h * v_sh + c * VEC;
+  uint4 kv, vv;
   if constexpr (ALIGNED) {
-    const uint4 kv = *reinterpret_cast<const uint4 *>(ks);
-    const uint4 vv = *reinterpret_cast<const uint4 *>(vs);
+    kv = *reinterpret_cast<const uint4 *>(ks);
+    vv = *reinterpret_cast<const uint4 *>(vs);
     *reinterpret_cast<uint4 *>(kc + dst) = kv;
+  } else {
+    kv = load16_unaligned<DT>(ks);
+    vv = load16_unaligned<DT>(vs);
+    store16_unaligned<DT>(kc + dst, kv);
+  }
+  if constexpr (VT) {
+    static_assert(DT != VFL_FLOAT32, "transposed V tiles are 16-bit");
+    T *vt = vc + ((blk * num_heads + h) * head_dim + c * VEC) * block_size + off;
+    const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) vt[e * block_size] = (T)(w[e / 2] >> (16 * (e & 1)));
+  } else if constexpr (ALIGNED) {
     *reinterpret_cast<uint4 *>(vc + dst) = vv;
   } else {
-    store16_unaligned<DT>(kc + dst, load16_unaligned<DT>(ks));
-    store16_unaligned<DT>(vc + dst, load16_unaligned<DT>(vs));
+    store16_unaligned<DT>(vc + dst, vv);
   }
 }
 
@@ -77,12 +91,13 @@ static void launch_reshape(bool aligned, const void *key, const void *value, int
   const int64_t total = T * H * cpr;
   const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
+  constexpr bool VT = DT != VFL_FLOAT32;  // v_tile_transposed(DT)
   if (aligned)
-    reshape_and_cache_kernel<DT, true><<<dim3((unsigned)blocks), dim3(threads), 0, stream>>>(
+    reshape_and_cache_kernel<DT, true, VT><<<dim3((unsigned)blocks), dim3(threads), 0, stream>>>(
         (const E *)key, (const E *)value, k_st, k_sh, v_st, v_sh, (E *)kc, (E *)vc, slots, T, H,
         cpr, BS, num_blocks * BS);
   else
-    reshape_and_cache_kernel<DT, false><<<dim3((unsigned)blocks), dim3(threads), 0, stream>>>(
+    reshape_and_cache_kernel<DT, false, VT><<<dim3((unsigned)blocks), dim3(threads), 0, stream>>>(
         (const E *)key, (const E *)value, k_st, k_sh, v_st, v_sh, (E *)kc, (E *)vc, slots, T, H,
         cpr, BS, num_blocks * BS);
 }

@@ -17,13 +17,13 @@
 //   token rows keeps its own online-softmax state, merged across rows once at the
 //   end (no cross-row traffic in the loop).
 #include "common.h"
+#include "decode_mfma.h"
 
 namespace vfl {
 
-constexpr float NEG_INF = -__builtin_huge_valf();
-
 // Fold NT loaded token rows (K chunks kr, V chunks vr) into the running state of
-// every live row of the group.  MASKED selects per-lane validity `valid[j]`.
+// every live row of the group.  MASKED applies per-lane validity `valid[j]` (token
+// past the context, or a block id outside the pool).
 template <int DT, int D, int G, int NT, bool MASKED>
 __device__ __forceinline__ void consume(const uint4 (&qv)[G], const uint4 *kr, const uint4 *vr,
                                         const bool *valid, int nrows, float scale_log2,
@@ -46,18 +46,24 @@ __device__ __forceinline__ void consume(const uint4 (&qv)[G], const uint4 *kr, c
   for (int gi = 0; gi < G; ++gi) {
     if (gi >= nrows) break;
     float s[NT];
-    float mx = m[gi];
+    float mb = NEG_INF_F;
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       s[j] = group_sum<LPT>(dot16<DT>(qv[gi], kr[j])) * scale_log2;
-      if constexpr (MASKED) s[j] = valid[j] ? s[j] : NEG_INF;
-      mx = fmaxf(mx, s[j]);
+      if constexpr (MASKED) s[j] = valid[j] ? s[j] : NEG_INF_F;
+      mb = fmaxf(mb, s[j]);
     }
-    const float ms = (mx == NEG_INF) ? 0.f : mx;
-    const float corr = fast_exp2(m[gi] - ms);
-    float lsum = l[gi] * corr;
+    // Wave-uniform branch: rescale only if some lane's block max ran away.
+    if (__builtin_amdgcn_ballot_w64(mb > m[gi] + RESCALE_SLACK_LOG2) != 0) {
+      const float mn = fmaxf(m[gi], mb);
+      const float corr = (mn == NEG_INF_F) ? 1.f : fast_exp2(m[gi] - mn);
+      l[gi] *= corr;
 #pragma unroll
-    for (int d = 0; d < VEC; ++d) acc[gi][d] *= corr;
+      for (int d = 0; d < VEC; ++d) acc[gi][d] *= corr;
+      m[gi] = mn;
+    }
+    const float ms = (m[gi] == NEG_INF_F) ? 0.f : m[gi];
+    float lsum = l[gi];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const float p = fast_exp2(s[j] - ms);
@@ -66,7 +72,57 @@ __device__ __forceinline__ void consume(const uint4 (&qv)[G], const uint4 *kr, c
       for (int d = 0; d < VEC; ++d) acc[gi][d] = fmaf(p, vf[j][d], acc[gi][d]);
     }
     l[gi] = lsum;
-    m[gi] = mx;
+  }
+}
+
+// Issue the loads of U consecutive blocks (one stage) into registers.  Block ids
+// outside the pool load nothing and are marked invalid.
+template <int DT, int D, int BS, int U>
+__device__ __forceinline__ void load_stage(const typename Elem<DT>::T *__restrict__ kc,
+                                           const typename Elem<DT>::T *__restrict__ vc,
+                                           WaveBlockIds &ids, int b, int64_t block_elems,
+                                           int lane_off, int64_t num_blocks, uint4 *kr,
+                                           uint4 *vr, bool *ok) {
+  constexpr int VEC = Elem<DT>::VEC;
+  constexpr int TPL = 64 / (D / VEC);
+  constexpr int NLD = BS / TPL;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int id = ids.get(b + u);
+    ok[u] = id >= 0 && id < num_blocks;
+    const int64_t base = (ok[u] ? (int64_t)id : 0) * block_elems + lane_off;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      kr[u * NLD + i] = make_uint4(0, 0, 0, 0);
+      vr[u * NLD + i] = make_uint4(0, 0, 0, 0);
+      if (ok[u]) {
+        kr[u * NLD + i] = *reinterpret_cast<const uint4 *>(kc + base + i * TPL * D);
+        vr[u * NLD + i] = *reinterpret_cast<const uint4 *>(vc + base + i * TPL * D);
+      }
+    }
+  }
+}
+
+// Consume one stage of U whole blocks; a stage holding an invalid block id takes the
+// masked path for its tokens.
+template <int DT, int D, int BS, int G, int U>
+__device__ __forceinline__ void consume_stage(const uint4 (&qv)[G], const uint4 *kr,
+                                              const uint4 *vr, const bool *ok, int nrows,
+                                              float scale_log2, float (&m)[G], float (&l)[G],
+                                              float (&acc)[G][Elem<DT>::VEC]) {
+  constexpr int VEC = Elem<DT>::VEC;
+  constexpr int TPL = 64 / (D / VEC);
+  constexpr int NLD = BS / TPL;
+  bool all_ok = true;
+#pragma unroll
+  for (int u = 0; u < U; ++u) all_ok = all_ok && ok[u];
+  if (all_ok) {
+    consume<DT, D, G, U * NLD, false>(qv, kr, vr, nullptr, nrows, scale_log2, m, l, acc);
+  } else {
+    bool valid[U * NLD];
+#pragma unroll
+    for (int j = 0; j < U * NLD; ++j) valid[j] = ok[j / NLD];
+    consume<DT, D, G, U * NLD, true>(qv, kr, vr, valid, nrows, scale_log2, m, l, acc);
   }
 }
 
@@ -79,7 +135,7 @@ template <int DT> __device__ __forceinline__ typename Elem<DT>::T to_elem(float 
     return (typename Elem<DT>::T)f32_to_f16(v);
 }
 
-template <int DT, int D, int BS, int G, int NW, int U>
+template <int DT, int D, int BS, int G, int NW, int U, bool PIPE>
 __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
     const typename Elem<DT>::T *__restrict__ q, int64_t q_st, int64_t q_sh,
     const typename Elem<DT>::T *__restrict__ kc, const typename Elem<DT>::T *__restrict__ vc,
@@ -143,62 +199,60 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
   float m[G], l[G], acc[G][VEC];
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
-    m[gi] = NEG_INF;
+    m[gi] = NEG_INF_F;
     l[gi] = 0.f;
 #pragma unroll
     for (int d = 0; d < VEC; ++d) acc[gi][d] = 0.f;
   }
 
-  const int32_t *btrow = bt + (int64_t)row0 * bt_stride;
+  WaveBlockIds ids;
+  ids.init(bt + (int64_t)row0 * bt_stride, b0, b1);
   const int64_t block_elems = (int64_t)H * BS * D;
   const int lane_off = h * BS * D + tok * D + c * VEC;
 
+  // Whole blocks of this wave's run are consumed U at a time.  With PIPE the loads
+  // of stage s+1 are issued before stage s is consumed (two register stages live),
+  // so each wave keeps K/V in flight while it computes; without it, latency is hidden
+  // by the other waves the smaller register footprint lets the CU hold.
+  const int bfull = max(b0, min(b1, Lc / BS));
+  const int stages = (bfull - b0) / U;
   int b = b0;
-  // Fast path: U whole blocks per step, every token valid.
-  const int bfull = min(b1, Lc / BS);
-  for (; b + U <= bfull; b += U) {
-    int ids[U];
-    bool ok = true;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      ids[u] = btrow[b + u];
-      ok = ok && ids[u] >= 0 && ids[u] < num_blocks;
-    }
-    if (!ok) break;  // the masked loop below handles blocks with bad ids
-    uint4 kr[U * NLD], vr[U * NLD];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const T *kb = kc + (int64_t)ids[u] * block_elems + lane_off;
-      const T *vb = vc + (int64_t)ids[u] * block_elems + lane_off;
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        kr[u * NLD + i] = *reinterpret_cast<const uint4 *>(kb + i * TPL * D);
-        vr[u * NLD + i] = *reinterpret_cast<const uint4 *>(vb + i * TPL * D);
+  if constexpr (PIPE) {
+    if (stages > 0) {
+      uint4 ka[U * NLD], va[U * NLD], kb[U * NLD], vb[U * NLD];
+      bool oka[U], okb[U];
+      load_stage<DT, D, BS, U>(kc, vc, ids, b, block_elems, lane_off, num_blocks, ka, va,
+                               oka);
+      for (int st = 0; st < stages; st += 2) {
+        if (st + 1 < stages)
+          load_stage<DT, D, BS, U>(kc, vc, ids, b + U, block_elems, lane_off, num_blocks, kb,
+                                   vb, okb);
+        consume_stage<DT, D, BS, G, U>(qv, ka, va, oka, nrows, scale_log2, m, l, acc);
+        b += U;
+        if (st + 1 >= stages) break;
+        if (st + 2 < stages)
+          load_stage<DT, D, BS, U>(kc, vc, ids, b + U, block_elems, lane_off, num_blocks, ka,
+                                   va, oka);
+        consume_stage<DT, D, BS, G, U>(qv, kb, vb, okb, nrows, scale_log2, m, l, acc);
+        b += U;
       }
     }
-    consume<DT, D, G, U * NLD, false>(qv, kr, vr, nullptr, nrows, scale_log2, m, l, acc);
+  } else {
+    for (int st = 0; st < stages; ++st, b += U) {
+      uint4 kr[U * NLD], vr[U * NLD];
+      bool ok[U];
+      load_stage<DT, D, BS, U>(kc, vc, ids, b, block_elems, lane_off, num_blocks, kr, vr, ok);
+      consume_stage<DT, D, BS, G, U>(qv, kr, vr, ok, nrows, scale_log2, m, l, acc);
+    }
   }
   // Remaining blocks one at a time, with token and block-id masking.
   for (; b < b1; ++b) {
-    const int id = btrow[b];
-    const bool ok = id >= 0 && id < num_blocks;
     uint4 kr[NLD], vr[NLD];
+    bool ok[1];
+    load_stage<DT, D, BS, 1>(kc, vc, ids, b, block_elems, lane_off, num_blocks, kr, vr, ok);
     bool valid[NLD];
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      valid[i] = ok && (b * BS + i * TPL + tok) < Lc;
-      kr[i] = make_uint4(0, 0, 0, 0);
-      vr[i] = make_uint4(0, 0, 0, 0);
-    }
-    if (ok) {
-      const T *kb = kc + (int64_t)id * block_elems + lane_off;
-      const T *vb = vc + (int64_t)id * block_elems + lane_off;
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        kr[i] = *reinterpret_cast<const uint4 *>(kb + i * TPL * D);
-        vr[i] = *reinterpret_cast<const uint4 *>(vb + i * TPL * D);
-      }
-    }
+    for (int i = 0; i < NLD; ++i) valid[i] = ok[0] && (b * BS + i * TPL + tok) < Lc;
     consume<DT, D, G, NLD, true>(qv, kr, vr, valid, nrows, scale_log2, m, l, acc);
   }
 
@@ -211,7 +265,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
       const float mo = __shfl_xor(m[gi], off, 64);
       const float lo = __shfl_xor(l[gi], off, 64);
       const float mx = fmaxf(m[gi], mo);
-      const float ms = (mx == NEG_INF) ? 0.f : mx;
+      const float ms = (mx == NEG_INF_F) ? 0.f : mx;
       const float wa = fast_exp2(m[gi] - ms);
       const float wb = fast_exp2(mo - ms);
       l[gi] = l[gi] * wa + lo * wb;
@@ -253,10 +307,10 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
     __syncthreads();
     for (int i = threadIdx.x; i < nrows * D; i += NW * 64) {
       const int gi = i / D, d = i % D;
-      float M = NEG_INF;
+      float M = NEG_INF_F;
 #pragma unroll
       for (int w = 0; w < NW; ++w) M = fmaxf(M, s_ml[w][gi][0]);
-      const float Ms = (M == NEG_INF) ? 0.f : M;
+      const float Ms = (M == NEG_INF_F) ? 0.f : M;
       float S = 0.f, o = 0.f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
@@ -269,12 +323,15 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
   }
 }
 
-// Whole blocks per fast-path step: about four 16-byte K loads (and four V loads)
-// in flight per lane, so fp32 and head_dim 128 (more loads per block) unroll less.
-template <int DT, int D> constexpr int unroll_blocks() {
+// Blocks per stage: about four 16-byte K loads (plus four V loads) per lane -- fewer
+// when fp32 or head_dim 128 need more loads per block.
+template <int DT, int D, int G> constexpr int stage_blocks() {
   constexpr int nld = 16 / (64 / (D / Elem<DT>::VEC));
   return nld >= 4 ? 1 : 4 / nld;
 }
+// Register pipelining (two live stages) measured slower than the occupancy the
+// smaller footprint buys, for every beam count; kept as a kernel option.
+template <int G> constexpr bool stage_pipeline() { return false; }
 
 struct AttnArgs {
   const void *q;
@@ -292,43 +349,76 @@ struct AttnArgs {
   hipStream_t stream;
 };
 
-template <int DT, int D, int G, int NW>
-static int launch_attention(const AttnArgs &a) {
+// fp32 caches: VALU kernel over the logical V layout, G query rows per group.
+template <int D, int G, int NW>
+static int launch_valu(const AttnArgs &a) {
+  constexpr int DT = VFL_FLOAT32;
   using T = typename Elem<DT>::T;
   constexpr int BS = 16;
   const dim3 grid((unsigned)(a.num_groups * a.H));
-  paged_decode_kernel<DT, D, BS, G, NW, unroll_blocks<DT, D>()><<<grid, dim3(NW * 64), 0,
-                                                                    a.stream>>>(
+  paged_decode_kernel<DT, D, BS, G, NW, stage_blocks<DT, D, G>(), stage_pipeline<G>()>
+      <<<grid, dim3(NW * 64), 0, a.stream>>>(
       (const T *)a.q, a.q_st, a.q_sh, (const T *)a.kc, (const T *)a.vc, (T *)a.out, a.seq_lens,
       a.bt, a.bt_stride, a.max_blocks, a.group_start, a.group_order, a.num_rows, a.num_groups,
       a.H, a.num_blocks, a.scale_log2);
   return launch_status("attention_with_kv_cache");
 }
 
-template <int DT, int D, int G>
-static int dispatch_waves(const AttnArgs &a, int nw) {
+template <int D, int G>
+static int valu_waves(const AttnArgs &a, int nw) {
   switch (nw) {
-    case 1: return launch_attention<DT, D, G, 1>(a);
-    case 2: return launch_attention<DT, D, G, 2>(a);
-    case 4: return launch_attention<DT, D, G, 4>(a);
-    default: return launch_attention<DT, D, G, 8>(a);
+    case 1: return launch_valu<D, G, 1>(a);
+    case 2: return launch_valu<D, G, 2>(a);
+    case 4: return launch_valu<D, G, 4>(a);
+    default: return launch_valu<D, G, 8>(a);
   }
 }
 
-template <int DT, int D>
-static int dispatch_group(const AttnArgs &a, int gmax, int nw) {
-  if (gmax <= 1) return dispatch_waves<DT, D, 1>(a, nw);
-  if (gmax <= 2) return dispatch_waves<DT, D, 2>(a, nw);
-  if (gmax <= 4) return dispatch_waves<DT, D, 4>(a, nw);
-  return dispatch_waves<DT, D, 8>(a, nw);
+template <int D>
+static int valu_group(const AttnArgs &a, int gmax, int nw) {
+  if (gmax <= 1) return valu_waves<D, 1>(a, nw);
+  if (gmax <= 2) return valu_waves<D, 2>(a, nw);
+  if (gmax <= 4) return valu_waves<D, 4>(a, nw);
+  return valu_waves<D, 8>(a, nw);
 }
 
-template <int DT>
-static int dispatch_dim(const AttnArgs &a, int head_dim, int gmax, int nw) {
-  switch (head_dim) {
-    case 64: return dispatch_group<DT, 64>(a, gmax, nw);
-    case 128: return dispatch_group<DT, 128>(a, gmax, nw);
-    default: break;
+// bf16 / fp16 caches: matrix-core kernel over the tile-transposed V layout; the tile
+// columns hold up to 16 query rows per group, so one instantiation serves any G.
+constexpr int MFMA_STAGE_BLOCKS = 2;
+
+template <int DT, int D, int NW>
+static int launch_mfma(const AttnArgs &a) {
+  const dim3 grid((unsigned)(a.num_groups * a.H));
+  paged_decode_mfma_kernel<DT, D, NW, MFMA_STAGE_BLOCKS><<<grid, dim3(NW * 64), 0, a.stream>>>(
+      (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
+      (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
+      a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2);
+  return launch_status("attention_with_kv_cache");
+}
+
+template <int DT, int D>
+static int mfma_waves(const AttnArgs &a, int nw) {
+  switch (nw) {
+    case 1: return launch_mfma<DT, D, 1>(a);
+    case 2: return launch_mfma<DT, D, 2>(a);
+    case 4: return launch_mfma<DT, D, 4>(a);
+    default:
+      // The merge buffer of 8 waves x head_dim 128 exceeds 64 KiB of LDS.
+      if constexpr (D <= 64) return launch_mfma<DT, D, 8>(a);
+      else return launch_mfma<DT, D, 4>(a);
+  }
+}
+
+static int dispatch(const AttnArgs &a, int dtype, int head_dim, int gmax, int nw) {
+  if (dtype == VFL_FLOAT32) {
+    if (head_dim == 64) return valu_group<64>(a, gmax, nw);
+    if (head_dim == 128) return valu_group<128>(a, gmax, nw);
+  } else if (dtype == VFL_BFLOAT16) {
+    if (head_dim == 64) return mfma_waves<VFL_BFLOAT16, 64>(a, nw);
+    if (head_dim == 128) return mfma_waves<VFL_BFLOAT16, 128>(a, nw);
+  } else {
+    if (head_dim == 64) return mfma_waves<VFL_FLOAT16, 64>(a, nw);
+    if (head_dim == 128) return mfma_waves<VFL_FLOAT16, 128>(a, nw);
   }
   set_error("attention_with_kv_cache: head_dim %d has no kernel (built: 64, 128)", head_dim);
   return VFL_E_UNSUPPORTED;
@@ -341,14 +431,14 @@ static bool kernel_exists(int dtype, int block_size, int head_dim) {
 
 constexpr int MAX_GROUP = 8;
 constexpr int MAX_WAVES = 8;
-// Waves the default plan aims to have in flight: 256 CUs x 32 wave slots.
-constexpr int64_t TARGET_WAVES = 256 * 32;
 
+// Waves per (group, head) workgroup.  Measured on MI355X (bf16, head_dim 64): four
+// waves is best both for 256 ragged self-attention rows (4096 workgroups) and for
+// 64 x 4-beam cross-attention (1024 workgroups); eight only pays when there are
+// few workgroups to spread over 256 CUs.  Never more waves than blocks.
 static int default_waves(int64_t num_groups, int num_heads, int64_t max_blocks) {
   const int64_t wgs = num_groups * num_heads;
-  int nw = 1;
-  while (nw < MAX_WAVES && wgs * nw < TARGET_WAVES) nw *= 2;
-  // No more waves than blocks in the longest context.
+  int nw = wgs >= 512 ? 4 : 8;
   while (nw > 1 && nw / 2 >= max_blocks) nw /= 2;
   return nw;
 }
@@ -488,10 +578,5 @@ extern "C" int vfl_attention_with_kv_cache(
   a.num_blocks = num_blocks;
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
   a.stream = (hipStream_t)stream;
-  const int gmax = meta->max_group_size;
-  switch (dtype) {
-    case VFL_FLOAT32: return dispatch_dim<VFL_FLOAT32>(a, head_dim, gmax, nw);
-    case VFL_BFLOAT16: return dispatch_dim<VFL_BFLOAT16>(a, head_dim, gmax, nw);
-    default: return dispatch_dim<VFL_FLOAT16>(a, head_dim, gmax, nw);
-  }
+  return dispatch(a, dtype, head_dim, meta->max_group_size, nw);
 }

@@ -32,6 +32,35 @@ SUPPORTED_BLOCK_SIZES = frozenset({16})
 MAX_GROUP_SIZE = 8
 
 
+def v_tile_transposed(dtype: torch.dtype) -> bool:
+    """Whether V pools of ``dtype`` store each [block][head] slice transposed.
+
+    16-bit pools keep each 2 KiB block-head slice of V as [head_dim][block_size] so
+    the matrix-core decode kernel reads tokens contiguously for a fixed dim; fp32 pools
+    keep the logical [block_size][head_dim] order.  The tensor shape is the reference's
+    [num_blocks, H, block_size, head_dim] either way, and only this library's ops
+    address the inside of a block (the reference leaves that layout to the attention
+    backend: AGENTS.md section 5.3, "internal layout determined by the selected ISA").
+    """
+    return dtype != torch.float32
+
+
+def v_cache_logical(v_cache: torch.Tensor) -> torch.Tensor:
+    """[NB, H, bs, D] view of a V pool in logical (token, dim) order."""
+    if not v_tile_transposed(v_cache.dtype):
+        return v_cache
+    nb, h, bs, d = v_cache.shape
+    return v_cache.view(nb, h, d, bs).transpose(2, 3)
+
+
+def v_cache_from_logical(v_logical: torch.Tensor) -> torch.Tensor:
+    """A contiguous V pool (device layout) holding the given logical [NB, H, bs, D] values."""
+    if not v_tile_transposed(v_logical.dtype):
+        return v_logical.contiguous()
+    nb, h, bs, d = v_logical.shape
+    return v_logical.transpose(2, 3).contiguous().view(nb, h, bs, d)
+
+
 def _dtype_code(dtype: torch.dtype) -> int:
     try:
         return _DTYPE_CODES[dtype]
