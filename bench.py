@@ -137,9 +137,10 @@ def capture_steps(torch, wl):
         slots = torch.tensor(plan.slot_mapping, dtype=torch.int64, device=dev)
         order = torch.tensor(hip_attn.longest_first(plan.context_lens), dtype=torch.int32,
                              device=dev)
+        # slots come from BlockManager tables (private last blocks): fused KV write
         meta = hip_attn.get_scheduler_metadata(
             num_reqs=rows, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS, head_dim=HEAD_DIM,
-            dtype=torch.bfloat16, block_size=BLOCK, group_order=order)
+            dtype=torch.bfloat16, block_size=BLOCK, group_order=order, fuse_kv_write=True)
         src = dst = None
         staged = False
         if plan.copies:
@@ -221,6 +222,33 @@ def raw_attention_launcher(torch, query, k_cache, v_cache, out, seq_lens, table,
     return launch
 
 
+def raw_fused_launcher(torch, case, out, sm):
+    """Prebuilt ctypes call of vfl_self_attention_with_kv_write (validated once)."""
+    from vflorence_amd import hip_attn
+    from vflorence_amd._lib import check, lib
+
+    c = case
+    hip_attn.self_attention_with_kv_write(c.query, c.key, c.value, c.k_cache, c.v_cache, out,
+                                          c.context_lens, c.slot_mapping, scale=c.scale,
+                                          block_table=c.block_tables, scheduler_metadata=sm)
+    rows = c.query.shape[0]
+    meta = sm.plan(rows, c.block_tables.shape[1])
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    args = (c.query.data_ptr(), c.query.stride(0), c.query.stride(1), c.key.data_ptr(),
+            c.key.stride(0), c.key.stride(1), c.value.data_ptr(), c.value.stride(0),
+            c.value.stride(1), c.slot_mapping.data_ptr(), c.k_cache.data_ptr(),
+            c.v_cache.data_ptr(), out.data_ptr(), c.context_lens.data_ptr(),
+            c.block_tables.data_ptr(), c.block_tables.stride(0),
+            None if sm.group_order is None else sm.group_order.data_ptr(), rows, NUM_HEADS,
+            HEAD_DIM, BLOCK, c.k_cache.shape[0], c.scale, 1, ctypes.byref(meta), stream)
+    fn = lib.vfl_self_attention_with_kv_write
+
+    def launch():
+        check(fn(*args))
+
+    return launch
+
+
 def cross_kernel_timing(torch, wl, reps: int):
     """Dominant kernel of the workload: beam-grouped cross-attention, over all 12 layers'
     pools in rotation (12 x 168 MB, so the 256 MB last-level cache cannot serve it)."""
@@ -248,21 +276,26 @@ def cross_kernel_timing(torch, wl, reps: int):
 def self_op_timing(torch, reps: int, seed: int):
     """256 ragged sequences (ctx U[1,1024]) over a random permutation of a 20k-block pool;
     three independent pools in rotation.  Returns (attention kernel avg s, bytes of the
-    attention kernel, op avg s incl. the KV slot write, op bytes)."""
+    attention kernel, op avg s incl. the KV slot write -- the fused self-attention
+    launch --, op bytes)."""
     from vflorence_amd import hip_attn, workloads
 
     cases = [workloads.self_attention_case(seed=seed + i) for i in range(3)]
-    launches, outs = [], []
+    launches, fused, outs = [], [], []
     kernel_bytes = op_bytes = 0
     for c in cases:
         out = torch.empty(c.query.shape, dtype=c.query.dtype, device=c.query.device)
         order = torch.tensor(hip_attn.longest_first(c.context_lens.tolist()), dtype=torch.int32,
                              device=c.query.device)
-        sm = hip_attn.get_scheduler_metadata(
+        plain = hip_attn.get_scheduler_metadata(
             num_reqs=c.num_seqs, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS, head_dim=HEAD_DIM,
             dtype=c.query.dtype, block_size=BLOCK, group_order=order)
+        fuse = hip_attn.get_scheduler_metadata(
+            num_reqs=c.num_seqs, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS, head_dim=HEAD_DIM,
+            dtype=c.query.dtype, block_size=BLOCK, group_order=order, fuse_kv_write=True)
         launches.append(raw_attention_launcher(torch, c.query, c.k_cache, c.v_cache, out,
-                                               c.context_lens, c.block_tables, sm))
+                                               c.context_lens, c.block_tables, plain))
+        fused.append(raw_fused_launcher(torch, c, out, fuse))
         outs.append(out)
         lens = c.context_lens.tolist()
         row = NUM_HEADS * HEAD_DIM * 2
@@ -275,8 +308,7 @@ def self_op_timing(torch, reps: int, seed: int):
             f()
 
     def ops():
-        for c, f in zip(cases, launches):
-            hip_attn.reshape_and_cache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping)
+        for f in fused:
             f()
 
     k_avg = time_kernel(torch, kernels, reps) / len(cases)

@@ -14,10 +14,17 @@
  * any launch; out-of-range block ids or slots found on the device are skipped
  * rather than dereferenced (see each entry point).
  *
- * Cache layout (the reference's logical layout, vflorence/engine/model_runner.py:66-77):
- *   cache[num_blocks][num_heads][block_size][head_dim], contiguous, one tensor per
- *   layer and per K / V.  Token t of block b, head h lives at
- *   ((b * num_heads + h) * block_size + t) * head_dim.
+ * Cache layout: tensors of the reference's shape [num_blocks][num_heads][block_size]
+ *   [head_dim] (vflorence/engine/model_runner.py:66-77), contiguous, one per layer and
+ *   per K / V.  K: token t of block b, head h at ((b * H + h) * block_size + t) *
+ *   head_dim.  V: the same for fp32 pools; 16-bit pools store each [block][head] slice
+ *   with tokens interleaved in groups of four, dim d of token t at
+ *   (b * H + h) * head_dim * block_size + ((t / 4) * head_dim + d) * 4 + t % 4, so the
+ *   matrix-core kernel reads 4 tokens of a dim as one 8-byte operand and a token's
+ *   write spans one 512-byte run (head_dim 64).  The reference leaves the inside
+ *   of a block to its attention backend ("internal layout determined by the selected
+ *   ISA", AGENTS.md section 5.3); only these entry points address it, and whole-block
+ *   operations (copy_blocks, zero-filling a pool) are layout-independent.
  */
 #ifndef VFLORENCE_AMD_H
 #define VFLORENCE_AMD_H
@@ -145,6 +152,36 @@ int vfl_attention_with_kv_cache(const void *query, int64_t query_stride_token,
                                 int head_dim, int block_size, int64_t num_blocks,
                                 float scale, int dtype, const vfl_sched_meta *meta,
                                 void *stream);
+
+/*
+ * The body of the reference's vflorence::self_attention op in one launch
+ * (vflorence/layers/attention.py:53-73: reshape_and_cache of key/value at
+ * slot_mapping, then attention_with_kv_cache over the updated cache), for one query
+ * row per sequence (no row groups).
+ *
+ * Precondition (what the block manager's copy-on-write guarantees,
+ * vflorence/engine/block_manager.py:44-59): for every row r, slot_mapping[r] is
+ * either negative, or the cache slot of position seq_lens[r]-1 of row r's block
+ * table, or a slot that no row of this call attends to; and the block holding a
+ * row's new token is read by no other row.  Then the result -- cache contents and
+ * out -- equals reshape_and_cache followed by attention_with_kv_cache.  Callers that
+ * cannot vouch for it use those two entry points.  fp32 caches run the two steps.
+ *
+ * key / value: [num_rows][num_heads][head_dim] with token / head strides in
+ * elements (the strided views of a fused qkv projection).  Other arguments as for
+ * vfl_attention_with_kv_cache with group_start NULL and num_groups == num_rows.
+ */
+int vfl_self_attention_with_kv_write(const void *query, int64_t query_stride_token,
+                                     int64_t query_stride_head, const void *key,
+                                     int64_t key_stride_token, int64_t key_stride_head,
+                                     const void *value, int64_t value_stride_token,
+                                     int64_t value_stride_head, const int64_t *slot_mapping,
+                                     void *k_cache, void *v_cache, void *out,
+                                     const int32_t *seq_lens, const int32_t *block_table,
+                                     int64_t block_table_stride, const int32_t *group_order,
+                                     int64_t num_rows, int num_heads, int head_dim,
+                                     int block_size, int64_t num_blocks, float scale,
+                                     int dtype, const vfl_sched_meta *meta, void *stream);
 
 /*
  * Replaces ModelRunner._copy_blocks (vflorence/engine/model_runner.py:162-167):

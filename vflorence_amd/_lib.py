@@ -25,6 +25,7 @@ EXPORTED_SYMBOLS = (
     "vfl_reshape_and_cache",
     "vfl_get_scheduler_metadata",
     "vfl_attention_with_kv_cache",
+    "vfl_self_attention_with_kv_write",
     "vfl_copy_blocks",
 )
 
@@ -62,6 +63,11 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _i32,
          _i64, _f32, _i32, ctypes.POINTER(SchedMeta), _vp],
+    ),
+    "vfl_self_attention_with_kv_write": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+         _vp, _i64, _i32, _i32, _i32, _i64, _f32, _i32, ctypes.POINTER(SchedMeta), _vp],
     ),
     "vfl_copy_blocks": (
         ctypes.c_int,

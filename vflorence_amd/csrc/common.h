@@ -213,10 +213,25 @@ constexpr float NEG_INF_F = -__builtin_huge_valf();
 // the rescale.  The final normalisation makes the result exact in exact arithmetic.
 constexpr float RESCALE_SLACK_LOG2 = 8.0f;
 
-// V pools of 16-bit element type hold every [block][head] slice transposed
-// ([head_dim][block_size]) so the matrix-core kernel can feed tokens along the
-// reduction dimension; fp32 pools keep the logical [block_size][head_dim] order.
-inline bool v_tile_transposed(int dtype) { return dtype != VFL_FLOAT32; }
+// V pools of 16-bit element type hold every [block][head] slice with tokens grouped
+// by four and interleaved: [block_size/4][head_dim][4].  The matrix-core kernel then
+// reads 4 consecutive tokens of one dim as 8 bytes (its reduction operand), and one
+// token's head_dim values lie 8 bytes apart in a 512-byte span, so writing a token
+// touches few memory sectors.  fp32 pools keep the logical [block_size][head_dim].
+inline bool v_tile_interleaved(int dtype) { return dtype != VFL_FLOAT32; }
+
+// Element offset of (token t, dim d) inside an interleaved V tile of head size D.
+__host__ __device__ __forceinline__ int vtile_index(int t, int d, int D) {
+  return ((t >> 2) * D + d) * 4 + (t & 3);
+}
+
+// Workgroup barrier that orders LDS only: global stores issued before it (the fused
+// KV write) stay in flight instead of being drained, as __syncthreads() would.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // A wave's block ids, 64 at a time in one VGPR (lane i holds the id of block
 // base + i), read back with readlane: no scalar load sits between one block's

@@ -9,9 +9,10 @@
 //
 // The S output layout (lane l, register j -> row 4*(l/16)+j, column l%16) is exactly
 // the B-operand layout of the second product, so the probabilities never leave the
-// lane that computed them.  The second product needs tokens contiguous for a fixed
-// dim, which is why V pools of 16-bit type store each [block][head] slice transposed
-// ([head_dim][block_size]); K keeps the logical [block_size][head_dim] order.
+// lane that computed them.  The second product takes 4 consecutive tokens of one dim
+// per lane, which is why V pools of 16-bit type store each [block][head] slice with
+// tokens interleaved in groups of four ([block_size/4][head_dim][4], vtile_index);
+// K keeps the logical [block_size][head_dim] order.
 // P is split into two 16-bit terms (p = hi + lo) so the weights keep ~16 mantissa
 // bits; the extra products are cheap next to the HBM traffic.
 //
@@ -61,10 +62,21 @@ template <> struct Mfma<VFL_FLOAT16> {
 };
 
 // Loads of one block for this lane: D/32 16-byte K chunks (token `col`, dims
-// 32*kk + 8*rg ..) and D/16 8-byte V^T chunks (dim 16*c + col, tokens 4*rg ..).
+// 32*kk + 8*rg ..) and D/16 8-byte V chunks (dim 16*c + col, tokens 4*rg .. 4*rg+3).
 template <int D> struct MfmaBlock {
   uint4 k[D / 32];
   uint2 v[D / 16];
+};
+
+// The self-attention op's new token: its K/V rows and the slot they are written to.
+// With it, the kernel writes the slot itself and feeds the new values straight into
+// the last block instead of a separate scatter launch before the attention.
+struct KvWrite {
+  const uint16_t *k;
+  int64_t k_st, k_sh;
+  const uint16_t *v;
+  int64_t v_st, v_sh;
+  const int64_t *slots;
 };
 
 template <int DT, int D>
@@ -72,7 +84,6 @@ __device__ __forceinline__ void mfma_load_block(const uint16_t *__restrict__ kc,
                                                 const uint16_t *__restrict__ vc, int id, bool ok,
                                                 int64_t block_elems, int head_off, int k_lane,
                                                 int v_lane, MfmaBlock<D> &blk) {
-  constexpr int BS = 16;
   const int64_t base = (ok ? (int64_t)id : 0) * block_elems + head_off;
 #pragma unroll
   for (int kk = 0; kk < D / 32; ++kk) {
@@ -82,7 +93,7 @@ __device__ __forceinline__ void mfma_load_block(const uint16_t *__restrict__ kc,
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
     blk.v[c] = make_uint2(0, 0);
-    if (ok) blk.v[c] = *reinterpret_cast<const uint2 *>(vc + base + v_lane + 16 * c * BS);
+    if (ok) blk.v[c] = *reinterpret_cast<const uint2 *>(vc + base + v_lane + 64 * c);
   }
 }
 
@@ -148,14 +159,56 @@ __device__ __forceinline__ void mfma_consume(const uint4 (&qop)[D / 32], MfmaBlo
   }
 }
 
-template <int DT, int D, int NW, int U>
+// Put the new token (K row chunks newk, V values newv) into the registers of its block
+// and store it to the cache.  Lanes holding token t_new's K row (col == t_new) store
+// their 16-byte chunks; lanes holding its 4-token V group (rg == t_new / 4) store the
+// whole 8-byte word of each chunk, so 16 lanes cover one full 128-byte line and the
+// write needs no read-modify-write below.  The other three tokens' bytes go back
+// unchanged; no other workgroup touches this head's slice of a private block.
+template <int D>
+__device__ __forceinline__ void write_new_token(const uint16_t *kc, const uint16_t *vc, int id,
+                                                int64_t block_elems, int head_off, int k_lane,
+                                                int v_lane, int col, int rg, int t_new,
+                                                const uint4 (&newk)[D / 32],
+                                                const uint32_t (&newv)[D / 16],
+                                                MfmaBlock<D> &blk) {
+  uint16_t *tile_k = const_cast<uint16_t *>(kc) + (int64_t)id * block_elems + head_off;
+  uint16_t *tile_v = const_cast<uint16_t *>(vc) + (int64_t)id * block_elems + head_off;
+  if (col == t_new) {
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) {
+      blk.k[kk] = newk[kk];
+      *reinterpret_cast<uint4 *>(tile_k + k_lane + 32 * kk) = newk[kk];
+    }
+  }
+  if (rg == t_new / 4) {
+    // Selects, not a dynamically indexed reference, so the block stays in registers.
+    const bool upper = (t_new & 2) != 0;
+    const int sh = 16 * (t_new & 1);
+    const uint32_t keep = ~(0xffffu << sh);
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      const uint32_t x = (blk.v[c].x & keep) | (newv[c] << sh);
+      const uint32_t y = (blk.v[c].y & keep) | (newv[c] << sh);
+      blk.v[c].x = upper ? blk.v[c].x : x;
+      blk.v[c].y = upper ? y : blk.v[c].y;
+      *reinterpret_cast<uint2 *>(tile_v + v_lane + 64 * c) = blk.v[c];
+    }
+  }
+}
+
+// FUSE: also perform the KV slot write of `kvw` (one row per group).  The caller
+// guarantees that a row's slot, when it is the cache position of the row's last
+// context token, lies in a block no other row reads; the write then needs no ordering
+// against other workgroups.  A slot elsewhere is still written, without substitution.
+template <int DT, int D, int NW, int U, bool FUSE>
 __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
-    const uint16_t *__restrict__ q, int64_t q_st, int64_t q_sh, const uint16_t *__restrict__ kc,
-    const uint16_t *__restrict__ vc, uint16_t *__restrict__ out,
-    const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride,
-    int max_blocks, const int32_t *__restrict__ group_start,
-    const int32_t *__restrict__ group_order, int64_t num_rows, int64_t num_groups, int H,
-    int64_t num_blocks, float scale_log2) {
+    const uint16_t *__restrict__ q, int64_t q_st, int64_t q_sh, const uint16_t *kc,
+    const uint16_t *vc, uint16_t *__restrict__ out, const int32_t *__restrict__ seq_lens,
+    const int32_t *__restrict__ bt, int64_t bt_stride, int max_blocks,
+    const int32_t *__restrict__ group_start, const int32_t *__restrict__ group_order,
+    int64_t num_rows, int64_t num_groups, int H, int64_t num_blocks, float scale_log2,
+    KvWrite kvw) {
   constexpr int BS = 16;
   constexpr int KCH = D / 32;
   constexpr int VCH = D / 16;
@@ -185,14 +238,44 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
   const int col = lane & 15;  // query row (beam) of this lane's tile column
   const int rg = lane >> 4;   // row group: tokens 4*rg .. 4*rg+3 of a block
 
+  const int chunk = (nblk + NW - 1) / NW;
+  const int b0 = min(nblk, wave * chunk);
+  const int b1 = min(nblk, b0 + chunk);
+
+  // Fused KV write: the new token is position L-1; `subst` when its slot is where
+  // this row's table puts that position (the normal case).
+  int64_t wslot = -1;
+  int last = -1, t_new = 0;
+  int32_t lid = -1;
+  bool subst = false;
+  if constexpr (FUSE) {
+    wslot = kvw.slots[row0];
+    if (wslot >= num_blocks * BS) wslot = -1;
+    if (L >= 1 && (L - 1) / BS < nblk) {
+      last = (L - 1) / BS;
+      t_new = (L - 1) % BS;
+      lid = bt[(int64_t)row0 * bt_stride + last];
+      subst = wslot >= 0 && (int64_t)lid * BS + t_new == wslot;
+    }
+    // A slot the row does not attend to is written by wave 0 without substitution.
+    if (wslot >= 0 && !subst && wave == 0) {
+      const int64_t sb = wslot / BS, so = wslot % BS;
+      const uint16_t *ks = kvw.k + row0 * kvw.k_st + h * kvw.k_sh;
+      const uint16_t *vs = kvw.v + row0 * kvw.v_st + h * kvw.v_sh;
+      uint16_t *kd = const_cast<uint16_t *>(kc) + ((sb * H + h) * BS + so) * D;
+      uint16_t *vd = const_cast<uint16_t *>(vc) + (sb * H + h) * D * BS;
+      for (int d = lane; d < D; d += 64) {
+        kd[d] = ks[d];
+        vd[vtile_index((int)so, d, D)] = vs[d];
+      }
+    }
+  }
+
   if (nblk == 0) {
     for (int i = threadIdx.x; i < nrows * D; i += NW * 64)
       out[((int64_t)(row0 + i / D) * H + h) * D + i % D] = 0;
     return;
   }
-  const int chunk = (nblk + NW - 1) / NW;
-  const int b0 = min(nblk, wave * chunk);
-  const int b1 = min(nblk, b0 + chunk);
 
   // Q^T operand: lane holds Q[beam col][32*kk + 8*rg .. +7]; zero for absent beams.
   uint4 qop[KCH];
@@ -212,9 +295,32 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
   const int64_t block_elems = (int64_t)H * BS * D;
   const int head_off = h * BS * D;
   const int k_lane = col * D + 8 * rg;
-  const int v_lane = col * BS + 4 * rg;
+  const int v_lane = (rg * D + col) * 4;  // vtile_index(4 * rg, col, D)
 
-  const int bfull = max(b0, min(b1, Lc / BS));
+  int bfull = max(b0, min(b1, Lc / BS));
+  // The wave whose run ends with the new token's block loads that block and the new
+  // K/V first and issues the slot write after its first stage, so the write's latency
+  // hides behind the rest of the run; the block is still consumed last, in order, so
+  // results are bit-identical to the separate write + attention.
+  bool own_last = false;
+  int b_stop = b1;
+  MfmaBlock<D> lastblk;
+  uint4 newk[KCH];
+  uint32_t newv[VCH];
+  if constexpr (FUSE) {
+    own_last = subst && b0 <= last && last < b1;
+    if (own_last) {
+      b_stop = last;
+      mfma_load_block<DT, D>(kc, vc, lid, true, block_elems, head_off, k_lane, v_lane, lastblk);
+      const uint16_t *ks = kvw.k + row0 * kvw.k_st + h * kvw.k_sh;
+      const uint16_t *vs = kvw.v + row0 * kvw.v_st + h * kvw.v_sh;
+#pragma unroll
+      for (int kk = 0; kk < KCH; ++kk) newk[kk] = load16_unaligned<DT>(ks + 32 * kk + 8 * rg);
+#pragma unroll
+      for (int c = 0; c < VCH; ++c) newv[c] = vs[16 * c + col];
+    }
+  }
+  bfull = min(bfull, max(b0, b_stop));
   int b = b0;
   for (; b + U <= bfull; b += U) {
     MfmaBlock<D> blk[U];
@@ -234,13 +340,27 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
         mfma_consume<DT, D, true>(qop, blk[u], false, (b + u) * BS, Lc, rg, scale_log2, m, l,
                                   acc);
     }
+    if constexpr (FUSE) {
+      if (own_last && b == b0)
+        write_new_token<D>(kc, vc, lid, block_elems, head_off, k_lane, v_lane, col, rg, t_new,
+                           newk, newv, lastblk);
+    }
   }
-  for (; b < b1; ++b) {
+  if constexpr (FUSE) {
+    if (own_last && bfull - b0 < U)  // no whole stage ran: write now
+      write_new_token<D>(kc, vc, lid, block_elems, head_off, k_lane, v_lane, col, rg, t_new,
+                         newk, newv, lastblk);
+  }
+  for (; b < b_stop; ++b) {
     MfmaBlock<D> blk;
     const int id = ids.get(b);
     const bool ok = id >= 0 && id < num_blocks;
     mfma_load_block<DT, D>(kc, vc, id, ok, block_elems, head_off, k_lane, v_lane, blk);
     mfma_consume<DT, D, true>(qop, blk, ok, b * BS, Lc, rg, scale_log2, m, l, acc);
+  }
+  if constexpr (FUSE) {
+    if (own_last)
+      mfma_consume<DT, D, true>(qop, lastblk, true, last * BS, Lc, rg, scale_log2, m, l, acc);
   }
 
   // Column totals of the running sums (the 4 row groups hold disjoint tokens).
@@ -266,7 +386,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
       s_ml[wave][0][col] = m;
       s_ml[wave][1][col] = l;
     }
-    __syncthreads();
+    lds_barrier();
     for (int i = threadIdx.x; i < nrows * D; i += NW * 64) {
       const int beam = i / D, d = i % D;
       float M = NEG_INF_F;

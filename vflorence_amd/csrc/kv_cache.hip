@@ -33,8 +33,8 @@ int launch_status(const char *what) {
 // ---------------------------------------------------------------------------
 // reshape_and_cache: one thread per 16-byte chunk of a (token, head) row.
 // ---------------------------------------------------------------------------
-// VT: the V pool stores each [block][head] slice transposed ([head_dim][block_size],
-// 16-bit pools); the token's head_dim values then land block_size elements apart.
+// VT: the V pool stores each [block][head] slice with tokens interleaved in groups of
+// four (16-bit pools, vtile_index); the token's head_dim values land 4 elements apart.
 template <int DT, bool ALIGNED, bool VT>
 __global__ __launch_bounds__(256) void reshape_and_cache_kernel(
     const typename Elem<DT>::T *__restrict__ key, const typename Elem<DT>::T *__restrict__ value,
@@ -69,11 +69,12 @@ __global__ __launch_bounds__(256) void reshape_and_cache_kernel(
     store16_unaligned<DT>(kc + dst, kv);
   }
   if constexpr (VT) {
-    static_assert(DT != VFL_FLOAT32, "transposed V tiles are 16-bit");
-    T *vt = vc + ((blk * num_heads + h) * head_dim + c * VEC) * block_size + off;
+    static_assert(DT != VFL_FLOAT32, "interleaved V tiles are 16-bit");
+    T *vt = vc + (blk * num_heads + h) * (int64_t)head_dim * block_size;
     const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) vt[e * block_size] = (T)(w[e / 2] >> (16 * (e & 1)));
+    for (int e = 0; e < VEC; ++e)
+      vt[vtile_index(off, c * VEC + e, head_dim)] = (T)(w[e / 2] >> (16 * (e & 1)));
   } else if constexpr (ALIGNED) {
     *reinterpret_cast<uint4 *>(vc + dst) = vv;
   } else {
@@ -91,7 +92,7 @@ static void launch_reshape(bool aligned, const void *key, const void *value, int
   const int64_t total = T * H * cpr;
   const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
-  constexpr bool VT = DT != VFL_FLOAT32;  // v_tile_transposed(DT)
+  constexpr bool VT = DT != VFL_FLOAT32;  // v_tile_interleaved(DT)
   if (aligned)
     reshape_and_cache_kernel<DT, true, VT><<<dim3((unsigned)blocks), dim3(threads), 0, stream>>>(
         (const E *)key, (const E *)value, k_st, k_sh, v_st, v_sh, (E *)kc, (E *)vc, slots, T, H,

@@ -304,7 +304,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     for (int i = threadIdx.x; i < nrows * D; i += NW * 64) {
       const int gi = i / D, d = i % D;
       float M = NEG_INF_F;
@@ -347,6 +347,7 @@ struct AttnArgs {
   int64_t num_blocks;
   float scale_log2;
   hipStream_t stream;
+  KvWrite kvw;  // slots == nullptr: no fused KV write
 };
 
 // fp32 caches: VALU kernel over the logical V layout, G query rows per group.
@@ -382,17 +383,25 @@ static int valu_group(const AttnArgs &a, int gmax, int nw) {
   return valu_waves<D, 8>(a, nw);
 }
 
-// bf16 / fp16 caches: matrix-core kernel over the tile-transposed V layout; the tile
+// bf16 / fp16 caches: matrix-core kernel over the token-interleaved V layout; the tile
 // columns hold up to 16 query rows per group, so one instantiation serves any G.
 constexpr int MFMA_STAGE_BLOCKS = 2;
 
 template <int DT, int D, int NW>
 static int launch_mfma(const AttnArgs &a) {
   const dim3 grid((unsigned)(a.num_groups * a.H));
-  paged_decode_mfma_kernel<DT, D, NW, MFMA_STAGE_BLOCKS><<<grid, dim3(NW * 64), 0, a.stream>>>(
-      (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
-      (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
-      a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2);
+  if (a.kvw.slots)
+    paged_decode_mfma_kernel<DT, D, NW, MFMA_STAGE_BLOCKS, true>
+        <<<grid, dim3(NW * 64), 0, a.stream>>>(
+        (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
+        (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
+        a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw);
+  else
+    paged_decode_mfma_kernel<DT, D, NW, MFMA_STAGE_BLOCKS, false>
+        <<<grid, dim3(NW * 64), 0, a.stream>>>(
+        (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
+        (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
+        a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw);
   return launch_status("attention_with_kv_cache");
 }
 
@@ -498,65 +507,65 @@ extern "C" int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, 
   return VFL_OK;
 }
 
-extern "C" int vfl_attention_with_kv_cache(
-    const void *query, int64_t query_stride_token, int64_t query_stride_head,
-    const void *k_cache, const void *v_cache, void *out, const int32_t *seq_lens,
-    const int32_t *block_table, int64_t block_table_stride, const int32_t *group_start,
-    const int32_t *group_order, int64_t num_rows, int64_t num_groups, int num_heads,
-    int head_dim, int block_size, int64_t num_blocks, float scale, int dtype,
-    const vfl_sched_meta *meta, void *stream) {
-  clear_error();
+// Shared argument checks and launch of both attention entry points.
+static int attention_impl(const void *query, int64_t query_stride_token,
+                          int64_t query_stride_head, const void *k_cache, const void *v_cache,
+                          void *out, const int32_t *seq_lens, const int32_t *block_table,
+                          int64_t block_table_stride, const int32_t *group_start,
+                          const int32_t *group_order, int64_t num_rows, int64_t num_groups,
+                          int num_heads, int head_dim, int block_size, int64_t num_blocks,
+                          float scale, int dtype, const vfl_sched_meta *meta, void *stream,
+                          const KvWrite &kvw, const char *who) {
   if (!meta) {
-    set_error("attention_with_kv_cache: meta is NULL");
+    set_error("%s: meta is NULL", who);
     return VFL_E_INVALID;
   }
   if (!kernel_exists(dtype, block_size, head_dim)) {
-    set_error("attention_with_kv_cache: no kernel for dtype %d block_size %d head_dim %d", dtype,
-              block_size, head_dim);
+    set_error("%s: no kernel for dtype %d block_size %d head_dim %d", who, dtype, block_size,
+              head_dim);
     return VFL_E_UNSUPPORTED;
   }
   if (num_rows < 0 || num_heads <= 0 || num_blocks < 0) {
-    set_error("attention_with_kv_cache: bad sizes");
+    set_error("%s: bad sizes", who);
     return VFL_E_INVALID;
   }
   if (meta->num_rows != num_rows || meta->num_groups != num_groups ||
       meta->num_heads != num_heads || meta->head_dim != head_dim) {
-    set_error("attention_with_kv_cache: metadata was made for rows %lld groups %lld heads %d "
-              "head_dim %d, call has rows %lld groups %lld heads %d head_dim %d",
-              (long long)meta->num_rows, (long long)meta->num_groups, meta->num_heads,
+    set_error("%s: metadata was made for rows %lld groups %lld heads %d head_dim %d, call has "
+              "rows %lld groups %lld heads %d head_dim %d",
+              who, (long long)meta->num_rows, (long long)meta->num_groups, meta->num_heads,
               meta->head_dim, (long long)num_rows, (long long)num_groups, num_heads, head_dim);
     return VFL_E_INVALID;
   }
   if (group_start == nullptr && num_groups != num_rows) {
-    set_error("attention_with_kv_cache: without group_start, num_groups (%lld) must equal "
-              "num_rows (%lld)",
+    set_error("%s: without group_start, num_groups (%lld) must equal num_rows (%lld)", who,
               (long long)num_groups, (long long)num_rows);
     return VFL_E_INVALID;
   }
   if (num_groups < 0 || num_groups > num_rows || num_groups * num_heads > 2147483647LL ||
       num_heads > 65535) {
-    set_error("attention_with_kv_cache: num_groups %lld / num_heads %d out of range",
-              (long long)num_groups, num_heads);
+    set_error("%s: num_groups %lld / num_heads %d out of range", who, (long long)num_groups,
+              num_heads);
     return VFL_E_INVALID;
   }
   const int nw = meta->waves_per_workgroup;
   if (meta->max_group_size < 1 || meta->max_group_size > MAX_GROUP ||
       (nw != 1 && nw != 2 && nw != 4 && nw != 8) || meta->max_blocks_per_seq < 0) {
-    set_error("attention_with_kv_cache: inconsistent metadata");
+    set_error("%s: inconsistent metadata", who);
     return VFL_E_INVALID;
   }
   if (block_table_stride < meta->max_blocks_per_seq) {
-    set_error("attention_with_kv_cache: block_table_stride %lld < max_blocks_per_seq %d",
+    set_error("%s: block_table_stride %lld < max_blocks_per_seq %d", who,
               (long long)block_table_stride, meta->max_blocks_per_seq);
     return VFL_E_INVALID;
   }
   if (num_rows == 0 || num_groups == 0) return VFL_OK;
   if (!query || !k_cache || !v_cache || !out || !seq_lens || !block_table) {
-    set_error("attention_with_kv_cache: null pointer argument");
+    set_error("%s: null pointer argument", who);
     return VFL_E_INVALID;
   }
   if (((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) % 16 != 0) {
-    set_error("attention_with_kv_cache: caches and out must be 16-byte aligned");
+    set_error("%s: caches and out must be 16-byte aligned", who);
     return VFL_E_INVALID;
   }
   AttnArgs a;
@@ -578,5 +587,57 @@ extern "C" int vfl_attention_with_kv_cache(
   a.num_blocks = num_blocks;
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
   a.stream = (hipStream_t)stream;
+  a.kvw = kvw;
   return dispatch(a, dtype, head_dim, meta->max_group_size, nw);
+}
+
+extern "C" int vfl_attention_with_kv_cache(
+    const void *query, int64_t query_stride_token, int64_t query_stride_head,
+    const void *k_cache, const void *v_cache, void *out, const int32_t *seq_lens,
+    const int32_t *block_table, int64_t block_table_stride, const int32_t *group_start,
+    const int32_t *group_order, int64_t num_rows, int64_t num_groups, int num_heads,
+    int head_dim, int block_size, int64_t num_blocks, float scale, int dtype,
+    const vfl_sched_meta *meta, void *stream) {
+  clear_error();
+  const KvWrite none = {nullptr, 0, 0, nullptr, 0, 0, nullptr};
+  return attention_impl(query, query_stride_token, query_stride_head, k_cache, v_cache, out,
+                        seq_lens, block_table, block_table_stride, group_start, group_order,
+                        num_rows, num_groups, num_heads, head_dim, block_size, num_blocks, scale,
+                        dtype, meta, stream, none, "attention_with_kv_cache");
+}
+
+extern "C" int vfl_self_attention_with_kv_write(
+    const void *query, int64_t query_stride_token, int64_t query_stride_head, const void *key,
+    int64_t key_stride_token, int64_t key_stride_head, const void *value,
+    int64_t value_stride_token, int64_t value_stride_head, const int64_t *slot_mapping,
+    void *k_cache, void *v_cache, void *out, const int32_t *seq_lens,
+    const int32_t *block_table, int64_t block_table_stride, const int32_t *group_order,
+    int64_t num_rows, int num_heads, int head_dim, int block_size, int64_t num_blocks,
+    float scale, int dtype, const vfl_sched_meta *meta, void *stream) {
+  clear_error();
+  if (num_rows > 0 && (!key || !value || !slot_mapping)) {
+    set_error("self_attention_with_kv_write: null key, value or slot_mapping");
+    return VFL_E_INVALID;
+  }
+  if (dtype == VFL_FLOAT32) {
+    // The fp32 path has no fused kernel: the same two steps as the reference.
+    int st = vfl_reshape_and_cache(key, value, key_stride_token, key_stride_head,
+                                   value_stride_token, value_stride_head, k_cache, v_cache,
+                                   slot_mapping, num_rows, num_heads, head_dim, block_size,
+                                   num_blocks, dtype, stream);
+    if (st != VFL_OK) return st;
+    return vfl_attention_with_kv_cache(query, query_stride_token, query_stride_head, k_cache,
+                                       v_cache, out, seq_lens, block_table, block_table_stride,
+                                       nullptr, group_order, num_rows, num_rows, num_heads,
+                                       head_dim, block_size, num_blocks, scale, dtype, meta,
+                                       stream);
+  }
+  const KvWrite kvw = {(const uint16_t *)key, key_stride_token, key_stride_head,
+                       (const uint16_t *)value, value_stride_token, value_stride_head,
+                       slot_mapping};
+  if (num_rows == 0) return VFL_OK;
+  return attention_impl(query, query_stride_token, query_stride_head, k_cache, v_cache, out,
+                        seq_lens, block_table, block_table_stride, nullptr, group_order,
+                        num_rows, num_rows, num_heads, head_dim, block_size, num_blocks, scale,
+                        dtype, meta, stream, kvw, "self_attention_with_kv_write");
 }

@@ -30,13 +30,24 @@ _DTYPE_CODES = {
 SUPPORTED_HEAD_DIMS = frozenset({64, 128})
 SUPPORTED_BLOCK_SIZES = frozenset({16})
 MAX_GROUP_SIZE = 8
+# Waves per workgroup for the fused KV-write + self-attention launch (measured: two
+# beat four on both short decode-step contexts and 256 ragged rows up to 1024 tokens).
+FUSED_WAVES = 2
 
 
-def v_tile_transposed(dtype: torch.dtype) -> bool:
-    """Whether V pools of ``dtype`` store each [block][head] slice transposed.
+def _pow2_at_least(n: int) -> int:
+    p = 1
+    while p < n:
+        p *= 2
+    return p
 
-    16-bit pools keep each 2 KiB block-head slice of V as [head_dim][block_size] so
-    the matrix-core decode kernel reads tokens contiguously for a fixed dim; fp32 pools
+
+def v_tile_interleaved(dtype: torch.dtype) -> bool:
+    """Whether V pools of ``dtype`` store each [block][head] slice token-interleaved.
+
+    16-bit pools keep each block-head slice of V as [block_size/4][head_dim][4]: four
+    consecutive tokens of one dim are adjacent, which is the reduction operand of the
+    matrix-core kernel, and a token's head_dim values are 8 bytes apart.  fp32 pools
     keep the logical [block_size][head_dim] order.  The tensor shape is the reference's
     [num_blocks, H, block_size, head_dim] either way, and only this library's ops
     address the inside of a block (the reference leaves that layout to the attention
@@ -46,19 +57,20 @@ def v_tile_transposed(dtype: torch.dtype) -> bool:
 
 
 def v_cache_logical(v_cache: torch.Tensor) -> torch.Tensor:
-    """[NB, H, bs, D] view of a V pool in logical (token, dim) order."""
-    if not v_tile_transposed(v_cache.dtype):
+    """V pool values in logical [NB, H, bs, D] (token, dim) order (a copy for 16-bit pools)."""
+    if not v_tile_interleaved(v_cache.dtype):
         return v_cache
     nb, h, bs, d = v_cache.shape
-    return v_cache.view(nb, h, d, bs).transpose(2, 3)
+    return v_cache.view(nb, h, bs // 4, d, 4).permute(0, 1, 2, 4, 3).reshape(nb, h, bs, d)
 
 
 def v_cache_from_logical(v_logical: torch.Tensor) -> torch.Tensor:
     """A contiguous V pool (device layout) holding the given logical [NB, H, bs, D] values."""
-    if not v_tile_transposed(v_logical.dtype):
+    if not v_tile_interleaved(v_logical.dtype):
         return v_logical.contiguous()
     nb, h, bs, d = v_logical.shape
-    return v_logical.transpose(2, 3).contiguous().view(nb, h, bs, d)
+    return (v_logical.reshape(nb, h, bs // 4, 4, d).permute(0, 1, 2, 4, 3).contiguous()
+            .view(nb, h, bs, d))
 
 
 def _dtype_code(dtype: torch.dtype) -> int:
@@ -166,6 +178,10 @@ class SchedulerMetadata:
     num_groups: int | None = None
     max_group_size: int = 1
     waves_per_workgroup: int = 0
+    # The caller's promise that each row writes its new token at the slot of its last
+    # context position, in a block no other row reads (the block manager's
+    # copy-on-write invariant); lets the self-attention op fuse the KV write.
+    fuse_kv_write: bool = False
     _plans: dict = field(default_factory=dict, repr=False)
 
     def plan(self, num_rows: int, max_blocks: int) -> SchedMeta:
@@ -174,11 +190,15 @@ class SchedulerMetadata:
         if meta is None:
             meta = SchedMeta()
             groups = num_rows if self.group_start is None else self.num_groups
+            waves = self.waves_per_workgroup
+            if waves == 0 and self.fuse_kv_write:
+                # measured best for the fused write + attention kernel (MI355X, bf16)
+                waves = min(FUSED_WAVES, _pow2_at_least(max_blocks))
             check(
                 lib.vfl_get_scheduler_metadata(
                     num_rows, groups, self.num_heads, self.head_dim, self.block_size,
-                    max_blocks, self.max_group_size, _dtype_code(self.dtype),
-                    self.waves_per_workgroup, ctypes.byref(meta),
+                    max_blocks, self.max_group_size, _dtype_code(self.dtype), waves,
+                    ctypes.byref(meta),
                 )
             )
             self._plans[key] = meta
@@ -207,6 +227,7 @@ def get_scheduler_metadata(
     group_order: torch.Tensor | None = None,
     max_group_size: int = 1,
     waves_per_workgroup: int = 0,
+    fuse_kv_write: bool = False,
 ) -> SchedulerMetadata:
     """Counterpart of ``vllm_cpu_attn.get_scheduler_metadata`` (keyword names from
     vflorence/layers/attention.py:18-29 and vflorence/engine/model_runner.py:308-319).
@@ -244,6 +265,7 @@ def get_scheduler_metadata(
         num_groups=num_groups,
         max_group_size=max_group_size,
         waves_per_workgroup=waves_per_workgroup,
+        fuse_kv_write=fuse_kv_write,
     )
 
 
@@ -320,6 +342,75 @@ def attention_with_kv_cache(
             None if sm.group_order is None else sm.group_order.data_ptr(),
             num_rows, num_groups, num_heads, head_dim, block_size, num_blocks, float(scale),
             _dtype_code(query.dtype), ctypes.byref(meta), _stream(dev),
+        )
+    )
+
+
+def self_attention_with_kv_write(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    out: torch.Tensor,
+    seq_lens: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    *,
+    scale: float,
+    block_table: torch.Tensor,
+    scheduler_metadata: SchedulerMetadata,
+) -> None:
+    """``reshape_and_cache`` + ``attention_with_kv_cache`` in one launch (the body of the
+    reference's vflorence::self_attention op, vflorence/layers/attention.py:53-73).
+
+    Only valid under ``scheduler_metadata.fuse_kv_write`` (see SchedulerMetadata); the
+    op falls back to the two calls otherwise.
+    """
+    sm = scheduler_metadata
+    if not sm.fuse_kv_write:
+        raise ValueError("self_attention_with_kv_write needs metadata made with fuse_kv_write=True")
+    if sm.group_start is not None:
+        raise ValueError("the fused self-attention path takes one row per group")
+    dev = _require_gpu(query, key, value, k_cache, v_cache, out, seq_lens, slot_mapping,
+                       block_table)
+    if key.dim() != 3 or value.shape != key.shape or key.shape != query.shape:
+        raise ValueError("query, key and value must be [N, H, D] of one shape")
+    if key.stride(-1) != 1 or value.stride(-1) != 1 or query.stride(-1) != 1:
+        raise ValueError("query/key/value need a contiguous last dimension")
+    num_rows, num_heads, head_dim = query.shape
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must be [num_blocks, H, block_size, D] of one shape")
+    num_blocks, cache_heads, block_size, cache_dim = k_cache.shape
+    if (cache_heads, cache_dim) != (num_heads, head_dim):
+        raise ValueError("query/key shape does not match the caches")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    if not (query.dtype == key.dtype == value.dtype == k_cache.dtype == v_cache.dtype == out.dtype):
+        raise ValueError("query, key, value, caches and out must share one dtype")
+    if out.shape != query.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of query's shape")
+    if seq_lens.dtype != torch.int32 or seq_lens.shape != (num_rows,):
+        raise ValueError(f"seq_lens must be int32 [{num_rows}]")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.shape != (num_rows,):
+        raise ValueError(f"slot_mapping must be int64 [{num_rows}]")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != num_rows:
+        raise ValueError(f"block_table must be int32 [{num_rows}, max_blocks]")
+    if block_table.stride(1) != 1:
+        block_table = block_table.contiguous()
+    seq_lens = seq_lens.contiguous()
+    slot_mapping = slot_mapping.contiguous()
+    if sm.group_order is not None:
+        _require_gpu(query, sm.group_order)
+    meta = sm.plan(num_rows, block_table.shape[1])
+    check(
+        lib.vfl_self_attention_with_kv_write(
+            query.data_ptr(), query.stride(0), query.stride(1), key.data_ptr(), key.stride(0),
+            key.stride(1), value.data_ptr(), value.stride(0), value.stride(1),
+            slot_mapping.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+            seq_lens.data_ptr(), block_table.data_ptr(), block_table.stride(0),
+            None if sm.group_order is None else sm.group_order.data_ptr(), num_rows, num_heads,
+            head_dim, block_size, num_blocks, float(scale), _dtype_code(query.dtype),
+            ctypes.byref(meta), _stream(dev),
         )
     )
 

@@ -113,8 +113,26 @@ def decoder_self_attention(
 ) -> torch.Tensor:
     """Write new K/V into the paged cache and run self-attention."""
     ctx = get_context()
-    hip_attn.reshape_and_cache(key, value, k_cache, v_cache, ctx.slot_mapping, isa=ctx.isa)
     out = query.new_empty(query.shape)
+    meta = ctx.self_metadata
+    if meta is not None and meta.fuse_kv_write:
+        # The runner built the slots from block-manager tables: one launch writes the
+        # new K/V and attends (same cache contents and output as the two calls below).
+        hip_attn.self_attention_with_kv_write(
+            query,
+            key,
+            value,
+            k_cache,
+            v_cache,
+            out,
+            ctx.context_lens,
+            ctx.slot_mapping,
+            scale=scale,
+            block_table=ctx.block_tables,
+            scheduler_metadata=meta,
+        )
+        return out
+    hip_attn.reshape_and_cache(key, value, k_cache, v_cache, ctx.slot_mapping, isa=ctx.isa)
     # One query per sequence, the newest token; the cache holds nothing after it, so
     # attending to the whole context is the causal result.
     hip_attn.attention_with_kv_cache(
