@@ -24,6 +24,7 @@ import ctypes
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -47,6 +48,9 @@ def parse_args():
     p.add_argument("--kernel-reps", type=int, default=20,
                    help="launches per layer when timing the dominant kernel")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--counters", action="store_true",
+                   help="counter-collection run for rocprofv3 --pmc: the dominant kernel's "
+                        "launches and two copies of known size, nothing timed")
     return p.parse_args()
 
 
@@ -316,6 +320,56 @@ def self_op_timing(torch, reps: int, seed: int):
     return k_avg, kernel_bytes / len(cases), o_avg, op_bytes / len(cases), cases
 
 
+COPY_BYTES = 1 << 30
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_cross_attention_bart_large_4beam_bf16.md")
+
+
+def counter_pass(torch, wl, reps: int):
+    """What a byte-counter pass measures: the cross-attention launches over the 12 layers'
+    pools (``reps`` rounds), then two plain copies of COPY_BYTES each (a device-to-device
+    memcpy and an elementwise negation), whose counter readings calibrate the counters
+    against a known byte count."""
+    from vflorence_amd import workloads
+
+    launches = []
+    for i in range(NUM_LAYERS):
+        k, v, table, lens, sm = wl["staged"][i]
+        out = torch.empty_like(wl["qc"][i])
+        launches.append(raw_attention_launcher(torch, wl["qc"][i], k, v, out, lens, table, sm))
+    for _ in range(reps):
+        for f in launches:
+            f()
+    torch.cuda.synchronize()
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    c_bytes = workloads.cross_attention_bytes(wl["enc"], REQUESTS * BEAMS, NUM_HEADS, HEAD_DIM,
+                                              2, BLOCK)
+    print(json.dumps({"counter_pass": True, "cross_launches": NUM_LAYERS * (reps + 1),
+                      "cross_grid_threads": REQUESTS * NUM_HEADS * 64 * 4,
+                      "cross_algorithmic_bytes": int(c_bytes), "copy_bytes": COPY_BYTES,
+                      "copies": ["hipMemcpy device-to-device", "torch.neg float32"]}),
+          flush=True)
+
+
+def measured_traffic(c_bytes: int):
+    """HBM bytes per cross-attention launch from the committed counter summary, if it was
+    taken on this same workload (its algorithmic byte count matches); else None."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    fields = dict(re.findall(r"^- (\w+): (\d+)\s*$", text, flags=re.M))
+    if int(fields.get("algorithmic_bytes_per_launch", -1)) != int(c_bytes):
+        return None
+    t = fields.get("traffic_bytes_per_launch")
+    return int(t) if t is not None else None
+
+
 def cpu_baseline(torch, wl, budget_s: float):
     """The C restatement (oracle/, OpenMP, fp32 accumulation) on one decoder layer of the
     same workload: per sampled step, the CoW copy of that layer's two caches, the KV slot
@@ -395,6 +449,9 @@ def main():
     torch.manual_seed(args.seed)
     print("[bench] building workload (12 layers, 64 requests x 4 beams, bf16)", flush=True)
     wl = build_workload(torch, args.seed)
+    if args.counters:
+        counter_pass(torch, wl, reps=2)
+        return
     print("[bench] capturing 128 decode-step graphs", flush=True)
     graphs, keep = capture_steps(torch, wl)
     plans = wl["plans"]
@@ -470,12 +527,13 @@ def main():
         "wall_s_timed": round(wall, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_kernel<bf16, D=64, G=4> (cross-attention, 4 beams/group)",
+            "kernel": ("paged_decode_mfma_kernel<bf16, D=64, 4 waves, 2 blocks/stage> "
+                       "(cross-attention, 4 beams per group)"),
             "achieved": round(c_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(c_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(c_bytes),
             "avg_launch_us": round(c_avg * 1e6, 2),
             "algorithmic_bytes_per_launch": int(c_bytes),
         },
