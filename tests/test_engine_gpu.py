@@ -1,0 +1,195 @@
+"""The engine on the GPU: tokens equal transformers' (fp32, greedy and beam search),
+the runner's step metadata and encoder paging follow the reference's formulas, and
+every block and encoder page returns to its pool after a run or a failed step."""
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "token_fixtures.json")
+
+
+def fixtures():
+    with open(GOLDEN) as f:
+        return json.load(f)
+
+
+def engine(cfg_kwargs, checksum, **kwargs):
+    from transformers import BartConfig
+
+    from vflorence_amd import LLM
+    from vflorence_amd.utils.loader import state_dict_checksum, synthetic_state_dict
+
+    cfg = BartConfig(**cfg_kwargs)
+    sd = synthetic_state_dict(cfg, seed=0, device="cuda")
+    assert state_dict_checksum(sd) == checksum, "GPU-made weights differ from the fixture's"
+    return LLM(cfg, state_dict=sd, **kwargs)
+
+
+def assert_clean(llm):
+    bm = llm.scheduler.block_manager
+    assert llm.is_finished()
+    assert bm.num_free_blocks == bm.num_blocks and not any(bm.ref_counts)
+    assert not llm.scheduler._finished_beams
+    runner = llm.runner
+    assert not runner._cross_pages
+    assert sorted(runner._cross_free) == list(range(llm.config.num_cross_blocks))
+    assert runner._cross_staged is None
+
+
+SMALL_CASES = ["greedy", "greedy_rules", "greedy_forced", "beam2", "beam4_early", "beam4_rules"]
+
+
+@pytest.fixture(scope="module")
+def small_engine():
+    fx = fixtures()["small"]
+    return engine(fx["config"], fx["checksum"], max_num_seqs=24, dtype=torch.float32,
+                  max_decoder_len=32, max_encoder_len=128)
+
+
+@pytest.mark.parametrize("case", SMALL_CASES)
+def test_tokens_match_transformers_small_bart(small_engine, case):
+    from vflorence_amd import Request, SamplingParams
+
+    fx = fixtures()["small"]
+    c = fx["cases"][case]
+    # every near-tie in the fixture is far above fp32 noise
+    assert all(g is None or g > 1e-4 for g in c["min_gap"])
+    outs = small_engine.generate([Request(p) for p in fx["prompts"]], SamplingParams(**c["params"]))
+    got = [o.completion_token_ids for o in outs]
+    assert got == c["tokens"]
+    assert_clean(small_engine)
+
+
+def test_tokens_match_transformers_bart_large_fp32():
+    """BART-large shapes (12+12 layers, 16 heads x 64, vocab 50265), fp32, 8 requests
+    with encoder prompts of 128..1024 tokens, 64 greedy tokens each, batched."""
+    from vflorence_amd import Request, SamplingParams
+
+    fx = fixtures()["bart_large"]
+    c = fx["cases"]["greedy64"]
+    assert all(g > 1e-4 for g in c["min_gap"])
+    llm = engine(fx["config"], fx["checksum"], max_num_seqs=8, dtype=torch.float32,
+                 max_decoder_len=64, max_encoder_len=1024)
+    outs = llm.generate([Request(p) for p in fx["prompts"]], SamplingParams(**c["params"]))
+    assert [o.completion_token_ids for o in outs] == c["tokens"]
+    assert_clean(llm)
+
+
+def test_bf16_engine_runs_beams_and_stays_clean(small_engine):
+    from vflorence_amd import Request, SamplingParams
+
+    fx = fixtures()["small"]
+    llm = engine(fx["config"], fx["checksum"], max_num_seqs=24, dtype=torch.bfloat16,
+                 max_decoder_len=32, max_encoder_len=128)
+    params = SamplingParams(**fx["cases"]["beam4_early"]["params"])
+    outs = llm.generate([Request(p) for p in fx["prompts"]], params)
+    assert all(1 <= len(o.completion_token_ids) <= params.max_tokens for o in outs)
+    assert_clean(llm)
+
+
+def test_prepare_and_encode_follow_the_reference_formulas(small_engine):
+    """Slots, context lengths, tables and positions of one step
+    (model_runner.py:294-305) and the paged encoder K/V (:236-259) read back from HBM."""
+    from vflorence_amd import SamplingParams, hip_attn
+    from vflorence_amd.engine.sequence import Sequence
+    from vflorence_amd.utils.context import get_context
+
+    llm = small_engine
+    runner = llm.runner
+    params = SamplingParams(max_tokens=8).with_defaults(llm._sampling_params)
+    fx = fixtures()["small"]
+    seqs = [Sequence(i, [2], fx["prompts"][i], params) for i in range(3)]
+    bm = llm.scheduler.block_manager
+    with torch.inference_mode():
+        runner._encode(seqs)
+        # feed a few tokens by hand: seq i has i + 1 tokens cached before this step
+        for i, seq in enumerate(seqs):
+            seq.token_ids = [2] + [10 + t for t in range(i + 17)]
+            seq.num_cached_tokens = len(seq.token_ids) - 1
+            while len(seq.block_table) * 16 <= seq.num_cached_tokens:
+                seq.block_table.append(bm._allocate_block())
+        ids, pos = runner._prepare(seqs)
+        ctx = get_context()
+        want_pos = [s.num_cached_tokens for s in seqs]
+        assert pos.tolist() == want_pos
+        assert ids.tolist() == [s.token_ids[p] for s, p in zip(seqs, want_pos)]
+        assert ctx.context_lens.tolist() == [p + 1 for p in want_pos]
+        assert ctx.slot_mapping.tolist() == [s.block_table[p // 16] * 16 + p % 16
+                                             for s, p in zip(seqs, want_pos)]
+        width = max(len(s.block_table) for s in seqs)
+        assert ctx.block_tables.tolist() == [s.block_table + [0] * (width - len(s.block_table))
+                                             for s in seqs]
+        assert ctx.query_start_loc.tolist() == list(range(4))
+        # encoder pages: request i's tokens at pages[t // 16] * 16 + t % 16 hold kv_proj
+        layer = runner.decoder_layers[1]
+        attn = layer.encoder_attn
+        for seq in seqs:
+            pages, enc_len = runner._cross_pages[seq.request_id]
+            assert enc_len == len(seq.encoder_token_ids) and len(pages) == math.ceil(enc_len / 16)
+            hidden = runner.model.encode(torch.tensor([seq.encoder_token_ids], device="cuda"))
+            k, v = attn.kv_proj(hidden)[0].chunk(2, dim=-1)
+            t = torch.arange(enc_len)
+            blk, off = pages[t // 16].long().cuda(), (t % 16).cuda()
+            kc = attn.k_cache[blk, :, off, :]
+            vc = hip_attn.v_cache_logical(attn.v_cache)[blk, :, off, :]
+            torch.testing.assert_close(kc, k.view(enc_len, attn.num_heads, -1), rtol=0, atol=0)
+            torch.testing.assert_close(vc, v.view(enc_len, attn.num_heads, -1), rtol=0, atol=0)
+    from vflorence_amd.utils.context import set_context
+
+    set_context()
+    for seq in seqs:
+        bm.deallocate(seq)
+        runner.clear_request(seq.request_id)
+    assert_clean(llm)
+
+
+def test_failed_step_releases_everything(small_engine):
+    from vflorence_amd import Request, SamplingParams
+
+    llm = small_engine
+    model = llm.runner.model
+    fx = fixtures()["small"]
+    calls = []
+    original = model.forward
+
+    def failing(*args):
+        calls.append(1)
+        if len(calls) == 3:
+            raise RuntimeError("decode failed")
+        return original(*args)
+
+    model.forward = failing
+    try:
+        with pytest.raises(RuntimeError, match="decode failed"):
+            llm.generate([Request(p) for p in fx["prompts"][:3]],
+                         SamplingParams(max_tokens=8, num_beams=2))
+    finally:
+        del model.forward
+    assert_clean(llm)
+    from vflorence_amd.utils.context import get_context
+
+    assert get_context().cross_staged is None
+    # and the engine still works
+    outs = llm.generate([Request(fx["prompts"][0])], SamplingParams(max_tokens=4))
+    assert len(outs[0].completion_token_ids) >= 1
+    assert_clean(llm)
+
+
+def test_rejected_request_returns_empty_and_others_run(small_engine):
+    from vflorence_amd import Request, SamplingParams
+
+    fx = fixtures()["small"]
+    too_long = Request(list(range(3, 3 + 200)))
+    outs = small_engine.generate([Request(fx["prompts"][0]), too_long],
+                                 SamplingParams(max_tokens=4))
+    assert len(outs[0].completion_token_ids) >= 1 and outs[1].completion_token_ids == []
+    assert_clean(small_engine)
+    with pytest.raises(ValueError):
+        small_engine.add_request(Request([5]), SamplingParams(max_tokens=33))
+    np.testing.assert_equal(small_engine.is_finished(), True)

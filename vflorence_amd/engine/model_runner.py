@@ -1,0 +1,325 @@
+"""Per-step execution on one GPU: KV pools, encoder paging, step metadata, sampling.
+
+Counterpart of vflorence/engine/model_runner.py:22-442 with the same public surface
+(``run``, ``clear_request``, ``reset``, ``allocate_kv_cache``, ``_prepare``,
+``_encode``, ``_copy_blocks``, ``_sample``, ``_beam_search``) and bookkeeping (the
+encoder page pool and its free list, the per-batch cross-attention memo), laid out for
+the GPU:
+
+* every pool lives in HBM, one zero-filled tensor per layer and per K/V
+  (model_runner.py:62-77); a device table of the self-attention pools' addresses is
+  made once for the batched copy-on-write launch;
+* a step's metadata (token ids, positions, slots, copy pairs, lengths, dispatch
+  order, block tables) is packed on the host into one pinned buffer at fixed offsets
+  and sent with one asynchronous host->device copy; the Context holds views of the
+  device copy (model_runner.py:273-341);
+* the self-attention op receives a scheduler metadata that enables the fused KV write:
+  the block manager's copy-on-write rule guarantees each row writes its last context
+  position in a block no other row reads;
+* encoder K/V are projected on the device and scattered into pages with one
+  ``reshape_and_cache`` per layer (model_runner.py:208-259);
+* logits rules and top-k run on the device; only the chosen ids (greedy) or each
+  row's top-k (beam search) come back to the host.
+"""
+
+from __future__ import annotations
+
+import logging
+import math
+from collections import defaultdict
+
+import torch
+
+from .. import hip_attn
+from ..config import Config
+from ..layers import attention
+from ..layers.logits_processor import LogitsProcessor
+from ..sampling_params import SamplingParams
+from ..utils.context import set_context
+from ..utils.loader import load_model
+
+logger = logging.getLogger(__name__)
+
+
+class _StepBuffers:
+    """Pinned host staging and its device twin for one step's metadata.
+
+    int32 word layout for ``rows`` sequences and tables ``width`` blocks wide:
+    six int64 vectors of ``rows`` (token ids, positions, slots, copy sources, copy
+    destinations, lengths), then int32 context lengths, dispatch order and the
+    ``[rows, width]`` block tables.
+    """
+
+    I64 = ("input_ids", "positions", "slots", "copy_src", "copy_dst", "lengths")
+
+    def __init__(self, rows: int, width: int, device):
+        self.rows, self.width = rows, width
+        words = 12 * rows + 2 * rows + rows * width
+        self.host = torch.zeros(words, dtype=torch.int32, pin_memory=True)
+        self.dev = torch.zeros(words, dtype=torch.int32, device=device)
+        self.copied = torch.cuda.Event()
+        self.copied.record()
+        self.h = self._views(self.host)
+        self.d = self._views(self.dev)
+        self.np = {k: v.numpy() for k, v in self.h.items()}
+
+    def _views(self, buf):
+        r, w = self.rows, self.width
+        out = {name: buf[2 * r * i: 2 * r * (i + 1)].view(torch.int64)
+               for i, name in enumerate(self.I64)}
+        out["context_lens"] = buf[12 * r: 13 * r]
+        out["order"] = buf[13 * r: 14 * r]
+        out["tables"] = buf[14 * r: 14 * r + r * w].view(r, w)
+        return out
+
+    def upload(self) -> None:
+        self.dev.copy_(self.host, non_blocking=True)
+        self.copied.record()
+
+
+class ModelRunner:
+    def __init__(self, config: Config, state_dict: dict | None = None):
+        self.config = config
+        self.device = torch.device(config.device)
+        self.model = load_model(config, state_dict)
+        self.block_size = config.block_size
+        self.dtype = config.dtype
+        self.decoder_layers = list(self.model.decoder_layers)
+        self.num_heads = self.decoder_layers[0].self_attn.num_heads
+        self.head_dim = self.decoder_layers[0].self_attn.head_dim
+        if self.head_dim not in attention.HEAD_DIMS:
+            raise ValueError(f"no gfx950 kernel for head_dim={self.head_dim}; "
+                             f"must be one of {sorted(attention.HEAD_DIMS)}")
+        self.isa = hip_attn.get_isa(self.dtype, self.block_size, self.head_dim)
+        self.vocab_size = self.model.lm_head.out_features
+        self._cross_pages: dict[int, tuple[torch.Tensor, int]] = {}
+        self._cross_free = list(range(config.num_cross_blocks))
+        self._cross_key = None
+        self._cross_staged = None
+        self._logits_processor: LogitsProcessor | None = None
+        self._sampling_params: SamplingParams | None = None
+        self.allocate_kv_cache()
+        width = math.ceil(config.max_decoder_len / self.block_size) + 1
+        self._buffers = _StepBuffers(config.max_num_seqs, width, self.device)
+        self._query_start_loc = torch.arange(config.max_num_seqs + 1, dtype=torch.int32,
+                                             device=self.device)
+
+    # -- pools -------------------------------------------------------------------------
+
+    def allocate_kv_cache(self) -> None:
+        """Zero-filled pools in HBM, separate tensors per layer (model_runner.py:62-77)."""
+        cfg = self.config
+        shape = (cfg.num_blocks, self.num_heads, self.block_size, self.head_dim)
+        cross = (cfg.num_cross_blocks, *shape[1:])
+        for layer in self.decoder_layers:
+            layer.self_attn.k_cache = torch.zeros(shape, dtype=self.dtype, device=self.device)
+            layer.self_attn.v_cache = torch.zeros(shape, dtype=self.dtype, device=self.device)
+            layer.encoder_attn.k_cache = torch.zeros(cross, dtype=self.dtype, device=self.device)
+            layer.encoder_attn.v_cache = torch.zeros(cross, dtype=self.dtype, device=self.device)
+        self._self_caches = [c for layer in self.decoder_layers
+                             for c in (layer.self_attn.k_cache, layer.self_attn.v_cache)]
+        self._cache_ptrs = hip_attn.cache_pointer_table(self._self_caches)
+        mb = 1024**2
+        weights = sum(t.nbytes for t in (*self.model.parameters(), *self.model.buffers()))
+        kv = sum(c.nbytes for c in self._self_caches)
+        logger.info("Allocated in HBM: weights %.1f MB, self KV %.1f MB (%d blocks), cross KV "
+                    "%.1f MB (%d blocks)", weights / mb, kv / mb, cfg.num_blocks,
+                    2 * len(self.decoder_layers) * math.prod(cross) * self.model.lm_head.weight
+                    .element_size() / mb, cfg.num_cross_blocks)
+
+    def _copy_blocks(self, copies, src: torch.Tensor | None = None,
+                     dst: torch.Tensor | None = None) -> None:
+        """Copy-on-write of ``(src, dst)`` block pairs in every self-attention pool, one
+        launch (model_runner.py:162-167)."""
+        if not copies:
+            return
+        if src is None:
+            src = torch.tensor([s for s, _ in copies], dtype=torch.int64, device=self.device)
+            dst = torch.tensor([d for _, d in copies], dtype=torch.int64, device=self.device)
+        hip_attn.copy_blocks(self._self_caches, src, dst, self._cache_ptrs,
+                             staged=hip_attn.copy_pairs_need_staging(copies))
+
+    # -- encoder pages -----------------------------------------------------------------
+
+    def _allocate_cross_pages(self, num_pages: int) -> list[int]:
+        """Pages from the end of the encoder pool's free list (model_runner.py:169-177)."""
+        if num_pages > len(self._cross_free):
+            raise RuntimeError("encoder K/V pool is full; increase max_num_seqs or max_encoder_len")
+        pages = self._cross_free[-num_pages:]
+        del self._cross_free[-num_pages:]
+        return pages
+
+    def _encode(self, seqs) -> None:
+        """Encoder forward per group of equal prompt length, then page each layer's
+        cross-attention K/V (model_runner.py:208-259)."""
+        groups = defaultdict(list)
+        for seq in seqs:
+            if seq.pixel_values is not None:
+                raise ValueError("pixel_values are only supported for Florence-2 checkpoints")
+            groups[len(seq.encoder_token_ids)].append(seq)
+        bs = self.block_size
+        for enc_len, group in groups.items():
+            ids = torch.tensor([s.encoder_token_ids for s in group], dtype=torch.long)
+            hidden = self.model.encode(ids.to(self.device, non_blocking=True))
+            per_seq = math.ceil(enc_len / bs)
+            pages = torch.tensor(self._allocate_cross_pages(len(group) * per_seq),
+                                 dtype=torch.int32).view(len(group), per_seq)
+            token = torch.arange(enc_len)
+            slots = (pages[:, token // bs].long() * bs + token % bs).flatten()
+            for seq, seq_pages in zip(group, pages):
+                self._cross_pages[seq.request_id] = (seq_pages, enc_len)
+            slots = slots.to(self.device, non_blocking=True)
+            rows = len(group) * enc_len
+            for layer in self.decoder_layers:
+                attn = layer.encoder_attn
+                kv = attn.kv_proj(hidden).view(rows, 2 * attn.embed_dim)
+                key, value = (t.view(rows, attn.num_heads, attn.head_dim)
+                              for t in kv.chunk(2, dim=-1))
+                attention.reshape_and_cache(key, value, attn.k_cache, attn.v_cache, slots,
+                                            isa=self.isa)
+
+    def clear_request(self, request_id: int) -> None:
+        """Return a finished request's encoder pages; drop the staged cross state."""
+        pages, _ = self._cross_pages.pop(request_id, ((), 0))
+        self._cross_free.extend(int(p) for p in pages)
+        self._cross_key = self._cross_staged = None
+
+    def reset(self) -> None:
+        """Return every encoder page to the pool (after an aborted batch)."""
+        self._cross_pages.clear()
+        self._cross_free = list(range(self.config.num_cross_blocks))
+        self._cross_key = self._cross_staged = None
+
+    # -- step metadata -----------------------------------------------------------------
+
+    def _prepare(self, seqs, copies=()):
+        """Stage the step's metadata in HBM, run the copy-on-write, publish the Context.
+
+        Returns the device ``(input_ids, positions)`` of the one token fed per sequence.
+        """
+        bs = self.block_size
+        for seq in seqs:
+            num_new = len(seq.token_ids) - seq.num_cached_tokens
+            if num_new != 1:
+                raise ValueError(f"each step must feed 1 token per sequence, got {num_new}")
+        n = len(seqs)
+        buf = self._buffers
+        width = max(len(seq.block_table) for seq in seqs)
+        if n > buf.rows or width > buf.width or len(copies) > buf.rows:
+            buf = self._buffers = _StepBuffers(max(n, len(copies), buf.rows),
+                                               max(width, buf.width), self.device)
+        buf.copied.synchronize()  # the previous step's upload has left the staging
+        h = buf.np
+        positions = [seq.num_cached_tokens for seq in seqs]
+        h["input_ids"][:n] = [seq.token_ids[p] for seq, p in zip(seqs, positions)]
+        h["positions"][:n] = positions
+        h["slots"][:n] = [seq.block_table[p // bs] * bs + p % bs
+                          for seq, p in zip(seqs, positions)]
+        lens = [p + 1 for p in positions]
+        h["context_lens"][:n] = lens
+        h["order"][:n] = hip_attn.longest_first(lens)
+        tables = h["tables"]
+        for i, seq in enumerate(seqs):
+            tables[i, : len(seq.block_table)] = seq.block_table
+            tables[i, len(seq.block_table): width] = 0
+        if copies:
+            h["copy_src"][: len(copies)] = [s for s, _ in copies]
+            h["copy_dst"][: len(copies)] = [d for _, d in copies]
+        h["lengths"][:n] = [len(seq.token_ids) for seq in seqs]
+        buf.upload()
+        d = buf.d
+        # copy-on-write first: this step writes into the now-private blocks
+        self._copy_blocks(copies, d["copy_src"][: len(copies)], d["copy_dst"][: len(copies)])
+        self_metadata = hip_attn.get_scheduler_metadata(
+            num_reqs=n, num_heads=self.num_heads, num_kv_heads=self.num_heads,
+            head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
+            group_order=d["order"][:n], fuse_kv_write=True)
+        request_ids = tuple(seq.request_id for seq in seqs)
+        if request_ids != self._cross_key:
+            pages, enc_lens = zip(*(self._cross_pages[rid] for rid in request_ids))
+            self._cross_staged = attention.stage_cross(self.decoder_layers, pages, enc_lens, bs,
+                                                       self.isa)
+            self._cross_key = request_ids
+        set_context(
+            context_lens=d["context_lens"][:n],
+            block_tables=d["tables"][:n, :width],
+            slot_mapping=d["slots"][:n],
+            query_start_loc=self._query_start_loc[: n + 1],
+            self_metadata=self_metadata,
+            isa=self.isa,
+            cross_staged=self._cross_staged,
+        )
+        return d["input_ids"][:n], d["positions"][:n]
+
+    # -- sampling ----------------------------------------------------------------------
+
+    def _get_logits_processor(self, sampling_params: SamplingParams) -> LogitsProcessor:
+        if sampling_params != self._sampling_params or self._logits_processor is None:
+            # lengths count the decoder start token, as transformers does
+            self._logits_processor = LogitsProcessor(
+                sampling_params, vocab_size=self.vocab_size,
+                max_length=1 + sampling_params.max_tokens,
+                begin_index=1 + int(sampling_params.forced_bos_token_id is not None),
+                device=self.device)
+            self._sampling_params = sampling_params
+        return self._logits_processor
+
+    def _sample(self, seqs, logits, lengths: torch.Tensor | None = None):
+        """Greedy: one token id per sequence.  Beam search: ``{request_id: candidates}``
+        (model_runner.py:355-381)."""
+        sp = seqs[0].sampling_params
+        processor = self._get_logits_processor(sp)
+        device = logits.device
+        if lengths is None:
+            lengths = torch.tensor([len(s.token_ids) for s in seqs], dtype=torch.long,
+                                   device=device)
+        history = None
+        if processor.needs_history:
+            width = max(len(s.token_ids) for s in seqs)
+            history = torch.tensor([[-1] * (width - len(s.token_ids)) + s.token_ids
+                                    for s in seqs], dtype=torch.long).to(device)
+        scores = logits.float()
+        if sp.num_beams > 1:
+            scores = torch.log_softmax(scores, dim=-1)
+        scores = processor(history, scores, lengths)
+        if sp.num_beams == 1:
+            return scores.argmax(dim=-1).tolist()
+        return self._beam_search(seqs, scores, sp)
+
+    def _beam_search(self, seqs, scores, sampling_params) -> dict[int, list]:
+        """Each request's best ``max(2, 1 + n_eos) * num_beams`` continuations as
+        ``(parent, token_id, cum_logprob)``, best first (model_runner.py:383-410).
+
+        Per-row top-k runs on the device; only ``[rows, k]`` values and ids come back,
+        and the per-request merge keeps the reference's ordering (a stable sort of the
+        candidates listed row by row).
+        """
+        keep = max(2, 1 + len(sampling_params.eos_ids())) * sampling_params.num_beams
+        top_scores, top_ids = torch.topk(scores, min(keep, scores.shape[-1]), dim=-1)
+        top_scores = top_scores.float().cpu()
+        top_ids = top_ids.cpu()
+        top_scores += torch.tensor([s.cum_logprob for s in seqs], dtype=torch.float32).unsqueeze(-1)
+        candidates = defaultdict(list)
+        for seq, row_scores, row_ids in zip(seqs, top_scores.tolist(), top_ids.tolist()):
+            candidates[seq.request_id].extend(zip([seq] * len(row_ids), row_ids, row_scores))
+        for cands in candidates.values():
+            cands.sort(key=lambda c: c[2], reverse=True)
+            del cands[keep:]
+        return dict(candidates)
+
+    # -- step ----------------------------------------------------------------------------
+
+    @torch.inference_mode()
+    def run(self, seqs, copies=()):
+        """Encode fresh sequences, run one decoder step, return ``_sample``'s result."""
+        if not seqs:
+            return []
+        fresh = [seq for seq in seqs if seq.num_cached_tokens == 0]
+        if fresh:
+            self._encode(fresh)
+        try:
+            input_ids, positions = self._prepare(seqs, copies)
+            logits = self.model(input_ids, positions)
+        finally:
+            set_context()
+        return self._sample(seqs, logits, self._buffers.d["lengths"][: len(seqs)])

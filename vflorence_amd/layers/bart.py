@@ -1,0 +1,244 @@
+"""BART encoder-decoder whose decoder attention runs through the gfx950 paged ops.
+
+The callers of the path (vflorence/models/bart.py:93-146): the decoder's self-attention
+projects a fused q|k|v, views each third as ``[tokens, heads, head_dim]`` (strided
+views, token stride 3 * d_model) and hands them to ``vflorence::self_attention``, which
+writes k/v into this layer's paged pool and attends over the sequence's context; the
+cross-attention projects q only and calls ``vflorence::cross_attention``, which reads
+the encoder K/V that ``ModelRunner._encode`` paged once per request.  ``scaling`` is
+``head_dim ** -0.5`` (:52).
+
+Module and parameter names follow the transformers BART checkpoint layout
+(``model.encoder.layers.N.self_attn...``, ``lm_head``, ``final_logits_bias``) so a
+checkpoint's state dict loads after its q/k/v projections are concatenated
+(``fuse_projections``).  The encoder runs dense attention with torch's SDPA on the
+GPU: it is outside the decode path.  One decode step is ``forward(input_ids,
+positions)`` over one token per running sequence.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .attention import decoder_cross_attention, decoder_self_attention
+
+
+def _activation(name: str):
+    from transformers.activations import ACT2FN
+
+    return ACT2FN[name]
+
+
+class BartLearnedPositionalEmbedding(nn.Embedding):
+    """Learned positions with BART's offset of 2."""
+
+    OFFSET = 2
+
+    def __init__(self, num_embeddings: int, embedding_dim: int):
+        super().__init__(num_embeddings + self.OFFSET, embedding_dim)
+
+    def forward(self, positions: torch.Tensor) -> torch.Tensor:
+        return super().forward(positions + self.OFFSET)
+
+
+class BartScaledWordEmbedding(nn.Embedding):
+    def __init__(self, num_embeddings, embedding_dim, padding_idx, embed_scale=1.0):
+        super().__init__(num_embeddings, embedding_dim, padding_idx)
+        self.embed_scale = embed_scale
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        return super().forward(ids) * self.embed_scale
+
+
+class _Heads(nn.Module):
+    def __init__(self, embed_dim: int, num_heads: int):
+        super().__init__()
+        if embed_dim % num_heads:
+            raise ValueError("embed_dim must be divisible by num_heads")
+        self.embed_dim, self.num_heads = embed_dim, num_heads
+        self.head_dim = embed_dim // num_heads
+        self.scaling = self.head_dim**-0.5
+
+
+class BartEncoderSelfAttention(_Heads):
+    fused_projections = {"qkv_proj": ("q_proj", "k_proj", "v_proj")}
+
+    def __init__(self, embed_dim: int, num_heads: int):
+        super().__init__(embed_dim, num_heads)
+        self.qkv_proj = nn.Linear(embed_dim, 3 * embed_dim)
+        self.out_proj = nn.Linear(embed_dim, embed_dim)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        b, s, _ = x.shape
+        q, k, v = (t.view(b, s, self.num_heads, self.head_dim).transpose(1, 2)
+                   for t in self.qkv_proj(x).chunk(3, dim=-1))
+        out = F.scaled_dot_product_attention(q, k, v, scale=self.scaling)
+        return self.out_proj(out.transpose(1, 2).reshape(b, s, self.embed_dim))
+
+
+class BartDecoderSelfAttention(_Heads):
+    """One new token per running sequence; K/V go to the paged pool ``k_cache``/``v_cache``
+    that the runner attaches (never reallocated)."""
+
+    fused_projections = {"qkv_proj": ("q_proj", "k_proj", "v_proj")}
+
+    def __init__(self, embed_dim: int, num_heads: int):
+        super().__init__(embed_dim, num_heads)
+        self.qkv_proj = nn.Linear(embed_dim, 3 * embed_dim)
+        self.out_proj = nn.Linear(embed_dim, embed_dim)
+        self.k_cache = self.v_cache = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        n = x.shape[0]
+        q, k, v = (t.view(n, self.num_heads, self.head_dim)
+                   for t in self.qkv_proj(x).chunk(3, dim=-1))
+        out = decoder_self_attention(q, k, v, self.k_cache, self.v_cache, self.scaling)
+        return self.out_proj(out.view(n, self.embed_dim))
+
+
+class BartDecoderCrossAttention(_Heads):
+    """Queries only; the encoder K/V were paged by the runner (``kv_proj`` is used there)."""
+
+    fused_projections = {"kv_proj": ("k_proj", "v_proj")}
+
+    def __init__(self, embed_dim: int, num_heads: int, layer_idx: int):
+        super().__init__(embed_dim, num_heads)
+        self.q_proj = nn.Linear(embed_dim, embed_dim)
+        self.kv_proj = nn.Linear(embed_dim, 2 * embed_dim)
+        self.out_proj = nn.Linear(embed_dim, embed_dim)
+        self.layer_idx = layer_idx
+        self.k_cache = self.v_cache = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        n = x.shape[0]
+        q = self.q_proj(x).view(n, self.num_heads, self.head_dim)
+        out = decoder_cross_attention(q, self.layer_idx, self.scaling)
+        return self.out_proj(out.view(n, self.embed_dim))
+
+
+class BartEncoderLayer(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        d = config.d_model
+        self.self_attn = BartEncoderSelfAttention(d, config.encoder_attention_heads)
+        self.self_attn_layer_norm = nn.LayerNorm(d)
+        self.activation_fn = _activation(config.activation_function)
+        self.fc1 = nn.Linear(d, config.encoder_ffn_dim)
+        self.fc2 = nn.Linear(config.encoder_ffn_dim, d)
+        self.final_layer_norm = nn.LayerNorm(d)
+
+    def forward(self, h: torch.Tensor) -> torch.Tensor:
+        h = self.self_attn_layer_norm(h + self.self_attn(h))
+        return self.final_layer_norm(h + self.fc2(self.activation_fn(self.fc1(h))))
+
+
+class BartDecoderLayer(nn.Module):
+    def __init__(self, config, layer_idx: int):
+        super().__init__()
+        d, heads = config.d_model, config.decoder_attention_heads
+        self.self_attn = BartDecoderSelfAttention(d, heads)
+        self.self_attn_layer_norm = nn.LayerNorm(d)
+        self.encoder_attn = BartDecoderCrossAttention(d, heads, layer_idx)
+        self.encoder_attn_layer_norm = nn.LayerNorm(d)
+        self.activation_fn = _activation(config.activation_function)
+        self.fc1 = nn.Linear(d, config.decoder_ffn_dim)
+        self.fc2 = nn.Linear(config.decoder_ffn_dim, d)
+        self.final_layer_norm = nn.LayerNorm(d)
+
+    def forward(self, h: torch.Tensor) -> torch.Tensor:
+        h = self.self_attn_layer_norm(h + self.self_attn(h))
+        h = self.encoder_attn_layer_norm(h + self.encoder_attn(h))
+        return self.final_layer_norm(h + self.fc2(self.activation_fn(self.fc1(h))))
+
+
+def _embed_scale(config) -> float:
+    return math.sqrt(config.d_model) if config.scale_embedding else 1.0
+
+
+class BartEncoder(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        d = config.d_model
+        self.embed_tokens = BartScaledWordEmbedding(config.vocab_size, d, config.pad_token_id,
+                                                    _embed_scale(config))
+        self.embed_positions = BartLearnedPositionalEmbedding(config.max_position_embeddings, d)
+        self.layers = nn.ModuleList(BartEncoderLayer(config) for _ in range(config.encoder_layers))
+        self.layernorm_embedding = nn.LayerNorm(d)
+
+    def forward(self, input_ids, positions):
+        h = self.layernorm_embedding(self.embed_tokens(input_ids) + self.embed_positions(positions))
+        for layer in self.layers:
+            h = layer(h)
+        return h
+
+
+class BartDecoder(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        d = config.d_model
+        self.embed_tokens = BartScaledWordEmbedding(config.vocab_size, d, config.pad_token_id,
+                                                    _embed_scale(config))
+        self.embed_positions = BartLearnedPositionalEmbedding(config.max_position_embeddings, d)
+        self.layers = nn.ModuleList(BartDecoderLayer(config, i)
+                                    for i in range(config.decoder_layers))
+        self.layernorm_embedding = nn.LayerNorm(d)
+
+    def forward(self, input_ids, positions):
+        h = self.layernorm_embedding(self.embed_tokens(input_ids) + self.embed_positions(positions))
+        for layer in self.layers:
+            h = layer(h)
+        return h
+
+
+class BartModel(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        self.shared = BartScaledWordEmbedding(config.vocab_size, config.d_model,
+                                              config.pad_token_id, _embed_scale(config))
+        self.encoder = BartEncoder(config)
+        self.decoder = BartDecoder(config)
+        if config.tie_word_embeddings:
+            self.encoder.embed_tokens.weight = self.shared.weight
+            self.decoder.embed_tokens.weight = self.shared.weight
+
+
+class BartForConditionalGeneration(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        self.config = config
+        self.model = BartModel(config)
+        self.register_buffer("final_logits_bias", torch.zeros(1, config.vocab_size))
+        self.lm_head = nn.Linear(config.d_model, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.shared.weight
+
+    @property
+    def decoder_layers(self):
+        return self.model.decoder.layers
+
+    @torch.no_grad()
+    def encode(self, encoder_token_ids: torch.Tensor) -> torch.Tensor:
+        """Encoder hidden states [B, S, d_model] of equal-length prompts [B, S]."""
+        b, s = encoder_token_ids.shape
+        positions = torch.arange(s, device=encoder_token_ids.device).expand(b, s)
+        return self.model.encoder(encoder_token_ids, positions)
+
+    def forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        """One decode step: logits [N, vocab] for one token per running sequence."""
+        return self.lm_head(self.model.decoder(input_ids, positions)) + self.final_logits_bias
+
+
+def fuse_projections(model: nn.Module, state_dict: dict) -> None:
+    """Concatenate a checkpoint's separate projections (q/k/v_proj -> qkv_proj,
+    k/v_proj -> kv_proj) along the output dimension, in place."""
+    for prefix, module in model.named_modules():
+        for target, sources in getattr(module, "fused_projections", {}).items():
+            for suffix in ("weight", "bias"):
+                names = [f"{prefix}.{s}.{suffix}" for s in sources]
+                if all(n in state_dict for n in names):
+                    state_dict[f"{prefix}.{target}.{suffix}"] = torch.cat(
+                        [state_dict.pop(n) for n in names], dim=0)
