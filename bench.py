@@ -48,6 +48,8 @@ def parse_args():
     p.add_argument("--kernel-reps", type=int, default=20,
                    help="launches per layer when timing the dominant kernel")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-engine", action="store_true",
+                   help="skip the whole-engine decoder tokens/s measurement")
     p.add_argument("--counters", action="store_true",
                    help="counter-collection run for rocprofv3 --pmc: the dominant kernel's "
                         "launches and two copies of known size, nothing timed")
@@ -370,6 +372,56 @@ def measured_traffic(c_bytes: int):
     return int(t) if t is not None else None
 
 
+def engine_decode(torch, seed: int):
+    """Decoder tokens/s through the whole engine: BART-large (12+12 layers, d_model 1024,
+    vocab 50265, synthetic weights) in bf16, 64 requests x 4 beams with encoder prompts
+    of U[256, 1024] random token ids, 128 beam-search steps (EOS suppressed by
+    min_length, so every step runs 256 rows), decode steps replayed from HIP graphs.
+    Timed: the steps after the first two (encoder + first beam step + capture); each
+    step includes scheduling, metadata upload, copy-on-write, the decoder forward, the
+    logits rules, top-k and the beam bookkeeping."""
+    from transformers import BartConfig
+
+    from vflorence_amd import LLM, Request, SamplingParams
+
+    cfg = BartConfig(forced_eos_token_id=None)
+    llm = LLM(cfg, max_num_seqs=REQUESTS * BEAMS, dtype=torch.bfloat16,
+              max_decoder_len=DECODE_STEPS, max_encoder_len=MAX_ENC, cuda_graphs=True)
+    g = torch.Generator().manual_seed(seed + 101)
+    lens = torch.randint(ENC_MIN, ENC_MAX + 1, (REQUESTS,), generator=g).tolist()
+    params = SamplingParams(max_tokens=DECODE_STEPS, num_beams=BEAMS,
+                            min_length=DECODE_STEPS + 2, eos_token_id=[cfg.eos_token_id])
+    for n in lens:
+        llm.add_request(Request(torch.randint(3, cfg.vocab_size, (n,), generator=g).tolist()),
+                        params)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    llm.step()
+    llm.step()
+    torch.cuda.synchronize()
+    first = time.perf_counter() - t0
+    rows_done = steps = 0
+    t0 = time.perf_counter()
+    while not llm.is_finished():
+        rows_done += len(llm.scheduler.running)
+        llm.step()
+        steps += 1
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    del llm
+    torch.cuda.empty_cache()
+    return {
+        "model": "BART-large shapes, synthetic weights, bf16",
+        "requests": REQUESTS, "beams": BEAMS, "enc_len": f"U[{ENC_MIN},{ENC_MAX}]",
+        "timed_steps": steps,
+        "ms_per_step": round(el * 1e3 / steps, 3),
+        "decoded_rows_per_s": round(rows_done / el, 1),
+        "request_tokens_per_s": round(REQUESTS * steps / el, 1),
+        "first_two_steps_s": round(first, 3),
+        "hip_graphs": True,
+    }
+
+
 def cpu_baseline(torch, wl, budget_s: float):
     """The C restatement (oracle/, OpenMP, fp32 accumulation) on one decoder layer of the
     same workload: per sampled step, the CoW copy of that layer's two caches, the KV slot
@@ -492,6 +544,11 @@ def main():
 
     print("[bench] op-level self-attention, 256 ragged sequences", flush=True)
     k_avg, k_bytes, o_avg, o_bytes, _ = self_op_timing(torch, args.kernel_reps, args.seed)
+    torch.cuda.empty_cache()
+    decoder = None
+    if not args.no_engine:
+        print("[bench] engine decode: BART-large bf16, 64 requests x 4 beams", flush=True)
+        decoder = engine_decode(torch, args.seed)
 
     rows = REQUESTS * BEAMS
     result = {
@@ -553,6 +610,7 @@ def main():
                 "kernel_bytes": int(c_bytes),
             },
         },
+        "decoder_tokens": decoder,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

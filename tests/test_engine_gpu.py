@@ -45,11 +45,11 @@ def assert_clean(llm):
 SMALL_CASES = ["greedy", "greedy_rules", "greedy_forced", "beam2", "beam4_early", "beam4_rules"]
 
 
-@pytest.fixture(scope="module")
-def small_engine():
+@pytest.fixture(scope="module", params=[False, True], ids=["eager", "hipgraph"])
+def small_engine(request):
     fx = fixtures()["small"]
     return engine(fx["config"], fx["checksum"], max_num_seqs=24, dtype=torch.float32,
-                  max_decoder_len=32, max_encoder_len=128)
+                  max_decoder_len=32, max_encoder_len=128, cuda_graphs=request.param)
 
 
 @pytest.mark.parametrize("case", SMALL_CASES)
@@ -66,7 +66,8 @@ def test_tokens_match_transformers_small_bart(small_engine, case):
     assert_clean(small_engine)
 
 
-def test_tokens_match_transformers_bart_large_fp32():
+@pytest.mark.parametrize("graphs", [False, True], ids=["eager", "hipgraph"])
+def test_tokens_match_transformers_bart_large_fp32(graphs):
     """BART-large shapes (12+12 layers, 16 heads x 64, vocab 50265), fp32, 8 requests
     with encoder prompts of 128..1024 tokens, 64 greedy tokens each, batched."""
     from vflorence_amd import Request, SamplingParams
@@ -75,22 +76,32 @@ def test_tokens_match_transformers_bart_large_fp32():
     c = fx["cases"]["greedy64"]
     assert all(g > 1e-4 for g in c["min_gap"])
     llm = engine(fx["config"], fx["checksum"], max_num_seqs=8, dtype=torch.float32,
-                 max_decoder_len=64, max_encoder_len=1024)
+                 max_decoder_len=64, max_encoder_len=1024, cuda_graphs=graphs)
     outs = llm.generate([Request(p) for p in fx["prompts"]], SamplingParams(**c["params"]))
     assert [o.completion_token_ids for o in outs] == c["tokens"]
     assert_clean(llm)
 
 
-def test_bf16_engine_runs_beams_and_stays_clean(small_engine):
+def test_bf16_hip_graph_steps_equal_eager_steps():
+    """bf16 beam search: replayed decode steps give the same tokens as eager ones
+    (every replay reads fresh metadata from the fixed buffers)."""
     from vflorence_amd import Request, SamplingParams
 
     fx = fixtures()["small"]
-    llm = engine(fx["config"], fx["checksum"], max_num_seqs=24, dtype=torch.bfloat16,
-                 max_decoder_len=32, max_encoder_len=128)
     params = SamplingParams(**fx["cases"]["beam4_early"]["params"])
-    outs = llm.generate([Request(p) for p in fx["prompts"]], params)
-    assert all(1 <= len(o.completion_token_ids) <= params.max_tokens for o in outs)
-    assert_clean(llm)
+    got = []
+    for graphs in (False, True):
+        llm = engine(fx["config"], fx["checksum"], max_num_seqs=24, dtype=torch.bfloat16,
+                     max_decoder_len=32, max_encoder_len=128, cuda_graphs=graphs)
+        outs = llm.generate([Request(p) for p in fx["prompts"]], params)
+        assert all(1 <= len(o.completion_token_ids) <= params.max_tokens for o in outs)
+        assert_clean(llm)
+        # a second batch in a different composition reuses the captured sizes
+        outs2 = llm.generate([Request(p) for p in fx["prompts"][::-1]], params)
+        got.append(([o.completion_token_ids for o in outs], [o.completion_token_ids
+                                                            for o in outs2]))
+        assert_clean(llm)
+    assert got[0] == got[1]
 
 
 def test_prepare_and_encode_follow_the_reference_formulas(small_engine):
@@ -122,7 +133,10 @@ def test_prepare_and_encode_follow_the_reference_formulas(small_engine):
         assert ctx.context_lens.tolist() == [p + 1 for p in want_pos]
         assert ctx.slot_mapping.tolist() == [s.block_table[p // 16] * 16 + p % 16
                                              for s, p in zip(seqs, want_pos)]
-        width = max(len(s.block_table) for s in seqs)
+        # 0-padded rows at the runner's fixed table width (the kernels read only
+        # ceil(len / 16) entries of a row)
+        width = ctx.block_tables.shape[1]
+        assert width >= max(len(s.block_table) for s in seqs)
         assert ctx.block_tables.tolist() == [s.block_table + [0] * (width - len(s.block_table))
                                              for s in seqs]
         assert ctx.query_start_loc.tolist() == list(range(4))
@@ -153,10 +167,10 @@ def test_failed_step_releases_everything(small_engine):
     from vflorence_amd import Request, SamplingParams
 
     llm = small_engine
-    model = llm.runner.model
+    runner = llm.runner
     fx = fixtures()["small"]
     calls = []
-    original = model.forward
+    original = runner._sample
 
     def failing(*args):
         calls.append(1)
@@ -164,13 +178,13 @@ def test_failed_step_releases_everything(small_engine):
             raise RuntimeError("decode failed")
         return original(*args)
 
-    model.forward = failing
+    runner._sample = failing
     try:
         with pytest.raises(RuntimeError, match="decode failed"):
             llm.generate([Request(p) for p in fx["prompts"][:3]],
                          SamplingParams(max_tokens=8, num_beams=2))
     finally:
-        del model.forward
+        del runner._sample
     assert_clean(llm)
     from vflorence_amd.utils.context import get_context
 

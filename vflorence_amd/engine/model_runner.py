@@ -103,6 +103,11 @@ class ModelRunner:
         self._buffers = _StepBuffers(config.max_num_seqs, width, self.device)
         self._query_start_loc = torch.arange(config.max_num_seqs + 1, dtype=torch.int32,
                                              device=self.device)
+        self._cross_buffers = attention.CrossStagingBuffers(
+            config.max_num_seqs, math.ceil(config.max_encoder_len / self.block_size), self.device)
+        # decode steps captured per batch size (rows), replayed while the shapes repeat
+        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
 
     # -- pools -------------------------------------------------------------------------
 
@@ -208,6 +213,7 @@ class ModelRunner:
         if n > buf.rows or width > buf.width or len(copies) > buf.rows:
             buf = self._buffers = _StepBuffers(max(n, len(copies), buf.rows),
                                                max(width, buf.width), self.device)
+            self._graphs.clear()  # they read the old buffers
         buf.copied.synchronize()  # the previous step's upload has left the staging
         h = buf.np
         positions = [seq.num_cached_tokens for seq in seqs]
@@ -221,7 +227,7 @@ class ModelRunner:
         tables = h["tables"]
         for i, seq in enumerate(seqs):
             tables[i, : len(seq.block_table)] = seq.block_table
-            tables[i, len(seq.block_table): width] = 0
+            tables[i, len(seq.block_table):] = 0
         if copies:
             h["copy_src"][: len(copies)] = [s for s, _ in copies]
             h["copy_dst"][: len(copies)] = [d for _, d in copies]
@@ -238,11 +244,11 @@ class ModelRunner:
         if request_ids != self._cross_key:
             pages, enc_lens = zip(*(self._cross_pages[rid] for rid in request_ids))
             self._cross_staged = attention.stage_cross(self.decoder_layers, pages, enc_lens, bs,
-                                                       self.isa)
+                                                       self.isa, buffers=self._cross_buffers)
             self._cross_key = request_ids
         set_context(
             context_lens=d["context_lens"][:n],
-            block_tables=d["tables"][:n, :width],
+            block_tables=d["tables"][:n],
             slot_mapping=d["slots"][:n],
             query_start_loc=self._query_start_loc[: n + 1],
             self_metadata=self_metadata,
@@ -319,7 +325,35 @@ class ModelRunner:
             self._encode(fresh)
         try:
             input_ids, positions = self._prepare(seqs, copies)
-            logits = self.model(input_ids, positions)
+            logits = self._forward(input_ids, positions)
         finally:
             set_context()
         return self._sample(seqs, logits, self._buffers.d["lengths"][: len(seqs)])
+
+    def _forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        """The decoder step, eager or replayed from a HIP graph of this batch size.
+
+        Every tensor the step reads -- token ids, positions, the Context's lengths,
+        tables and slots, the cross-attention staging -- lives at a fixed address for a
+        given row count, and the launch shapes depend on the row count only, so one
+        capture per row count serves every later step of that size.  The first step of
+        a size runs eagerly (initialising libraries) before the capture; its KV write
+        repeats in the replay with the same values.
+        """
+        if not self.config.cuda_graphs:
+            return self.model(input_ids, positions)
+        n = input_ids.shape[0]
+        entry = self._graphs.get(n)
+        if entry is None:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                self.model(input_ids, positions)
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, pool=self._graph_pool):
+                logits = self.model(input_ids, positions)
+            entry = self._graphs[n] = (graph, logits)
+        graph, logits = entry
+        graph.replay()
+        return logits

@@ -112,6 +112,9 @@ class Scheduler:
                 for parent, child in live:
                     self.block_manager.fork(parent, child)
                     self.running.append(child)
+        # retire every parent: blocks freed in step order, one pass over ``running``
         for seq in seqs:
-            self.remove(seq)
+            self.block_manager.deallocate(seq)
+        retired = set(map(id, seqs))
+        self.running = [s for s in self.running if id(s) not in retired]
         return outputs

@@ -39,38 +39,98 @@ def beam_groups(pages, enc_lens, max_group: int = hip_attn.MAX_GROUP_SIZE) -> li
     return starts
 
 
-def stage_cross(layers, pages, enc_lens, block_size: int, isa: str):
+class CrossStagingBuffers:
+    """Fixed-address staging for ``stage_cross``: a pinned host buffer and its device
+    twin laid out for up to ``max_rows`` rows and ``max_pages`` pages per row.
+
+    int32 words: lengths [max_rows] | group starts [max_rows + 1] | dispatch order
+    [max_rows] | page table [max_rows, max_pages].  Every batch of n rows uses the
+    same addresses and launch shape (n groups, unused slots marked -1 in the order),
+    so a decode step captured in a HIP graph stays valid when the batch's requests,
+    and hence its beam groups and pages, change.
+    """
+
+    def __init__(self, max_rows: int, max_pages: int, device):
+        self.max_rows, self.max_pages = max_rows, max_pages
+        m = max_rows
+        words = 3 * m + 1 + m * max_pages
+        self.host = torch.zeros(words, dtype=torch.int32, pin_memory=True)
+        self.dev = torch.zeros(words, dtype=torch.int32, device=device)
+        self.copied = torch.cuda.Event()
+        self.copied.record()
+        self.np = self.host.numpy()
+        self.offsets = (0, m, 2 * m + 1, 3 * m + 1)
+
+    def views(self, n: int):
+        o = self.offsets
+        return (self.dev[o[0]: o[0] + n], self.dev[o[1]: o[1] + n + 1], self.dev[o[2]: o[2] + n],
+                self.dev[o[3]: o[3] + self.max_rows * self.max_pages]
+                .view(self.max_rows, self.max_pages)[:n])
+
+
+def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts):
+    n = len(pages)
+    if n > buffers.max_rows or max(len(p) for p in pages) > buffers.max_pages:
+        raise ValueError(f"{n} rows / {max(len(p) for p in pages)} pages exceed the staging "
+                         f"capacity ({buffers.max_rows} rows, {buffers.max_pages} pages)")
+    ng = len(starts) - 1
+    o, h = buffers.offsets, buffers.np
+    buffers.copied.synchronize()  # the previous upload has left the host buffer
+    h[o[0]: o[0] + n] = enc_lens
+    h[o[1]: o[1] + ng + 1] = starts
+    h[o[1] + ng + 1: o[1] + n + 1] = n  # empty groups past the last
+    order = hip_attn.longest_first([enc_lens[a] for a in starts[:-1]])
+    h[o[2]: o[2] + ng] = order
+    h[o[2] + ng: o[2] + n] = -1  # their workgroups exit at once
+    table = h[o[3]: o[3] + buffers.max_rows * buffers.max_pages].reshape(
+        buffers.max_rows, buffers.max_pages)
+    for i, p in enumerate(pages):
+        table[i, : len(p)] = p.numpy() if isinstance(p, torch.Tensor) else p
+        table[i, len(p):] = 0
+    buffers.dev.copy_(buffers.host, non_blocking=True)
+    buffers.copied.record()
+    return buffers.views(n)
+
+
+def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=None):
     """Point this step's sequences at their encoder K/V pages in each layer's pool.
 
     ``pages[i]`` (int32 tensor) and ``enc_lens[i]`` belong to running sequence i; beams
     of one request repeat its pages.  Nothing is copied: the padded block table,
     lengths and beam groups go to the device once and every layer shares them.
+    With ``buffers`` (a ``CrossStagingBuffers``) they go to its fixed addresses
+    instead of a fresh allocation, with one launch slot per row.
     """
     attn = layers[0].encoder_attn
     device = attn.k_cache.device
-    block_table = torch.nn.utils.rnn.pad_sequence(
-        [p.to(torch.int32).cpu() for p in pages], batch_first=True
-    )
     starts = beam_groups(pages, enc_lens)
     max_group = max(b - a for a, b in zip(starts, starts[1:]))
-    n, width, ng = len(pages), block_table.shape[1], len(starts) - 1
-    order = hip_attn.longest_first([enc_lens[a] for a in starts[:-1]])
-    # One host->device copy:
-    # [seq_lens (n) | group starts (ng + 1) | group order (ng) | block table (n * width)].
-    host = torch.cat(
-        [
-            torch.tensor(enc_lens, dtype=torch.int32),
-            torch.tensor(starts, dtype=torch.int32),
-            torch.tensor(order, dtype=torch.int32),
-            block_table.flatten(),
-        ]
-    )
-    dev = host.to(device)
-    seq_lens = dev[:n]
-    grouped = max_group > 1
-    group_start = dev[n : n + ng + 1] if grouped else None
-    group_order = dev[n + ng + 1 : n + 2 * ng + 1]
-    block_table = dev[n + 2 * ng + 1 :].view(n, width)
+    n, ng = len(pages), len(starts) - 1
+    if buffers is not None:
+        seq_lens, group_start, group_order, block_table = _stage_into(buffers, pages, enc_lens,
+                                                                      starts)
+        max_group = hip_attn.MAX_GROUP_SIZE  # one launch shape for every batch of n rows
+    else:
+        block_table = torch.nn.utils.rnn.pad_sequence(
+            [p.to(torch.int32).cpu() for p in pages], batch_first=True
+        )
+        width = block_table.shape[1]
+        order = hip_attn.longest_first([enc_lens[a] for a in starts[:-1]])
+        # One host->device copy:
+        # [seq_lens (n) | group starts (ng + 1) | group order (ng) | block table (n * width)].
+        host = torch.cat(
+            [
+                torch.tensor(enc_lens, dtype=torch.int32),
+                torch.tensor(starts, dtype=torch.int32),
+                torch.tensor(order, dtype=torch.int32),
+                block_table.flatten(),
+            ]
+        )
+        dev = host.to(device)
+        seq_lens = dev[:n]
+        group_start = dev[n : n + ng + 1] if max_group > 1 else None
+        group_order = dev[n + ng + 1 : n + 2 * ng + 1]
+        block_table = dev[n + 2 * ng + 1 :].view(n, width)
     metadata = hip_attn.get_scheduler_metadata(
         num_reqs=n,
         num_heads=attn.num_heads,
