@@ -207,3 +207,36 @@ def test_rejected_request_returns_empty_and_others_run(small_engine):
     with pytest.raises(ValueError):
         small_engine.add_request(Request([5]), SamplingParams(max_tokens=33))
     np.testing.assert_equal(small_engine.is_finished(), True)
+
+
+@pytest.mark.parametrize("graphs", [False, True], ids=["eager", "hipgraph"])
+def test_continuous_batching_keeps_each_requests_tokens(graphs):
+    """Requests arrive at seeded Poisson times and leave when done, so the batch (and its
+    cross-attention staging) changes from step to step; every completion still equals
+    transformers' output for its prompt alone."""
+    from vflorence_amd import Request, SamplingParams
+
+    fx = fixtures()["small"]
+    c = fx["cases"]["greedy"]
+    llm = engine(fx["config"], fx["checksum"], max_num_seqs=8, dtype=torch.float32,
+                 max_decoder_len=32, max_encoder_len=128, cuda_graphs=graphs)
+    rng = np.random.default_rng(0)
+    arrive = np.cumsum(rng.poisson(1.5, size=30)).tolist()
+    which = rng.integers(0, len(fx["prompts"]), size=30).tolist()
+    params = SamplingParams(**c["params"])
+    prompt_of, done, step = {}, {}, 0
+    pending = list(zip(arrive, which))
+    sizes = set()
+    while pending or not llm.is_finished():
+        while pending and pending[0][0] <= step:
+            _, i = pending.pop(0)
+            prompt_of[llm.add_request(Request(fx["prompts"][i]), params)] = i
+        if not llm.is_finished():
+            for rid, out in llm.step():
+                done[rid] = out.completion_token_ids
+            sizes.add(len(llm.scheduler.running))
+        step += 1
+    assert len(done) == 30 and len(sizes) > 3
+    for rid, tokens in done.items():
+        assert tokens == c["tokens"][prompt_of[rid]], rid
+    assert_clean(llm)
