@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import gc
 import json
 import math
 import os
@@ -395,19 +396,23 @@ def engine_decode(torch, seed: int):
         llm.add_request(Request(torch.randint(3, cfg.vocab_size, (n,), generator=g).tolist()),
                         params)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    llm.step()
-    llm.step()
-    torch.cuda.synchronize()
-    first = time.perf_counter() - t0
-    rows_done = steps = 0
-    t0 = time.perf_counter()
-    while not llm.is_finished():
-        rows_done += len(llm.scheduler.running)
+    gc.disable()  # as LLM.generate does around its step loop
+    try:
+        t0 = time.perf_counter()
         llm.step()
-        steps += 1
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
+        llm.step()
+        torch.cuda.synchronize()
+        first = time.perf_counter() - t0
+        rows_done = steps = 0
+        t0 = time.perf_counter()
+        while not llm.is_finished():
+            rows_done += len(llm.scheduler.running)
+            llm.step()
+            steps += 1
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+    finally:
+        gc.enable()
     del llm
     torch.cuda.empty_cache()
     return {

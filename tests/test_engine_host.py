@@ -3,11 +3,11 @@ beam-candidate selection, the scheduler's beam gate (the reference's known answe
 block-manager invariants, the synthetic checkpoint, and the BART encoder against
 transformers' (dense part only: the decoder's paged attention needs the GPU)."""
 
-import itertools
 import json
 import os
 from types import SimpleNamespace
 
+import numpy as np
 import pytest
 import torch
 
@@ -236,3 +236,38 @@ def test_encoder_matches_transformers():
         want = hf.model.encoder(input_ids=ids).last_hidden_state
         got = mine.encode(ids)
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_vectorised_beam_merge_equals_the_general_merge():
+    """Equal-size adjacent beam groups take the vectorised merge; it must list the same
+    candidates in the same order as the row-by-row stable sort, ties included."""
+    from vflorence_amd.engine import model_runner as mr
+
+    params = SamplingParams(num_beams=3, eos_token_id=[2]).with_defaults(defaults())
+    g = torch.Generator().manual_seed(3)
+    for rows_per_req, vocab in ((3, 40), (1, 40), (3, 4)):
+        seqs = [Sequence(r, [1], [3], params) for r in range(5) for _ in range(rows_per_req)]
+        for s in seqs:
+            s.cum_logprob = -float(torch.rand((), generator=g))
+        scores = torch.log_softmax(torch.randn(len(seqs), vocab, generator=g), dim=-1)
+        scores[:, 5:9] = -1.0  # exact ties inside and across rows
+        scores[1, :] = float("-inf")
+        keep = max(2, 1 + len(params.eos_ids())) * params.num_beams
+        top, ids = torch.topk(scores, min(keep, vocab), dim=-1)
+        top = top + torch.tensor([s.cum_logprob for s in seqs]).unsqueeze(-1)
+        fast = mr._merge_equal_beam_groups(seqs, top.numpy(), ids.numpy(), keep)
+        assert fast is not None
+        general = {}
+        for s, row_s, row_i in zip(seqs, top.tolist(), ids.tolist()):
+            general.setdefault(s.request_id, []).extend(zip([s] * len(row_i), row_i, row_s))
+        for c in general.values():
+            c.sort(key=lambda x: x[2], reverse=True)
+            del c[keep:]
+        assert fast == general
+    # unequal or interleaved groups are left to the general merge
+    seqs = [Sequence(r, [1], [3], params) for r in (0, 0, 1)]
+    assert mr._merge_equal_beam_groups(seqs, np.zeros((3, 2), np.float32),
+                                       np.zeros((3, 2), np.int64), 4) is None
+    seqs = [Sequence(r, [1], [3], params) for r in (0, 1, 0, 1)]
+    assert mr._merge_equal_beam_groups(seqs, np.zeros((4, 2), np.float32),
+                                       np.zeros((4, 2), np.int64), 4) is None

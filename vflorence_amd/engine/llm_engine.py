@@ -8,6 +8,7 @@ drops every request and returns all blocks and encoder pages.
 
 from __future__ import annotations
 
+import gc
 import logging
 import math
 from contextlib import contextmanager
@@ -88,10 +89,19 @@ class LLMEngine:
                 logger.error("request rejected: %s", e)
                 slots.append(RequestOut(request.input_ids, [], request.pixel_values))
         outputs: dict[int, RequestOut] = {}
-        with self._abort_on_failure():
-            while not self.is_finished():
-                for request_id, out in self.step():
-                    outputs[request_id] = out
+        # Every step allocates and drops one Sequence per running row; they hold no
+        # reference cycles, so reference counting frees them and the cyclic collector
+        # would only add pauses to the step loop.
+        collecting = gc.isenabled()
+        gc.disable()
+        try:
+            with self._abort_on_failure():
+                while not self.is_finished():
+                    for request_id, out in self.step():
+                        outputs[request_id] = out
+        finally:
+            if collecting:
+                gc.enable()
         return [outputs[s] if isinstance(s, int) else s for s in slots]
 
     def _validate(self, request: Request, sampling_params: SamplingParams) -> None:

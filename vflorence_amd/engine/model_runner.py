@@ -28,6 +28,7 @@ import logging
 import math
 from collections import defaultdict
 
+import numpy as np
 import torch
 
 from .. import hip_attn
@@ -75,6 +76,36 @@ class _StepBuffers:
     def upload(self) -> None:
         self.dev.copy_(self.host, non_blocking=True)
         self.copied.record()
+
+
+def _merge_equal_beam_groups(seqs, scores, ids, keep: int):
+    """The per-request candidate merge, vectorised for the usual beam-search batch: each
+    request's rows adjacent and every request with the same number of rows.  Returns
+    None for any other batch (the general merge handles it).
+
+    Equals sorting each request's candidates -- listed row by row, each row best first
+    -- by score, stably, best first: a stable ascending sort of the negated scores.
+    """
+    n, k = scores.shape
+    rids = [s.request_id for s in seqs]
+    nb = 1
+    while nb < n and rids[nb] == rids[0]:
+        nb += 1
+    if n % nb:
+        return None
+    heads = rids[::nb]
+    if len(set(heads)) != len(heads) or any(rids[i] != rids[i - i % nb] for i in range(n)):
+        return None
+    flat = scores.reshape(n // nb, nb * k)
+    order = np.argsort(-flat, axis=1, kind="stable")[:, :keep]
+    out = {}
+    for j, rid in enumerate(heads):
+        base = j * nb
+        sel = order[j].tolist()
+        vals = flat[j, order[j]].tolist()
+        out[rid] = [(seqs[base + f // k], int(ids[base + f // k, f % k]), v)
+                    for f, v in zip(sel, vals)]
+    return out
 
 
 class ModelRunner:
@@ -305,6 +336,9 @@ class ModelRunner:
         top_scores = top_scores.float().cpu()
         top_ids = top_ids.cpu()
         top_scores += torch.tensor([s.cum_logprob for s in seqs], dtype=torch.float32).unsqueeze(-1)
+        fast = _merge_equal_beam_groups(seqs, top_scores.numpy(), top_ids.numpy(), keep)
+        if fast is not None:
+            return fast
         candidates = defaultdict(list)
         for seq, row_scores, row_ids in zip(seqs, top_scores.tolist(), top_ids.tolist()):
             candidates[seq.request_id].extend(zip([seq] * len(row_ids), row_ids, row_scores))

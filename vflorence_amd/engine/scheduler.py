@@ -89,13 +89,15 @@ class Scheduler:
         for request_id, candidates in candidates_by_request.items():
             sp = candidates[0][0].sampling_params
             num_beams = sp.num_beams
+            eos, max_tokens = sp.eos_ids(), sp.max_tokens
             finished = self._finished_beams[request_id]
             live: list[tuple[Sequence, Sequence]] = []
             for rank, (parent, token, cum_logprob) in enumerate(candidates):
                 if rank >= num_beams and len(live) >= num_beams:
                     break
                 child = parent.fork(token, cum_logprob)
-                if child.is_finished:
+                # Sequence.is_finished, with the request's EOS set built once
+                if token in eos or child.num_generated >= max_tokens:
                     if rank < num_beams:
                         finished.append(child)
                 elif len(live) < num_beams:

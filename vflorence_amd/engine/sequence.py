@@ -51,8 +51,12 @@ class Sequence:
         self.token_ids.append(token_id)
 
     def fork(self, token_id: int, cum_logprob: float = 0.0) -> "Sequence":
-        """A child hypothesis extending this one by ``token_id`` (blocks not yet shared)."""
-        child = copy.copy(self)
+        """A child hypothesis extending this one by ``token_id`` (blocks not yet shared).
+
+        A shallow copy of every field (what ``copy.copy`` gives, without its generic
+        reduce protocol: beam search forks every running row each step)."""
+        child = Sequence.__new__(Sequence)
+        child.__dict__.update(self.__dict__)
         child.token_ids = [*self.token_ids, token_id]
         child.block_table = []
         child.cum_logprob = cum_logprob
