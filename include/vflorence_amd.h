@@ -1,5 +1,6 @@
 /*
- * vflorence_amd.h -- C ABI of the MI355X (gfx950) decode-step attention library.
+ * vflorence_amd.h -- C ABI of the MI355X (gfx950) decode-step attention library and the
+ * decoder-step kernels around it (residual + LayerNorm, log-softmax + rules + top-k).
  *
  * Every entry point takes plain device pointers, element strides and sizes, and a
  * hipStream_t passed as `void *` (NULL = the legacy default stream).  No entry point
@@ -197,6 +198,46 @@ int vfl_self_attention_with_kv_write(const void *query, int64_t query_stride_tok
 int vfl_copy_blocks(void *const *caches, int num_caches, const int64_t *src,
                     const int64_t *dst, int64_t num_pairs, int64_t block_bytes,
                     int64_t num_blocks, void *staging, void *stream);
+
+/*
+ * The decoder layer's residual + LayerNorm (vflorence/models/bart.py:192-201:
+ * `layer_norm(hidden + sublayer(hidden))`, torch ops in the reference, no
+ * vllm_cpu_attn counterpart):
+ *   out[r] = (s - mean(s)) / sqrt(var(s) + eps) * weight + bias,  s = x[r] + residual[r]
+ * with s rounded to the element type first (the stored sum of a separate add), the
+ * statistics (biased variance) in fp32.  Rows are `dim` contiguous elements at the
+ * given row strides (elements); dim a multiple of 4, at most 4096; rows and
+ * weight / bias aligned to 4 elements.  `out` may alias `x` or `residual`.
+ */
+int vfl_add_layer_norm(const void *x, int64_t x_stride, const void *residual,
+                       int64_t residual_stride, const void *weight, const void *bias, void *out,
+                       int64_t out_stride, int64_t rows, int dim, float eps, int dtype,
+                       void *stream);
+
+/*
+ * Replaces the device work of ModelRunner._sample / _beam_search
+ * (vflorence/engine/model_runner.py:355-398) and LogitsProcessor
+ * (vflorence/layers/logits_processor.py:24-51) for the rules that need no token
+ * history: per row r of `logits` ([rows][vocab], row stride in elements)
+ *   score(t) = log_softmax(logits[r])(t)          (log_softmax != 0; else logits[r][t])
+ * then, in the processors' order, with len = lengths[r]:
+ *   len < min_length            -> the EOS tokens score -inf
+ *   len == 1                    -> only the forced-BOS tokens remain, at score 0
+ *   len == max_length - 1       -> only the forced-EOS tokens remain, at score 0
+ *   always                      -> the suppressed tokens score -inf
+ *   len == begin_index          -> the begin-suppressed tokens score -inf
+ * and writes the k best (score, token) pairs, best first (ties: lower token first),
+ * to scores / ids ([rows][k]).  rule_tokens is a DEVICE int32 array holding, in order,
+ * n_eos EOS, n_suppress suppressed, n_begin begin-suppressed, n_bos forced-BOS and
+ * n_forced_eos forced-EOS token ids.  1 <= k <= 32; lengths may be NULL only without
+ * rule tokens.  Repetition penalty and n-gram bans (which read the history) are not
+ * covered: their callers apply them before, on the logits.
+ */
+int vfl_logprob_topk(const void *logits, int64_t row_stride, int64_t rows, int vocab, int dtype,
+                     const int64_t *lengths, const int32_t *rule_tokens, int min_length,
+                     int max_length, int begin_index, int n_eos, int n_suppress, int n_begin,
+                     int n_bos, int n_forced_eos, int log_softmax, int k, float *scores,
+                     int64_t *ids, void *stream);
 
 #ifdef __cplusplus
 }

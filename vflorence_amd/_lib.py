@@ -27,6 +27,8 @@ EXPORTED_SYMBOLS = (
     "vfl_attention_with_kv_cache",
     "vfl_self_attention_with_kv_write",
     "vfl_copy_blocks",
+    "vfl_add_layer_norm",
+    "vfl_logprob_topk",
 )
 
 
@@ -72,6 +74,15 @@ _SIGNATURES = {
     "vfl_copy_blocks": (
         ctypes.c_int,
         [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp],
+    ),
+    "vfl_add_layer_norm": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _f32, _i32, _vp],
+    ),
+    "vfl_logprob_topk": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+         _i32, _i32, _vp, _vp, _vp],
     ),
 }
 

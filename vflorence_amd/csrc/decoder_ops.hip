@@ -1,0 +1,465 @@
+// Decoder-step kernels around the attention path, for gfx950:
+//
+//   add_layer_norm_kernel  -- out = LayerNorm(x + residual) * weight + bias, one row per
+//                             workgroup; the sum is rounded to the element type first
+//                             (what a separate add kernel stores), statistics in fp32.
+//   logprob_topk_kernel    -- per row: log-softmax of the logits, the generation rules
+//                             (min length, forced BOS / EOS, suppressed tokens), and the
+//                             k best (score, token) pairs, best first; one read of the
+//                             logits.  With log_softmax off the scores are the processed
+//                             logits themselves (greedy decoding's argmax at k = 1).
+//
+// Both are bandwidth-bound streams over [rows, dim] / [rows, vocab] in HBM.
+#include <math.h>
+#include <stdio.h>
+
+#include "common.h"
+
+namespace vfl {
+
+// ---------------------------------------------------------------------------
+// block-wide sums (256 threads = 4 waves)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float block_sum(float v, float *lds4) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();  // lds4 may still be read from the previous call
+  if ((threadIdx.x & 63) == 0) lds4[wave] = v;
+  __syncthreads();
+  return lds4[0] + lds4[1] + lds4[2] + lds4[3];
+}
+
+template <int DT> __device__ __forceinline__ void load4(const typename Elem<DT>::T *p, float v[4]);
+template <> __device__ __forceinline__ void load4<VFL_FLOAT32>(const float *p, float v[4]) {
+  const float4 u = *reinterpret_cast<const float4 *>(p);
+  v[0] = u.x, v[1] = u.y, v[2] = u.z, v[3] = u.w;
+}
+template <> __device__ __forceinline__ void load4<VFL_BFLOAT16>(const uint16_t *p, float v[4]) {
+  const uint2 u = *reinterpret_cast<const uint2 *>(p);
+  v[0] = bf16lo(u.x), v[1] = bf16hi(u.x), v[2] = bf16lo(u.y), v[3] = bf16hi(u.y);
+}
+template <> __device__ __forceinline__ void load4<VFL_FLOAT16>(const uint16_t *p, float v[4]) {
+  const uint2 u = *reinterpret_cast<const uint2 *>(p);
+  const f16x2_t a = __builtin_bit_cast(f16x2_t, u.x), b = __builtin_bit_cast(f16x2_t, u.y);
+  v[0] = (float)a.x, v[1] = (float)a.y, v[2] = (float)b.x, v[3] = (float)b.y;
+}
+
+template <int DT> __device__ __forceinline__ void store4(typename Elem<DT>::T *p, const float v[4]);
+template <> __device__ __forceinline__ void store4<VFL_FLOAT32>(float *p, const float v[4]) {
+  *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <> __device__ __forceinline__ void store4<VFL_BFLOAT16>(uint16_t *p, const float v[4]) {
+  uint2 u;
+  u.x = f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16);
+  u.y = f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16);
+  *reinterpret_cast<uint2 *>(p) = u;
+}
+template <> __device__ __forceinline__ void store4<VFL_FLOAT16>(uint16_t *p, const float v[4]) {
+  uint2 u;
+  u.x = f32_to_f16(v[0]) | (f32_to_f16(v[1]) << 16);
+  u.y = f32_to_f16(v[2]) | (f32_to_f16(v[3]) << 16);
+  *reinterpret_cast<uint2 *>(p) = u;
+}
+
+// The value a kernel that stores `v` in the element type would leave behind.
+template <int DT> __device__ __forceinline__ float round_to_elem(float v);
+template <> __device__ __forceinline__ float round_to_elem<VFL_FLOAT32>(float v) { return v; }
+template <> __device__ __forceinline__ float round_to_elem<VFL_BFLOAT16>(float v) {
+  return __uint_as_float(f32_to_bf16(v) << 16);
+}
+template <> __device__ __forceinline__ float round_to_elem<VFL_FLOAT16>(float v) {
+  return (float)(_Float16)v;
+}
+
+// ---------------------------------------------------------------------------
+// residual add + LayerNorm
+// ---------------------------------------------------------------------------
+constexpr int LN_THREADS = 256;
+
+template <int DT, int NV>  // NV: 4-element vectors per thread (dim <= 1024 * NV)
+__global__ __launch_bounds__(LN_THREADS) void add_layer_norm_kernel(
+    const typename Elem<DT>::T *x, int64_t x_stride, const typename Elem<DT>::T *residual,
+    int64_t r_stride, const typename Elem<DT>::T *__restrict__ weight,
+    const typename Elem<DT>::T *__restrict__ bias, typename Elem<DT>::T *out, int64_t out_stride,
+    int dim, float eps) {
+  // out may alias x or residual: each thread reads its elements before the two
+  // workgroup reductions and writes the same elements after them.
+  __shared__ float lds4[4];
+  const int64_t row = blockIdx.x;
+  const int nvec = dim >> 2;
+  float v[NV][4];
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int vi = threadIdx.x + k * LN_THREADS;
+    if (vi < nvec) {
+      float a[4], b[4];
+      load4<DT>(x + row * x_stride + vi * 4, a);
+      load4<DT>(residual + row * r_stride + vi * 4, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[k][e] = round_to_elem<DT>(a[e] + b[e]);
+        sum += v[k][e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[k][e] = 0.f;
+    }
+  }
+  const float mean = block_sum(sum, lds4) / (float)dim;
+  float sq = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    if (threadIdx.x + k * LN_THREADS < nvec) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = v[k][e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  const float rstd = rsqrtf(block_sum(sq, lds4) / (float)dim + eps);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int vi = threadIdx.x + k * LN_THREADS;
+    if (vi < nvec) {
+      float w[4], b[4], o[4];
+      load4<DT>(weight + vi * 4, w);
+      load4<DT>(bias + vi * 4, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (v[k][e] - mean) * rstd * w[e] + b[e];
+      store4<DT>(out + row * out_stride + vi * 4, o);
+    }
+  }
+}
+
+template <int DT>
+static int launch_add_layer_norm(const void *x, int64_t xs, const void *r, int64_t rs,
+                                 const void *w, const void *b, void *out, int64_t os, int64_t rows,
+                                 int dim, float eps, hipStream_t stream) {
+  using T = typename Elem<DT>::T;
+  const int nvec = dim / 4;
+  const dim3 grid((unsigned)rows), block(LN_THREADS);
+#define VFL_LN(NV)                                                                             \
+  add_layer_norm_kernel<DT, NV><<<grid, block, 0, stream>>>(                                   \
+      (const T *)x, xs, (const T *)r, rs, (const T *)w, (const T *)b, (T *)out, os, dim, eps)
+  if (nvec <= LN_THREADS)
+    VFL_LN(1);
+  else if (nvec <= 2 * LN_THREADS)
+    VFL_LN(2);
+  else
+    VFL_LN(4);
+#undef VFL_LN
+  return launch_status("add_layer_norm");
+}
+
+// ---------------------------------------------------------------------------
+// log-softmax + generation rules + per-row top-k
+// ---------------------------------------------------------------------------
+constexpr int TK_THREADS = 256;
+constexpr int TK_MAX_RULE_TOKENS = 256;
+
+// (score, token) order: higher score first, then lower token id, then lower lane.
+__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
+  return a > b || (a == b && ia < ib);
+}
+
+// Insert (v, t) into a descending list of K entries if it beats the last one.
+template <int K> __device__ __forceinline__ void insert(float (&val)[K], int (&tok)[K], float v, int t) {
+  if (!better(v, t, val[K - 1], tok[K - 1])) return;
+  val[K - 1] = v, tok[K - 1] = t;
+#pragma unroll
+  for (int j = K - 1; j > 0; --j) {
+    if (better(val[j], tok[j], val[j - 1], tok[j - 1])) {
+      const float fv = val[j];
+      val[j] = val[j - 1], val[j - 1] = fv;
+      const int ft = tok[j];
+      tok[j] = tok[j - 1], tok[j - 1] = ft;
+    }
+  }
+}
+
+// Pop the head of a descending list (the tail refills with an empty entry).
+template <int K> __device__ __forceinline__ void pop_head(float (&val)[K], int (&tok)[K]) {
+#pragma unroll
+  for (int j = 0; j + 1 < K; ++j) val[j] = val[j + 1], tok[j] = tok[j + 1];
+  val[K - 1] = -INFINITY, tok[K - 1] = INT32_MAX;
+}
+
+// Wave-wide best (score, token) among every lane's head; ties by lane.
+__device__ __forceinline__ void wave_best(float v, int t, float &bv, int &bt, int &blane) {
+  int lane = threadIdx.x & 63;
+  bv = v, bt = t, blane = lane;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int ot = __shfl_xor(bt, o, 64), ol = __shfl_xor(blane, o, 64);
+    if (better(ov, ot, bv, bt) || (ov == bv && ot == bt && ol < blane)) bv = ov, bt = ot, blane = ol;
+  }
+}
+
+struct TopkRules {
+  int32_t min_length, max_length, begin_index;
+  int32_t n_eos, n_suppress, n_begin, n_bos, n_feos;
+};
+
+__device__ __forceinline__ bool in_list(const int *list, int n, int t) {
+  for (int i = 0; i < n; ++i)
+    if (list[i] == t) return true;
+  return false;
+}
+
+template <int DT, int K>
+__global__ __launch_bounds__(TK_THREADS) void logprob_topk_kernel(
+    const typename Elem<DT>::T *__restrict__ logits, int64_t stride, int vocab,
+    const int64_t *__restrict__ lengths, const int32_t *__restrict__ rule_tokens, TopkRules rules,
+    int log_softmax, int k_out, float *__restrict__ out_scores, int64_t *__restrict__ out_ids) {
+  using T = typename Elem<DT>::T;
+  __shared__ int s_ban[TK_MAX_RULE_TOKENS];
+  __shared__ int s_force[TK_MAX_RULE_TOKENS];
+  __shared__ float s_val[4][K];
+  __shared__ int s_tok[4][K];
+  __shared__ float s_m[4], s_s[4];
+  __shared__ int s_nban, s_nforce;
+
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const T *x = logits + row * stride;
+
+  // The row's active rules, in the processors' order: min-length bans EOS; forced BOS
+  // (length 1) and forced EOS (length max_length - 1) replace every score; suppressed
+  // tokens and, at begin_index, the begin-suppressed tokens are banned afterwards.
+  if (threadIdx.x == 0) {
+    const int64_t len = lengths ? lengths[row] : 0;
+    const int *eos = rule_tokens, *sup = eos + rules.n_eos, *beg = sup + rules.n_suppress;
+    const int *bos = beg + rules.n_begin, *feos = bos + rules.n_bos;
+    int nf = 0, nb = 0;
+    if (rules.n_feos && len == rules.max_length - 1) {
+      for (int i = 0; i < rules.n_feos; ++i) s_force[nf++] = feos[i];
+    } else if (rules.n_bos && len == 1) {
+      for (int i = 0; i < rules.n_bos; ++i) s_force[nf++] = bos[i];
+    }
+    if (nf == 0 && len < rules.min_length)
+      for (int i = 0; i < rules.n_eos; ++i) s_ban[nb++] = eos[i];
+    for (int i = 0; i < rules.n_suppress; ++i) s_ban[nb++] = sup[i];
+    if (len == rules.begin_index)
+      for (int i = 0; i < rules.n_begin; ++i) s_ban[nb++] = beg[i];
+    s_nban = nb, s_nforce = nf;
+  }
+  __syncthreads();
+  const int nban = s_nban, nforce = s_nforce;
+
+  float val[K];
+  int tok[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) val[j] = -INFINITY, tok[j] = INT32_MAX;
+  // running max / sum of exp for the log-softmax normaliser (every token counts)
+  float m = -INFINITY, s = 0.f;
+
+  for (int t = threadIdx.x; t < vocab; t += TK_THREADS) {
+    const float xv = [&] {
+      if constexpr (DT == VFL_FLOAT32) return x[t];
+      else if constexpr (DT == VFL_BFLOAT16) return __uint_as_float((uint32_t)x[t] << 16);
+      else return (float)__builtin_bit_cast(_Float16, x[t]);
+    }();
+    if (log_softmax) {
+      if (xv > m) {
+        s = s * expf(m - xv) + 1.f;
+        m = xv;
+      } else if (xv != -INFINITY) {
+        s += expf(xv - m);
+      }
+    }
+    if (nforce) {
+      const float v = (in_list(s_force, nforce, t) && !in_list(s_ban, nban, t)) ? 0.f : -INFINITY;
+      insert<K>(val, tok, v, t);
+    } else if (better(xv, t, val[K - 1], tok[K - 1])) {
+      insert<K>(val, tok, in_list(s_ban, nban, t) ? -INFINITY : xv, t);
+    }
+  }
+
+  // normaliser: max and sum over the workgroup
+  float lse = 0.f;
+  if (log_softmax) {
+    float wm = m;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o, 64));
+    float ws = (m == -INFINITY) ? 0.f : s * expf(m - wm);
+    ws = wave_sum(ws);
+    if (lane == 0) s_m[wave] = wm, s_s[wave] = ws;
+  }
+
+  // each wave's K best, then the workgroup's
+  for (int r = 0; r < K; ++r) {
+    float bv;
+    int bt, bl;
+    wave_best(val[0], tok[0], bv, bt, bl);
+    if (lane == bl) pop_head<K>(val, tok);
+    if (lane == 0) s_val[wave][r] = bv, s_tok[wave][r] = bt;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float mx = 0.f;
+  if (log_softmax) {
+    mx = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    float tot = 0.f;
+    for (int w = 0; w < 4; ++w)
+      if (s_m[w] != -INFINITY) tot += s_s[w] * expf(s_m[w] - mx);
+    lse = logf(tot);
+  }
+  // lane l holds candidates l and l + 64 of the 4K (each wave's list is sorted)
+  float cv[2];
+  int ct[2];
+  for (int i = 0; i < 2; ++i) {
+    const int c = lane + 64 * i;
+    cv[i] = c < 4 * K ? s_val[c / K][c % K] : -INFINITY;
+    ct[i] = c < 4 * K ? s_tok[c / K][c % K] : INT32_MAX;
+  }
+  if (better(cv[1], ct[1], cv[0], ct[0])) {
+    const float fv = cv[0];
+    cv[0] = cv[1], cv[1] = fv;
+    const int ft = ct[0];
+    ct[0] = ct[1], ct[1] = ft;
+  }
+  for (int r = 0; r < k_out; ++r) {
+    float bv;
+    int bt, bl;
+    wave_best(cv[0], ct[0], bv, bt, bl);
+    if (lane == bl) cv[0] = cv[1], ct[0] = ct[1], cv[1] = -INFINITY, ct[1] = INT32_MAX;
+    if (lane == 0) {
+      // processed log-prob: (x - max) - log(sum exp(x - max)); forced tokens score 0
+      float outv = bv;
+      if (log_softmax && !nforce && bv != -INFINITY) outv = (bv - mx) - lse;
+      out_scores[row * k_out + r] = outv;
+      out_ids[row * k_out + r] = bt;
+    }
+  }
+}
+
+template <int DT>
+static int launch_topk(const void *logits, int64_t stride, int64_t rows, int vocab,
+                       const int64_t *lengths, const int32_t *rule_tokens, const TopkRules &rules,
+                       int log_softmax, int k, float *scores, int64_t *ids, hipStream_t stream) {
+  using T = typename Elem<DT>::T;
+  const dim3 grid((unsigned)rows), block(TK_THREADS);
+#define VFL_TK(KK)                                                                             \
+  logprob_topk_kernel<DT, KK><<<grid, block, 0, stream>>>((const T *)logits, stride, vocab,    \
+                                                          lengths, rule_tokens, rules,         \
+                                                          log_softmax, k, scores, ids)
+  if (k <= 1)
+    VFL_TK(1);
+  else if (k <= 8)
+    VFL_TK(8);
+  else if (k <= 16)
+    VFL_TK(16);
+  else
+    VFL_TK(32);
+#undef VFL_TK
+  return launch_status("logprob_topk");
+}
+
+}  // namespace vfl
+
+using namespace vfl;
+
+static bool aligned(const void *p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
+
+extern "C" int vfl_add_layer_norm(const void *x, int64_t x_stride, const void *residual,
+                                  int64_t residual_stride, const void *weight, const void *bias,
+                                  void *out, int64_t out_stride, int64_t rows, int dim, float eps,
+                                  int dtype, void *stream) {
+  clear_error();
+  if (dtype != VFL_FLOAT32 && dtype != VFL_BFLOAT16 && dtype != VFL_FLOAT16) {
+    set_error("add_layer_norm: unsupported dtype code %d", dtype);
+    return VFL_E_INVALID;
+  }
+  if (rows < 0 || rows > 2147483647LL || dim <= 0 || dim % 4 || dim > 4096) {
+    set_error("add_layer_norm: dim %d must be a positive multiple of 4 up to 4096 (rows %lld)",
+              dim, (long long)rows);
+    return VFL_E_INVALID;
+  }
+  if (!x || !residual || !weight || !bias || !out) {
+    set_error("add_layer_norm: null pointer argument");
+    return VFL_E_INVALID;
+  }
+  const int vb = 4 * elem_bytes(dtype);
+  if (x_stride % 4 || residual_stride % 4 || out_stride % 4 || !aligned(x, vb) ||
+      !aligned(residual, vb) || !aligned(weight, vb) || !aligned(bias, vb) || !aligned(out, vb) ||
+      x_stride < dim || residual_stride < dim || out_stride < dim) {
+    set_error("add_layer_norm: rows must be %d-byte aligned with strides that are multiples of 4 "
+              "elements and at least dim",
+              vb);
+    return VFL_E_INVALID;
+  }
+  if (rows == 0) return VFL_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == VFL_FLOAT32)
+    return launch_add_layer_norm<VFL_FLOAT32>(x, x_stride, residual, residual_stride, weight, bias,
+                                              out, out_stride, rows, dim, eps, s);
+  if (dtype == VFL_BFLOAT16)
+    return launch_add_layer_norm<VFL_BFLOAT16>(x, x_stride, residual, residual_stride, weight,
+                                               bias, out, out_stride, rows, dim, eps, s);
+  return launch_add_layer_norm<VFL_FLOAT16>(x, x_stride, residual, residual_stride, weight, bias,
+                                            out, out_stride, rows, dim, eps, s);
+}
+
+extern "C" int vfl_logprob_topk(const void *logits, int64_t row_stride, int64_t rows, int vocab,
+                                int dtype, const int64_t *lengths, const int32_t *rule_tokens,
+                                int min_length, int max_length, int begin_index, int n_eos,
+                                int n_suppress, int n_begin, int n_bos, int n_forced_eos,
+                                int log_softmax, int k, float *scores, int64_t *ids,
+                                void *stream) {
+  clear_error();
+  if (dtype != VFL_FLOAT32 && dtype != VFL_BFLOAT16 && dtype != VFL_FLOAT16) {
+    set_error("logprob_topk: unsupported dtype code %d", dtype);
+    return VFL_E_INVALID;
+  }
+  if (rows < 0 || rows > 2147483647LL || vocab <= 0 || row_stride < vocab || k < 1 || k > 32 ||
+      k > vocab) {
+    set_error("logprob_topk: need 1 <= k <= min(32, vocab) and row_stride >= vocab (k %d, vocab "
+              "%d, stride %lld)",
+              k, vocab, (long long)row_stride);
+    return VFL_E_INVALID;
+  }
+  const int counts[5] = {n_eos, n_suppress, n_begin, n_bos, n_forced_eos};
+  int total = 0;
+  for (int c : counts) {
+    if (c < 0) {
+      set_error("logprob_topk: negative rule-token count");
+      return VFL_E_INVALID;
+    }
+    total += c;
+  }
+  if (n_eos + n_suppress + n_begin > TK_MAX_RULE_TOKENS || n_bos > TK_MAX_RULE_TOKENS ||
+      n_forced_eos > TK_MAX_RULE_TOKENS) {
+    set_error("logprob_topk: at most %d banned and %d forced tokens", TK_MAX_RULE_TOKENS,
+              TK_MAX_RULE_TOKENS);
+    return VFL_E_INVALID;
+  }
+  if (!logits || !scores || !ids || (total && !rule_tokens)) {
+    set_error("logprob_topk: null pointer argument");
+    return VFL_E_INVALID;
+  }
+  if (!lengths && total) {
+    set_error("logprob_topk: the rules need per-row lengths");
+    return VFL_E_INVALID;
+  }
+  if (rows == 0) return VFL_OK;
+  TopkRules r{min_length, max_length, begin_index, n_eos, n_suppress, n_begin, n_bos,
+              n_forced_eos};
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == VFL_FLOAT32)
+    return launch_topk<VFL_FLOAT32>(logits, row_stride, rows, vocab, lengths, rule_tokens, r,
+                                    log_softmax, k, scores, ids, s);
+  if (dtype == VFL_BFLOAT16)
+    return launch_topk<VFL_BFLOAT16>(logits, row_stride, rows, vocab, lengths, rule_tokens, r,
+                                     log_softmax, k, scores, ids, s);
+  return launch_topk<VFL_FLOAT16>(logits, row_stride, rows, vocab, lengths, rule_tokens, r,
+                                  log_softmax, k, scores, ids, s);
+}

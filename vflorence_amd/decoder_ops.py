@@ -1,0 +1,89 @@
+"""torch wrappers of the decoder-step kernels around the attention path.
+
+``add_layer_norm`` is the decoder layer's ``layer_norm(hidden + sublayer(hidden))``
+(vflorence/models/bart.py:192-201) in one launch, registered as the custom op
+``vflorence_amd::add_layer_norm`` so a compiled decoder keeps it whole.
+``logprob_topk`` is the device half of sampling (vflorence/engine/model_runner.py:355-398):
+log-softmax, the history-free generation rules and the per-row top-k in one read of
+the logits.  Both run on the current stream; CPU tensors are rejected.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, lib
+from .hip_attn import _dtype_code, _require_gpu, _stream
+
+
+@torch.library.custom_op("vflorence_amd::add_layer_norm", mutates_args=())
+def add_layer_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                   bias: torch.Tensor, eps: float) -> torch.Tensor:
+    """``LayerNorm(x + residual) * weight + bias`` over the last dimension."""
+    dev = _require_gpu(x, residual, weight, bias)
+    dim = x.shape[-1]
+    if residual.shape != x.shape or weight.shape != (dim,) or bias.shape != (dim,):
+        raise ValueError("add_layer_norm: x and residual must match; weight / bias are [dim]")
+    if len({x.dtype, residual.dtype, weight.dtype, bias.dtype}) != 1:
+        raise ValueError("add_layer_norm: all tensors must share one dtype")
+    x2 = x.reshape(-1, dim)
+    r2 = residual.reshape(-1, dim)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    if r2.stride(-1) != 1:
+        r2 = r2.contiguous()
+    out = torch.empty(x2.shape, dtype=x.dtype, device=dev)
+    check(lib.vfl_add_layer_norm(x2.data_ptr(), x2.stride(0), r2.data_ptr(), r2.stride(0),
+                                 weight.contiguous().data_ptr(), bias.contiguous().data_ptr(),
+                                 out.data_ptr(), out.stride(0), x2.shape[0], dim, eps,
+                                 _dtype_code(x.dtype), _stream(dev)))
+    return out.view(x.shape)
+
+
+@add_layer_norm.register_fake
+def _(x, residual, weight, bias, eps):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+class TopkRules:
+    """The history-free generation rules of one SamplingParams, packed for the kernel:
+    a device int32 array ``[eos | suppressed | begin-suppressed | forced BOS | forced EOS]``
+    and the length thresholds (see LogitsProcessor for their meaning)."""
+
+    def __init__(self, *, eos, suppress, begin_suppress, forced_bos, forced_eos, min_length: int,
+                 max_length: int, begin_index: int, device):
+        lists = [list(t) for t in (eos, suppress, begin_suppress, forced_bos, forced_eos)]
+        self.counts = [len(t) for t in lists]
+        flat = [t for lst in lists for t in lst]
+        self.tokens = (torch.tensor(flat, dtype=torch.int32, device=device) if flat else None)
+        self.min_length = min_length if lists[0] else 0
+        self.max_length, self.begin_index = max_length, begin_index
+
+
+def logprob_topk(logits: torch.Tensor, k: int, *, log_softmax: bool,
+                 lengths: torch.Tensor | None = None, rules: TopkRules | None = None):
+    """Per row: (log-softmax), generation rules, and the k best scores with their token
+    ids, best first (ties: lower token id).  Returns (float32 [rows, k], int64 [rows, k])."""
+    dev = _require_gpu(logits)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [rows, vocab] with contiguous rows")
+    rows, vocab = logits.shape
+    if not 1 <= k <= min(32, vocab):
+        raise ValueError(f"k must be in [1, min(32, vocab)], got {k}")
+    counts = rules.counts if rules is not None else [0] * 5
+    tokens = rules.tokens if rules is not None else None
+    if sum(counts) and lengths is None:
+        raise ValueError("the rules need per-row lengths")
+    if lengths is not None and (lengths.dtype != torch.int64 or lengths.shape != (rows,)):
+        raise ValueError("lengths must be int64 [rows]")
+    scores = torch.empty(rows, k, dtype=torch.float32, device=dev)
+    ids = torch.empty(rows, k, dtype=torch.int64, device=dev)
+    check(lib.vfl_logprob_topk(
+        logits.data_ptr(), logits.stride(0), rows, vocab, _dtype_code(logits.dtype),
+        None if lengths is None else lengths.data_ptr(),
+        None if tokens is None else tokens.data_ptr(),
+        rules.min_length if rules else 0, rules.max_length if rules else 0,
+        rules.begin_index if rules else -1, *counts, int(log_softmax), k, scores.data_ptr(),
+        ids.data_ptr(), _stream(dev)))
+    return scores, ids
+

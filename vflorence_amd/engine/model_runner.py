@@ -31,7 +31,7 @@ from collections import defaultdict
 import numpy as np
 import torch
 
-from .. import hip_attn
+from .. import decoder_ops, hip_attn
 from ..config import Config
 from ..layers import attention
 from ..layers.logits_processor import LogitsProcessor
@@ -315,6 +315,17 @@ class ModelRunner:
             width = max(len(s.token_ids) for s in seqs)
             history = torch.tensor([[-1] * (width - len(s.token_ids)) + s.token_ids
                                     for s in seqs], dtype=torch.long).to(device)
+        rules = processor.topk_rules() if logits.is_cuda else None
+        keep = max(2, 1 + len(sp.eos_ids())) * sp.num_beams
+        if rules is not None and (sp.num_beams == 1 or keep <= 32):
+            # one kernel: log-softmax (beam search), the rules, the per-row top-k
+            if sp.num_beams == 1:
+                _, ids = decoder_ops.logprob_topk(logits, 1, log_softmax=False, lengths=lengths,
+                                                  rules=rules)
+                return ids[:, 0].tolist()
+            top, ids = decoder_ops.logprob_topk(logits, min(keep, logits.shape[-1]),
+                                                log_softmax=True, lengths=lengths, rules=rules)
+            return self._merge_candidates(seqs, top, ids, keep)
         scores = logits.float()
         if sp.num_beams > 1:
             scores = torch.log_softmax(scores, dim=-1)
@@ -333,6 +344,12 @@ class ModelRunner:
         """
         keep = max(2, 1 + len(sampling_params.eos_ids())) * sampling_params.num_beams
         top_scores, top_ids = torch.topk(scores, min(keep, scores.shape[-1]), dim=-1)
+        return ModelRunner._merge_candidates(seqs, top_scores, top_ids, keep)
+
+    @staticmethod
+    def _merge_candidates(seqs, top_scores, top_ids, keep: int) -> dict[int, list]:
+        """Add each row's cumulative log-prob to its top-k and keep every request's best
+        ``keep`` candidates over its rows, best first."""
         top_scores = top_scores.float().cpu()
         top_ids = top_ids.cpu()
         top_scores += torch.tensor([s.cum_logprob for s in seqs], dtype=torch.float32).unsqueeze(-1)

@@ -27,6 +27,16 @@ from torch import nn
 from .attention import decoder_cross_attention, decoder_self_attention
 
 
+def _residual_norm(h: torch.Tensor, y: torch.Tensor, norm: nn.LayerNorm) -> torch.Tensor:
+    """``norm(h + y)``: one fused kernel on the GPU (vflorence_amd::add_layer_norm);
+    torch's ops for host tensors (the encoder-only checks on the CPU)."""
+    if h.is_cuda:
+        from ..decoder_ops import add_layer_norm
+
+        return add_layer_norm(y, h, norm.weight, norm.bias, norm.eps)
+    return norm(h + y)
+
+
 def _activation(name: str):
     from transformers.activations import ACT2FN
 
@@ -132,8 +142,8 @@ class BartEncoderLayer(nn.Module):
         self.final_layer_norm = nn.LayerNorm(d)
 
     def forward(self, h: torch.Tensor) -> torch.Tensor:
-        h = self.self_attn_layer_norm(h + self.self_attn(h))
-        return self.final_layer_norm(h + self.fc2(self.activation_fn(self.fc1(h))))
+        h = _residual_norm(h, self.self_attn(h), self.self_attn_layer_norm)
+        return _residual_norm(h, self.fc2(self.activation_fn(self.fc1(h))), self.final_layer_norm)
 
 
 class BartDecoderLayer(nn.Module):
@@ -150,9 +160,9 @@ class BartDecoderLayer(nn.Module):
         self.final_layer_norm = nn.LayerNorm(d)
 
     def forward(self, h: torch.Tensor) -> torch.Tensor:
-        h = self.self_attn_layer_norm(h + self.self_attn(h))
-        h = self.encoder_attn_layer_norm(h + self.encoder_attn(h))
-        return self.final_layer_norm(h + self.fc2(self.activation_fn(self.fc1(h))))
+        h = _residual_norm(h, self.self_attn(h), self.self_attn_layer_norm)
+        h = _residual_norm(h, self.encoder_attn(h), self.encoder_attn_layer_norm)
+        return _residual_norm(h, self.fc2(self.activation_fn(self.fc1(h))), self.final_layer_norm)
 
 
 def _embed_scale(config) -> float:

@@ -65,6 +65,27 @@ class LogitsProcessor:
             self._set(scores, lengths == self.begin_index, self.begin_suppress, _NEG_INF)
         return scores
 
+    def topk_rules(self):
+        """These rules packed for the fused log-softmax + rules + top-k kernel, or None
+        when a rule reads the token history (repetition penalty, n-gram bans)."""
+        if self.needs_history:
+            return None
+        if not hasattr(self, "_topk_rules"):
+            from ..decoder_ops import TopkRules
+
+            def ids(t):
+                return [] if t is None else t.tolist()
+
+            device = next((t.device for t in (self.eos, self.suppress, self.begin_suppress,
+                                              self.forced_bos, self.forced_eos) if t is not None),
+                          None)
+            self._topk_rules = TopkRules(
+                eos=ids(self.eos), suppress=ids(self.suppress),
+                begin_suppress=ids(self.begin_suppress), forced_bos=ids(self.forced_bos),
+                forced_eos=ids(self.forced_eos), min_length=self.sampling_params.min_length,
+                max_length=self.max_length, begin_index=self.begin_index, device=device)
+        return self._topk_rules
+
     def _token_mask(self, history, valid, tokens) -> torch.Tensor:
         """[rows, vocab] bool: True where ``tokens[r, j]`` is a token and ``valid[r, j]``."""
         rows = history.shape[0]
