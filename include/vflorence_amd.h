@@ -229,7 +229,7 @@ int vfl_add_layer_norm(const void *x, int64_t x_stride, const void *residual,
  * and writes the k best (score, token) pairs, best first (ties: lower token first),
  * to scores / ids ([rows][k]).  rule_tokens is a DEVICE int32 array holding, in order,
  * n_eos EOS, n_suppress suppressed, n_begin begin-suppressed, n_bos forced-BOS and
- * n_forced_eos forced-EOS token ids.  1 <= k <= 32; lengths may be NULL only without
+ * n_forced_eos forced-EOS token ids.  1 <= k <= 16; lengths may be NULL only without
  * rule tokens.  Repetition penalty and n-gram bans (which read the history) are not
  * covered: their callers apply them before, on the logits.
  */

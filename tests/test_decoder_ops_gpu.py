@@ -78,7 +78,8 @@ RULES = [
 
 
 @pytest.mark.parametrize("rule", range(len(RULES)))
-@pytest.mark.parametrize("vocab,k", [(50265, 8), (50265, 1), (50265, 32), (40, 16), (12, 12)])
+@pytest.mark.parametrize("vocab,k", [(50265, 8), (50265, 1), (50265, 16), (40, 16), (12, 12),
+                                     (50265, 3)])
 @pytest.mark.parametrize("log_softmax", [True, False])
 def test_logprob_topk_matches_processor_and_topk(rule, vocab, k, log_softmax):
     from transformers import GenerationConfig

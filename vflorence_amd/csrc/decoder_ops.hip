@@ -18,21 +18,12 @@
 namespace vfl {
 
 // ---------------------------------------------------------------------------
-// block-wide sums (256 threads = 4 waves)
+// wave-wide sum (64 lanes)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
-}
-
-__device__ __forceinline__ float block_sum(float v, float *lds4) {
-  v = wave_sum(v);
-  const int wave = threadIdx.x >> 6;
-  __syncthreads();  // lds4 may still be read from the previous call
-  if ((threadIdx.x & 63) == 0) lds4[wave] = v;
-  __syncthreads();
-  return lds4[0] + lds4[1] + lds4[2] + lds4[3];
 }
 
 template <int DT> __device__ __forceinline__ void load4(const typename Elem<DT>::T *p, float v[4]);
@@ -78,33 +69,37 @@ template <> __device__ __forceinline__ float round_to_elem<VFL_FLOAT16>(float v)
 }
 
 // ---------------------------------------------------------------------------
-// residual add + LayerNorm
+// residual add + LayerNorm: one wave per row, statistics by wave shuffles (no
+// workgroup barrier on the row's critical path)
 // ---------------------------------------------------------------------------
-constexpr int LN_THREADS = 256;
+constexpr int LN_ROWS = 4;  // rows (waves) per workgroup
 
-template <int DT, int NV>  // NV: 4-element vectors per thread (dim <= 1024 * NV)
-__global__ __launch_bounds__(LN_THREADS) void add_layer_norm_kernel(
+template <int DT, int NV>  // NV: 4-element vectors per lane (dim <= 256 * NV)
+__global__ __launch_bounds__(64 * LN_ROWS) void add_layer_norm_kernel(
     const typename Elem<DT>::T *x, int64_t x_stride, const typename Elem<DT>::T *residual,
     int64_t r_stride, const typename Elem<DT>::T *__restrict__ weight,
     const typename Elem<DT>::T *__restrict__ bias, typename Elem<DT>::T *out, int64_t out_stride,
-    int dim, float eps) {
-  // out may alias x or residual: each thread reads its elements before the two
-  // workgroup reductions and writes the same elements after them.
-  __shared__ float lds4[4];
-  const int64_t row = blockIdx.x;
+    int64_t rows, int dim, float eps) {
+  // out may alias x or residual: each lane reads its elements before the reductions
+  // and writes the same elements after them.
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * LN_ROWS + (threadIdx.x >> 6);
+  if (row >= rows) return;  // wave-uniform
   const int nvec = dim >> 2;
-  float v[NV][4];
+  float v[NV][4], w[NV][4], b[NV][4];
   float sum = 0.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    const int vi = threadIdx.x + k * LN_THREADS;
+    const int vi = lane + 64 * k;
     if (vi < nvec) {
-      float a[4], b[4];
+      float a[4], c[4];
       load4<DT>(x + row * x_stride + vi * 4, a);
-      load4<DT>(residual + row * r_stride + vi * 4, b);
+      load4<DT>(residual + row * r_stride + vi * 4, c);
+      load4<DT>(weight + vi * 4, w[k]);
+      load4<DT>(bias + vi * 4, b[k]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[k][e] = round_to_elem<DT>(a[e] + b[e]);
+        v[k][e] = round_to_elem<DT>(a[e] + c[e]);
         sum += v[k][e];
       }
     } else {
@@ -112,11 +107,11 @@ __global__ __launch_bounds__(LN_THREADS) void add_layer_norm_kernel(
       for (int e = 0; e < 4; ++e) v[k][e] = 0.f;
     }
   }
-  const float mean = block_sum(sum, lds4) / (float)dim;
+  const float mean = wave_sum(sum) / (float)dim;
   float sq = 0.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    if (threadIdx.x + k * LN_THREADS < nvec) {
+    if (lane + 64 * k < nvec) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float d = v[k][e] - mean;
@@ -124,16 +119,14 @@ __global__ __launch_bounds__(LN_THREADS) void add_layer_norm_kernel(
       }
     }
   }
-  const float rstd = rsqrtf(block_sum(sq, lds4) / (float)dim + eps);
+  const float rstd = rsqrtf(wave_sum(sq) / (float)dim + eps);
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    const int vi = threadIdx.x + k * LN_THREADS;
+    const int vi = lane + 64 * k;
     if (vi < nvec) {
-      float w[4], b[4], o[4];
-      load4<DT>(weight + vi * 4, w);
-      load4<DT>(bias + vi * 4, b);
+      float o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (v[k][e] - mean) * rstd * w[e] + b[e];
+      for (int e = 0; e < 4; ++e) o[e] = (v[k][e] - mean) * rstd * w[k][e] + b[k][e];
       store4<DT>(out + row * out_stride + vi * 4, o);
     }
   }
@@ -145,16 +138,21 @@ static int launch_add_layer_norm(const void *x, int64_t xs, const void *r, int64
                                  int dim, float eps, hipStream_t stream) {
   using T = typename Elem<DT>::T;
   const int nvec = dim / 4;
-  const dim3 grid((unsigned)rows), block(LN_THREADS);
+  const dim3 grid((unsigned)((rows + LN_ROWS - 1) / LN_ROWS)), block(64 * LN_ROWS);
 #define VFL_LN(NV)                                                                             \
   add_layer_norm_kernel<DT, NV><<<grid, block, 0, stream>>>(                                   \
-      (const T *)x, xs, (const T *)r, rs, (const T *)w, (const T *)b, (T *)out, os, dim, eps)
-  if (nvec <= LN_THREADS)
+      (const T *)x, xs, (const T *)r, rs, (const T *)w, (const T *)b, (T *)out, os, rows, dim, \
+      eps)
+  if (nvec <= 64)
     VFL_LN(1);
-  else if (nvec <= 2 * LN_THREADS)
+  else if (nvec <= 128)
     VFL_LN(2);
-  else
+  else if (nvec <= 256)
     VFL_LN(4);
+  else if (nvec <= 512)
+    VFL_LN(8);
+  else
+    VFL_LN(16);
 #undef VFL_LN
   return launch_status("add_layer_norm");
 }
@@ -162,7 +160,6 @@ static int launch_add_layer_norm(const void *x, int64_t xs, const void *r, int64
 // ---------------------------------------------------------------------------
 // log-softmax + generation rules + per-row top-k
 // ---------------------------------------------------------------------------
-constexpr int TK_THREADS = 256;
 constexpr int TK_MAX_RULE_TOKENS = 256;
 
 // (score, token) order: higher score first, then lower token id, then lower lane.
@@ -215,18 +212,62 @@ __device__ __forceinline__ bool in_list(const int *list, int n, int t) {
   return false;
 }
 
-template <int DT, int K>
-__global__ __launch_bounds__(TK_THREADS) void logprob_topk_kernel(
+template <int DT> __device__ __forceinline__ float elem_to_f32(typename Elem<DT>::T v) {
+  if constexpr (DT == VFL_FLOAT32) return v;
+  else if constexpr (DT == VFL_BFLOAT16) return __uint_as_float((uint32_t)v << 16);
+  else return (float)__builtin_bit_cast(_Float16, v);
+}
+
+// Element j of a 16-byte vector as fp32 (j a compile-time constant after unrolling).
+template <int DT> __device__ __forceinline__ float vec_elem(const uint4 &u, int j) {
+  if constexpr (DT == VFL_FLOAT32) {
+    const uint32_t w = j == 0 ? u.x : j == 1 ? u.y : j == 2 ? u.z : u.w;
+    return __uint_as_float(w);
+  } else {
+    const uint32_t w = (j >> 1) == 0 ? u.x : (j >> 1) == 1 ? u.y : (j >> 1) == 2 ? u.z : u.w;
+    const uint32_t h = (j & 1) ? (w >> 16) : (w & 0xffffu);
+    if constexpr (DT == VFL_BFLOAT16) return __uint_as_float(h << 16);
+    else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  }
+}
+
+// Wave-wide maximum.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Row top-k in two reads of the row (the second mostly from L2):
+//   1. each thread's largest allowed value, and the row maximum for the normaliser;
+//      the k-th largest of the per-thread maxima, tau, bounds the row's k-th value
+//      from below (k threads hold a value >= tau);
+//   2. the sum of exp(x - max), and every allowed value >= tau appended to an LDS list
+//      (a handful per row);
+//   3. one wave picks the k best of that list.
+// Rows with a forced token, fewer than k allowed finite values, or more than CAP
+// values tied at the threshold take a third read that keeps per-lane k-best lists.
+template <int DT, int K, int NT>
+__global__ __launch_bounds__(NT, 2) void logprob_topk_kernel(
     const typename Elem<DT>::T *__restrict__ logits, int64_t stride, int vocab,
     const int64_t *__restrict__ lengths, const int32_t *__restrict__ rule_tokens, TopkRules rules,
     int log_softmax, int k_out, float *__restrict__ out_scores, int64_t *__restrict__ out_ids) {
   using T = typename Elem<DT>::T;
+  constexpr int NWAVE = NT / 64;
+  constexpr int VE = 16 / sizeof(T);  // elements per 16-byte load
+  constexpr int CAP = 512;            // threshold candidates kept in LDS
+  constexpr int LPL = CAP / 64;       // candidates per lane in the final pick
+  constexpr int TPL = NT / 64;        // per-thread maxima per lane when finding tau
   __shared__ int s_ban[TK_MAX_RULE_TOKENS];
   __shared__ int s_force[TK_MAX_RULE_TOKENS];
-  __shared__ float s_val[4][K];
-  __shared__ int s_tok[4][K];
-  __shared__ float s_m[4], s_s[4];
-  __shared__ int s_nban, s_nforce;
+  __shared__ float s_tmax[NT];
+  __shared__ float s_cv[CAP];
+  __shared__ int s_ct[CAP];
+  __shared__ float s_val[NWAVE][K];
+  __shared__ int s_tok[NWAVE][K];
+  __shared__ float s_red[NWAVE];
+  __shared__ int s_nban, s_nforce, s_count;
+  __shared__ float s_tau;
 
   const int64_t row = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -250,52 +291,137 @@ __global__ __launch_bounds__(TK_THREADS) void logprob_topk_kernel(
     for (int i = 0; i < rules.n_suppress; ++i) s_ban[nb++] = sup[i];
     if (len == rules.begin_index)
       for (int i = 0; i < rules.n_begin; ++i) s_ban[nb++] = beg[i];
-    s_nban = nb, s_nforce = nf;
+    s_nban = nb, s_nforce = nf, s_count = 0;
   }
   __syncthreads();
   const int nban = s_nban, nforce = s_nforce;
 
+  // The row in 16-byte loads: scalar elements up to the first aligned address, the
+  // aligned body RD loads per thread in flight at a time, then the scalar tail.  Every
+  // thread visits its tokens in increasing order.
+  constexpr int RD = 8;
+  const int head = min(vocab, (int)(((16 - ((uintptr_t)x & 15)) & 15) / sizeof(T)));
+  const int nvec = (vocab - head) / VE;
+  const uint4 *xv = reinterpret_cast<const uint4 *>(x + head);
+  auto scan = [&](auto &&visit) {
+    if ((int)threadIdx.x < head) visit(elem_to_f32<DT>(x[threadIdx.x]), (int)threadIdx.x);
+    for (int i = threadIdx.x; i < nvec; i += RD * NT) {
+      uint4 u[RD];
+#pragma unroll
+      for (int r = 0; r < RD; ++r)
+        if (i + r * NT < nvec) u[r] = xv[i + r * NT];
+#pragma unroll
+      for (int r = 0; r < RD; ++r) {
+        if (i + r * NT < nvec) {
+#pragma unroll
+          for (int j = 0; j < VE; ++j) visit(vec_elem<DT>(u[r], j), head + (i + r * NT) * VE + j);
+        }
+      }
+    }
+    for (int t = head + nvec * VE + threadIdx.x; t < vocab; t += NT)
+      visit(elem_to_f32<DT>(x[t]), t);
+  };
+
+  float mx = 0.f, lse = 0.f;
+  if (nforce == 0) {
+    // 1: row maximum and each thread's largest value (bans are applied to the few
+    // candidates of step 3, so the scans stay branch-free)
+    float rawmax = -INFINITY;
+    scan([&](float v, int) { rawmax = fmaxf(rawmax, v); });
+    s_tmax[threadIdx.x] = rawmax;
+    rawmax = wave_max(rawmax);
+    if (lane == 0) s_red[wave] = rawmax;
+    __syncthreads();
+    mx = s_red[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; ++w) mx = fmaxf(mx, s_red[w]);
+    if (wave == 0) {
+      // tau: the (K + nban)-th largest per-thread maximum (with multiplicity).  At least
+      // K + nban values are >= tau and at most nban of them are banned, so the row's
+      // K-th allowed value is >= tau too.
+      float c[TPL];
+      int ci[TPL];
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) c[i] = -INFINITY, ci[i] = INT32_MAX;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) insert<TPL>(c, ci, s_tmax[lane * TPL + i], lane * TPL + i);
+      float tau = -INFINITY;
+      const int need = min(K + nban, NT);
+      for (int r = 0; r < need; ++r) {
+        float bv;
+        int bt, bl;
+        wave_best(c[0], ci[0], bv, bt, bl);
+        if (lane == bl) pop_head<TPL>(c, ci);
+        tau = bv;
+      }
+      if (lane == 0) s_tau = (K + nban <= NT) ? tau : -INFINITY;
+    }
+    __syncthreads();
+    const float tau = s_tau;
+    const float pick = tau == -INFINITY ? INFINITY : tau;  // no shortcut without a bound
+    // 2: normaliser sum and every value at or above tau
+    float sum = 0.f;
+    scan([&](float v, int t) {
+      if (log_softmax && v != -INFINITY) sum += expf(v - mx);
+      if (v >= pick) {
+        const int slot = atomicAdd(&s_count, 1);
+        if (slot < CAP) s_cv[slot] = v, s_ct[slot] = t;
+      }
+    });
+    if (log_softmax) {
+      sum = wave_sum(sum);
+      __syncthreads();  // s_red is reused
+      if (lane == 0) s_red[wave] = sum;
+    }
+    __syncthreads();
+    if (log_softmax) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWAVE; ++w) tot += s_red[w];
+      lse = logf(tot);
+    }
+    const int count = s_count;
+    if (tau != -INFINITY && count <= CAP) {
+      // 3: the K best allowed candidates
+      if (wave != 0) return;
+      float cv[LPL];
+      int ct[LPL];
+#pragma unroll
+      for (int i = 0; i < LPL; ++i) cv[i] = -INFINITY, ct[i] = INT32_MAX;
+      for (int i = 0; i < LPL; ++i) {
+        const int c = lane + 64 * i;
+        if (c < count && !in_list(s_ban, nban, s_ct[c])) insert<LPL>(cv, ct, s_cv[c], s_ct[c]);
+      }
+      for (int r = 0; r < k_out; ++r) {
+        float bv;
+        int bt, bl;
+        wave_best(cv[0], ct[0], bv, bt, bl);
+        if (lane == bl) pop_head<LPL>(cv, ct);
+        if (lane == 0) {
+          out_scores[row * k_out + r] = log_softmax ? (bv - mx) - lse : bv;
+          out_ids[row * k_out + r] = bt;
+        }
+      }
+      return;
+    }
+  }
+
+  // Per-lane k-best lists over the whole row (forced rows and the rare fallbacks).
   float val[K];
   int tok[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) val[j] = -INFINITY, tok[j] = INT32_MAX;
-  // running max / sum of exp for the log-softmax normaliser (every token counts)
-  float m = -INFINITY, s = 0.f;
-
-  for (int t = threadIdx.x; t < vocab; t += TK_THREADS) {
-    const float xv = [&] {
-      if constexpr (DT == VFL_FLOAT32) return x[t];
-      else if constexpr (DT == VFL_BFLOAT16) return __uint_as_float((uint32_t)x[t] << 16);
-      else return (float)__builtin_bit_cast(_Float16, x[t]);
-    }();
-    if (log_softmax) {
-      if (xv > m) {
-        s = s * expf(m - xv) + 1.f;
-        m = xv;
-      } else if (xv != -INFINITY) {
-        s += expf(xv - m);
-      }
-    }
+  // a plain element loop: these rows are rare, and the code stays small
+#pragma nounroll
+  for (int t = threadIdx.x; t < vocab; t += NT) {
+    const float v = elem_to_f32<DT>(x[t]);
     if (nforce) {
-      const float v = (in_list(s_force, nforce, t) && !in_list(s_ban, nban, t)) ? 0.f : -INFINITY;
-      insert<K>(val, tok, v, t);
-    } else if (better(xv, t, val[K - 1], tok[K - 1])) {
-      insert<K>(val, tok, in_list(s_ban, nban, t) ? -INFINITY : xv, t);
+      const float f = (in_list(s_force, nforce, t) && !in_list(s_ban, nban, t)) ? 0.f : -INFINITY;
+      insert<K>(val, tok, f, t);
+    } else if (better(v, t, val[K - 1], tok[K - 1])) {
+      insert<K>(val, tok, in_list(s_ban, nban, t) ? -INFINITY : v, t);
     }
   }
-
-  // normaliser: max and sum over the workgroup
-  float lse = 0.f;
-  if (log_softmax) {
-    float wm = m;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o, 64));
-    float ws = (m == -INFINITY) ? 0.f : s * expf(m - wm);
-    ws = wave_sum(ws);
-    if (lane == 0) s_m[wave] = wm, s_s[wave] = ws;
-  }
-
-  // each wave's K best, then the workgroup's
   for (int r = 0; r < K; ++r) {
     float bv;
     int bt, bl;
@@ -305,33 +431,21 @@ __global__ __launch_bounds__(TK_THREADS) void logprob_topk_kernel(
   }
   __syncthreads();
   if (wave != 0) return;
-  float mx = 0.f;
-  if (log_softmax) {
-    mx = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
-    float tot = 0.f;
-    for (int w = 0; w < 4; ++w)
-      if (s_m[w] != -INFINITY) tot += s_s[w] * expf(s_m[w] - mx);
-    lse = logf(tot);
-  }
-  // lane l holds candidates l and l + 64 of the 4K (each wave's list is sorted)
-  float cv[2];
-  int ct[2];
-  for (int i = 0; i < 2; ++i) {
+  constexpr int CPL = (NWAVE * K + 63) / 64;
+  float cv[CPL];
+  int ct[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) cv[i] = -INFINITY, ct[i] = INT32_MAX;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
     const int c = lane + 64 * i;
-    cv[i] = c < 4 * K ? s_val[c / K][c % K] : -INFINITY;
-    ct[i] = c < 4 * K ? s_tok[c / K][c % K] : INT32_MAX;
-  }
-  if (better(cv[1], ct[1], cv[0], ct[0])) {
-    const float fv = cv[0];
-    cv[0] = cv[1], cv[1] = fv;
-    const int ft = ct[0];
-    ct[0] = ct[1], ct[1] = ft;
+    if (c < NWAVE * K) insert<CPL>(cv, ct, s_val[c / K][c % K], s_tok[c / K][c % K]);
   }
   for (int r = 0; r < k_out; ++r) {
     float bv;
     int bt, bl;
     wave_best(cv[0], ct[0], bv, bt, bl);
-    if (lane == bl) cv[0] = cv[1], ct[0] = ct[1], cv[1] = -INFINITY, ct[1] = INT32_MAX;
+    if (lane == bl) pop_head<CPL>(cv, ct);
     if (lane == 0) {
       // processed log-prob: (x - max) - log(sum exp(x - max)); forced tokens score 0
       float outv = bv;
@@ -347,19 +461,17 @@ static int launch_topk(const void *logits, int64_t stride, int64_t rows, int voc
                        const int64_t *lengths, const int32_t *rule_tokens, const TopkRules &rules,
                        int log_softmax, int k, float *scores, int64_t *ids, hipStream_t stream) {
   using T = typename Elem<DT>::T;
-  const dim3 grid((unsigned)rows), block(TK_THREADS);
-#define VFL_TK(KK)                                                                             \
-  logprob_topk_kernel<DT, KK><<<grid, block, 0, stream>>>((const T *)logits, stride, vocab,    \
-                                                          lengths, rule_tokens, rules,         \
-                                                          log_softmax, k, scores, ids)
+  const dim3 grid((unsigned)rows);
+  // 8 waves per row; each lane's list lives in registers (k <= 16 keeps it there)
+#define VFL_TK(KK, NT)                                                                         \
+  logprob_topk_kernel<DT, KK, NT><<<grid, dim3(NT), 0, stream>>>(                              \
+      (const T *)logits, stride, vocab, lengths, rule_tokens, rules, log_softmax, k, scores, ids)
   if (k <= 1)
-    VFL_TK(1);
+    VFL_TK(1, 512);
   else if (k <= 8)
-    VFL_TK(8);
-  else if (k <= 16)
-    VFL_TK(16);
+    VFL_TK(8, 512);
   else
-    VFL_TK(32);
+    VFL_TK(16, 512);
 #undef VFL_TK
   return launch_status("logprob_topk");
 }
@@ -420,9 +532,9 @@ extern "C" int vfl_logprob_topk(const void *logits, int64_t row_stride, int64_t 
     set_error("logprob_topk: unsupported dtype code %d", dtype);
     return VFL_E_INVALID;
   }
-  if (rows < 0 || rows > 2147483647LL || vocab <= 0 || row_stride < vocab || k < 1 || k > 32 ||
+  if (rows < 0 || rows > 2147483647LL || vocab <= 0 || row_stride < vocab || k < 1 || k > 16 ||
       k > vocab) {
-    set_error("logprob_topk: need 1 <= k <= min(32, vocab) and row_stride >= vocab (k %d, vocab "
+    set_error("logprob_topk: need 1 <= k <= min(16, vocab) and row_stride >= vocab (k %d, vocab "
               "%d, stride %lld)",
               k, vocab, (long long)row_stride);
     return VFL_E_INVALID;

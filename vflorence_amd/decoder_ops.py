@@ -15,6 +15,9 @@ import torch
 from ._lib import check, lib
 from .hip_attn import _dtype_code, _require_gpu, _stream
 
+# largest k of logprob_topk (each lane keeps its k best in registers)
+MAX_K = 16
+
 
 @torch.library.custom_op("vflorence_amd::add_layer_norm", mutates_args=())
 def add_layer_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
@@ -68,8 +71,8 @@ def logprob_topk(logits: torch.Tensor, k: int, *, log_softmax: bool,
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be [rows, vocab] with contiguous rows")
     rows, vocab = logits.shape
-    if not 1 <= k <= min(32, vocab):
-        raise ValueError(f"k must be in [1, min(32, vocab)], got {k}")
+    if not 1 <= k <= min(MAX_K, vocab):
+        raise ValueError(f"k must be in [1, min({MAX_K}, vocab)], got {k}")
     counts = rules.counts if rules is not None else [0] * 5
     tokens = rules.tokens if rules is not None else None
     if sum(counts) and lengths is None:

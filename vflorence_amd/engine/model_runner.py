@@ -317,7 +317,7 @@ class ModelRunner:
                                     for s in seqs], dtype=torch.long).to(device)
         rules = processor.topk_rules() if logits.is_cuda else None
         keep = max(2, 1 + len(sp.eos_ids())) * sp.num_beams
-        if rules is not None and (sp.num_beams == 1 or keep <= 32):
+        if rules is not None and (sp.num_beams == 1 or keep <= decoder_ops.MAX_K):
             # one kernel: log-softmax (beam search), the rules, the per-row top-k
             if sp.num_beams == 1:
                 _, ids = decoder_ops.logprob_topk(logits, 1, log_softmax=False, lengths=lengths,
