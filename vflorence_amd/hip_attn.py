@@ -33,6 +33,7 @@ MAX_GROUP_SIZE = 8
 # Waves per workgroup for the fused KV-write + self-attention launch (measured: two
 # beat four on both short decode-step contexts and 256 ragged rows up to 1024 tokens).
 FUSED_WAVES = 2
+FUSED_ONE_WAVE_BLOCKS = 4
 
 
 def _pow2_at_least(n: int) -> int:
@@ -192,8 +193,11 @@ class SchedulerMetadata:
             groups = num_rows if self.group_start is None else self.num_groups
             waves = self.waves_per_workgroup
             if waves == 0 and self.fuse_kv_write:
-                # measured best for the fused write + attention kernel (MI355X, bf16)
-                waves = min(FUSED_WAVES, _pow2_at_least(max_blocks))
+                # measured best for the fused write + attention kernel (MI355X, bf16, 256
+                # rows x 16 heads): one wave up to 4 blocks of context (a decode step's
+                # short contexts are latency-bound; more waves only add a merge), two
+                # beyond (ragged contexts up to 1024 tokens)
+                waves = 1 if max_blocks <= FUSED_ONE_WAVE_BLOCKS else FUSED_WAVES
             check(
                 lib.vfl_get_scheduler_metadata(
                     num_rows, groups, self.num_heads, self.head_dim, self.block_size,
