@@ -7,7 +7,9 @@ U[256, 1024], a 128-step beam search whose forks make copy-on-write pairs every 
 A step is one decode step of the attention path: the batched CoW block copy, then per
 layer the KV slot write + paged self-attention and the beam-grouped paged
 cross-attention, through the vflorence::self_attention / vflorence::cross_attention
-custom ops.  Each step is captured as a HIP graph; all inputs and per-step metadata
+custom ops.  Self-attention takes each request's beams as one row group that reads the
+prefix blocks they share once; the step's algorithmic bytes count a shared block once
+(``--ungrouped-self``: one row per workgroup, every row's blocks counted).  Each step is captured as a HIP graph; all inputs and per-step metadata
 are resident in HBM before timing.  Q/K/V values are synthetic (random), not produced
 by the decoder GEMMs.
 
@@ -51,6 +53,8 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-engine", action="store_true",
                    help="skip the whole-engine decoder tokens/s measurement")
+    p.add_argument("--ungrouped-self", action="store_true",
+                   help="self-attention one row per workgroup (no shared-prefix groups)")
     p.add_argument("--counters", action="store_true",
                    help="counter-collection run for rocprofv3 --pmc: the dominant kernel's "
                         "launches and two copies of known size, nothing timed")
@@ -111,18 +115,24 @@ def build_workload(torch, seed: int):
                 enc_rows=enc_rows, pages=pages, num_blocks=num_blocks, num_cross=num_cross)
 
 
-def step_bytes(plan, enc, elem=2):
+def step_bytes(plan, enc, elem=2, grouped=True):
     from vflorence_amd import workloads
 
     rows = len(plan.context_lens)
-    self_b = workloads.self_attention_bytes(plan.context_lens, NUM_HEADS, HEAD_DIM, elem, BLOCK)
+    if grouped:  # each request's beams read a shared prefix block once
+        self_b = workloads.shared_self_attention_bytes(plan.block_tables, plan.context_lens,
+                                                       BEAMS, NUM_HEADS, HEAD_DIM, elem, BLOCK)
+    else:
+        self_b = workloads.self_attention_bytes(plan.context_lens, NUM_HEADS, HEAD_DIM, elem,
+                                                BLOCK)
     cross_b = workloads.cross_attention_bytes(enc, rows, NUM_HEADS, HEAD_DIM, elem, BLOCK)
     cow_b = len(plan.copies) * 2 * NUM_LAYERS * (NUM_HEADS * BLOCK * HEAD_DIM * elem) * 2
     return NUM_LAYERS * (self_b + cross_b) + cow_b, self_b, cross_b, cow_b
 
 
-def capture_steps(torch, wl):
-    """One HIP graph per decode step of the schedule."""
+def capture_steps(torch, wl, grouped=True):
+    """One HIP graph per decode step of the schedule.  ``grouped``: each request's beams
+    form one self-attention row group (own tables, shared blocks read once)."""
     from vflorence_amd import hip_attn
     from vflorence_amd.layers import attention
     from vflorence_amd.utils.context import set_context
@@ -142,19 +152,29 @@ def capture_steps(torch, wl):
                               dtype=torch.int32, device=dev)
         lens = torch.tensor(plan.context_lens, dtype=torch.int32, device=dev)
         slots = torch.tensor(plan.slot_mapping, dtype=torch.int64, device=dev)
-        order = torch.tensor(hip_attn.longest_first(plan.context_lens), dtype=torch.int32,
-                             device=dev)
         # slots come from BlockManager tables (private last blocks): fused KV write
-        meta = hip_attn.get_scheduler_metadata(
-            num_reqs=rows, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS, head_dim=HEAD_DIM,
-            dtype=torch.bfloat16, block_size=BLOCK, group_order=order, fuse_kv_write=True)
+        if grouped:
+            # every group is resident at once: no dispatch order needed
+            starts = torch.arange(0, rows + 1, BEAMS, dtype=torch.int32, device=dev)
+            order = None
+            meta = hip_attn.get_scheduler_metadata(
+                num_reqs=rows, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS, head_dim=HEAD_DIM,
+                dtype=torch.bfloat16, block_size=BLOCK, group_start=starts,
+                max_group_size=BEAMS, own_tables=True, fuse_kv_write=True)
+        else:
+            starts = None
+            order = torch.tensor(hip_attn.longest_first(plan.context_lens), dtype=torch.int32,
+                                 device=dev)
+            meta = hip_attn.get_scheduler_metadata(
+                num_reqs=rows, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS, head_dim=HEAD_DIM,
+                dtype=torch.bfloat16, block_size=BLOCK, group_order=order, fuse_kv_write=True)
         src = dst = None
         staged = False
         if plan.copies:
             src = torch.tensor([s for s, _ in plan.copies], dtype=torch.int64, device=dev)
             dst = torch.tensor([d for _, d in plan.copies], dtype=torch.int64, device=dev)
             staged = hip_attn.copy_pairs_need_staging(plan.copies)
-        keep.append((tables, lens, slots, order, meta, src, dst))
+        keep.append((tables, lens, slots, starts, order, meta, src, dst))
 
         def run():
             set_context(context_lens=lens, block_tables=tables, slot_mapping=slots,
@@ -246,8 +266,10 @@ def raw_fused_launcher(torch, case, out, sm):
             c.value.stride(1), c.slot_mapping.data_ptr(), c.k_cache.data_ptr(),
             c.v_cache.data_ptr(), out.data_ptr(), c.context_lens.data_ptr(),
             c.block_tables.data_ptr(), c.block_tables.stride(0),
-            None if sm.group_order is None else sm.group_order.data_ptr(), rows, NUM_HEADS,
-            HEAD_DIM, BLOCK, c.k_cache.shape[0], c.scale, 1, ctypes.byref(meta), stream)
+            None if sm.group_start is None else sm.group_start.data_ptr(),
+            None if sm.group_order is None else sm.group_order.data_ptr(), rows,
+            rows if sm.group_start is None else sm.num_groups, NUM_HEADS, HEAD_DIM, BLOCK,
+            c.k_cache.shape[0], c.scale, 1, ctypes.byref(meta), stream)
     fn = lib.vfl_self_attention_with_kv_write
 
     def launch():
@@ -427,11 +449,11 @@ def engine_decode(torch, seed: int):
     }
 
 
-def cpu_baseline(torch, wl, budget_s: float):
+def cpu_baseline(torch, wl, budget_s: float, grouped: bool = True):
     """The C restatement (oracle/, OpenMP, fp32 accumulation) on one decoder layer of the
     same workload: per sampled step, the CoW copy of that layer's two caches, the KV slot
     write, paged self-attention and beam-shared cross-attention.  Rate in the same unit
-    (algorithmic GB/s)."""
+    (algorithmic GB/s, counted as for the GPU figure)."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -472,7 +494,7 @@ def cpu_baseline(torch, wl, budget_s: float):
             orc.paged_attention_c(q, kc, vc, lens, tab, HEAD_DIM**-0.5, orc.BF16, threads)
             orc.paged_attention_c(qc, ck, cv, clens, ctab, HEAD_DIM**-0.5, orc.BF16, threads)
             spent += time.perf_counter() - t0
-            _, self_b, cross_b, _ = step_bytes(plan, wl["enc"])
+            _, self_b, cross_b, _ = step_bytes(plan, wl["enc"], grouped=grouped)
             done_bytes += self_b + cross_b + len(plan.copies) * 2 * NUM_HEADS * BLOCK * HEAD_DIM * 2 * 2
             steps_done += 1
             if spent >= budget_s:
@@ -510,9 +532,10 @@ def main():
         counter_pass(torch, wl, reps=2)
         return
     print("[bench] capturing 128 decode-step graphs", flush=True)
-    graphs, keep = capture_steps(torch, wl)
+    grouped = not args.ungrouped_self
+    graphs, keep = capture_steps(torch, wl, grouped)
     plans = wl["plans"]
-    per_step = [step_bytes(p, wl["enc"]) for p in plans]
+    per_step = [step_bytes(p, wl["enc"], grouped=grouped) for p in plans]
 
     for i in range(args.warmup):
         graphs[i % DECODE_STEPS].replay()
@@ -543,7 +566,7 @@ def main():
     cpu = None
     if args.cpu_seconds > 0:
         print("[bench] CPU baseline (oracle restatement)", flush=True)
-        cpu = cpu_baseline(torch, wl, args.cpu_seconds)
+        cpu = cpu_baseline(torch, wl, args.cpu_seconds, grouped)
     del wl
     torch.cuda.empty_cache()
 
@@ -586,6 +609,7 @@ def main():
         "attn_path_rows_per_s": round(rows * args.steps / elapsed, 1),
         "attn_path_request_tokens_per_s": round(REQUESTS * args.steps / elapsed, 1),
         "bytes_per_step_avg": int(total_bytes / args.steps),
+        "self_attention_groups": "beams (shared prefix blocks read once)" if grouped else "rows",
         "wall_s_timed": round(wall, 4),
         "roofline": {
             "bound": "hbm",

@@ -40,6 +40,19 @@ extern "C" {
 /* element types of caches, queries and outputs */
 enum vfl_dtype { VFL_FLOAT32 = 0, VFL_BFLOAT16 = 1, VFL_FLOAT16 = 2 };
 
+/*
+ * What the rows of a row group share (vfl_get_scheduler_metadata's group_tables):
+ *   VFL_GROUP_SHARED_TABLE  the group's rows are read through its first row's block
+ *                           table and length (cross-attention: the beams of a request
+ *                           over one encoder page list);
+ *   VFL_GROUP_OWN_TABLES    every row keeps its own table and length; a block that
+ *                           several rows of the group list at the same position is
+ *                           read once for all of them (decoder self-attention: beams
+ *                           whose copy-on-write forks share prefix blocks).  Any
+ *                           partition of the rows gives the same results.
+ */
+enum vfl_group_tables { VFL_GROUP_SHARED_TABLE = 0, VFL_GROUP_OWN_TABLES = 1 };
+
 /* status codes */
 enum vfl_status {
   VFL_OK = 0,
@@ -96,21 +109,23 @@ typedef struct vfl_sched_meta {
   int32_t head_dim;            /* head size the plan was made for                   */
   int32_t max_blocks_per_seq;  /* block-table width; longer contexts are clamped    */
   int32_t waves_per_workgroup; /* waves splitting one (group, head) context: 1..8   */
-  int32_t max_group_size;      /* query rows sharing one block-table row (beams)    */
+  int32_t max_group_size;      /* largest row group (beams)                         */
+  int32_t group_tables;        /* enum vfl_group_tables                             */
 } vfl_sched_meta;
 
 /*
  * num_rows:            query rows (sequences, beams included)
- * num_groups:          row groups sharing a block-table row (== num_rows when no
- *                      rows are grouped)
+ * num_groups:          row groups (== num_rows when no rows are grouped)
  * max_blocks_per_seq:  width of the block table
  * max_group_size:      largest group, 1..8
  * waves_per_workgroup: 0 picks the library default, else 1, 2, 4 or 8
+ * group_tables:        VFL_GROUP_SHARED_TABLE or VFL_GROUP_OWN_TABLES (what a
+ *                      group's rows share; ignored when calls pass no group_start)
  */
 int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_heads,
                                int head_dim, int block_size,
                                int64_t max_blocks_per_seq, int max_group_size,
-                               int dtype, int waves_per_workgroup,
+                               int dtype, int waves_per_workgroup, int group_tables,
                                vfl_sched_meta *meta);
 
 /*
@@ -125,10 +140,14 @@ int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_hea
  * block_table[r][j / block_size] at offset j % block_size.  Decode queries sit at
  * the end of their context, so the reference's causal flag changes nothing here.
  *
- * Row groups (cross-attention beams): when group_start is non-NULL, group g owns
- * rows group_start[g] .. group_start[g+1]-1, which must share one block-table row
- * and one length; the kernel reads that row's K/V once for the whole group.  With
- * group_start NULL every row is its own group (num_groups == num_rows).
+ * Row groups: when group_start is non-NULL, group g owns rows group_start[g] ..
+ * group_start[g+1]-1 (at most 8).  With meta->group_tables VFL_GROUP_SHARED_TABLE
+ * (cross-attention beams) the rows must share one block-table row and one length, and
+ * the kernel reads that row's K/V once for the whole group.  With
+ * VFL_GROUP_OWN_TABLES every row keeps its own table and length, and each block that
+ * several rows of a group list at the same position is read once (fp32 caches run
+ * such groups row by row).  With group_start NULL every row is its own group
+ * (num_groups == num_rows).
  * group_order (optional, int32 [num_groups]): a permutation of the groups giving
  * the dispatch order (longest first balances the tail); NULL = natural order.
  *
@@ -158,7 +177,7 @@ int vfl_attention_with_kv_cache(const void *query, int64_t query_stride_token,
  * The body of the reference's vflorence::self_attention op in one launch
  * (vflorence/layers/attention.py:53-73: reshape_and_cache of key/value at
  * slot_mapping, then attention_with_kv_cache over the updated cache), for one query
- * row per sequence (no row groups).
+ * row per sequence.
  *
  * Precondition (what the block manager's copy-on-write guarantees,
  * vflorence/engine/block_manager.py:44-59): for every row r, slot_mapping[r] is
@@ -170,7 +189,8 @@ int vfl_attention_with_kv_cache(const void *query, int64_t query_stride_token,
  *
  * key / value: [num_rows][num_heads][head_dim] with token / head strides in
  * elements (the strided views of a fused qkv projection).  Other arguments as for
- * vfl_attention_with_kv_cache with group_start NULL and num_groups == num_rows.
+ * vfl_attention_with_kv_cache; row groups (group_start non-NULL) need metadata made
+ * with VFL_GROUP_OWN_TABLES.
  */
 int vfl_self_attention_with_kv_write(const void *query, int64_t query_stride_token,
                                      int64_t query_stride_head, const void *key,
@@ -179,8 +199,9 @@ int vfl_self_attention_with_kv_write(const void *query, int64_t query_stride_tok
                                      int64_t value_stride_head, const int64_t *slot_mapping,
                                      void *k_cache, void *v_cache, void *out,
                                      const int32_t *seq_lens, const int32_t *block_table,
-                                     int64_t block_table_stride, const int32_t *group_order,
-                                     int64_t num_rows, int num_heads, int head_dim,
+                                     int64_t block_table_stride, const int32_t *group_start,
+                                     const int32_t *group_order, int64_t num_rows,
+                                     int64_t num_groups, int num_heads, int head_dim,
                                      int block_size, int64_t num_blocks, float scale,
                                      int dtype, const vfl_sched_meta *meta, void *stream);
 

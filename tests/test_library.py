@@ -43,12 +43,12 @@ def test_version_and_isa():
         hip_attn.get_isa(torch.bfloat16, 16, 80)
 
 
-def plan(rows, groups, heads, dim, max_blocks, gmax=1, nw=0, dtype=1):
+def plan(rows, groups, heads, dim, max_blocks, gmax=1, nw=0, dtype=1, tables=0):
     from vflorence_amd._lib import SchedMeta, lib
 
     meta = SchedMeta()
     rc = lib.vfl_get_scheduler_metadata(rows, groups, heads, dim, 16, max_blocks, gmax, dtype, nw,
-                                        ctypes.byref(meta))
+                                        tables, ctypes.byref(meta))
     return rc, meta
 
 
@@ -81,6 +81,7 @@ def test_scheduler_metadata_plan():
         dict(groups=300),  # more groups than rows
         dict(nw=3),  # not a power of two
         dict(nw=16),
+        dict(tables=2),  # neither shared nor own tables
     ],
 )
 def test_scheduler_metadata_rejects(kwargs):
@@ -122,6 +123,26 @@ def test_attention_validates_before_launch():
     assert lib.vfl_attention_with_kv_cache(None, 0, 0, None, None, None, None, None, 8, None, None,
                                            0, 0, 16, 64, 16, 100, 0.125, 1, ctypes.byref(meta0),
                                            None) == 0
+
+
+def test_fused_self_attention_groups_need_own_tables():
+    """Row groups in the fused KV-write entry point must come with metadata that says
+    every row keeps its own block table; the call is refused before any launch."""
+    from vflorence_amd._lib import VFL_GROUP_OWN_TABLES, lib
+
+    fake = ctypes.c_void_p(0x1000)
+
+    def call(tables):
+        rc, meta = plan(4, 2, 16, 64, 8, gmax=2, tables=tables)
+        assert rc == 0 and meta.group_tables == tables
+        # num_rows 0: validation only, nothing is launched
+        return lib.vfl_self_attention_with_kv_write(
+            fake, 3072, 64, fake, 3072, 64, fake, 3072, 64, fake, fake, fake, fake, fake, fake,
+            8, fake, None, 0, 0, 16, 64, 16, 100, 0.125, 1, ctypes.byref(meta), None)
+
+    assert call(0) == -1
+    assert b"VFL_GROUP_OWN_TABLES" in lib.vfl_last_error()
+    assert call(VFL_GROUP_OWN_TABLES) == 0
 
 
 def test_reshape_and_copy_validate_before_launch():

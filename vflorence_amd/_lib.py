@@ -15,6 +15,7 @@ LIB_NAME = "libvflorence_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 VFL_FLOAT32, VFL_BFLOAT16, VFL_FLOAT16 = 0, 1, 2
+VFL_GROUP_SHARED_TABLE, VFL_GROUP_OWN_TABLES = 0, 1
 VFL_OK = 0
 
 # Every symbol include/vflorence_amd.h declares; tests check the library exports them.
@@ -43,6 +44,7 @@ class SchedMeta(ctypes.Structure):
         ("max_blocks_per_seq", ctypes.c_int32),
         ("waves_per_workgroup", ctypes.c_int32),
         ("max_group_size", ctypes.c_int32),
+        ("group_tables", ctypes.c_int32),
     ]
 
 
@@ -59,7 +61,7 @@ _SIGNATURES = {
     ),
     "vfl_get_scheduler_metadata": (
         ctypes.c_int,
-        [_i64, _i64, _i32, _i32, _i32, _i64, _i32, _i32, _i32, ctypes.POINTER(SchedMeta)],
+        [_i64, _i64, _i32, _i32, _i32, _i64, _i32, _i32, _i32, _i32, ctypes.POINTER(SchedMeta)],
     ),
     "vfl_attention_with_kv_cache": (
         ctypes.c_int,
@@ -69,7 +71,8 @@ _SIGNATURES = {
     "vfl_self_attention_with_kv_write": (
         ctypes.c_int,
         [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
-         _vp, _i64, _i32, _i32, _i32, _i64, _f32, _i32, ctypes.POINTER(SchedMeta), _vp],
+         _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64, _f32, _i32, ctypes.POINTER(SchedMeta),
+         _vp],
     ),
     "vfl_copy_blocks": (
         ctypes.c_int,

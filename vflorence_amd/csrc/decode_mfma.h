@@ -42,6 +42,7 @@ struct KvWrite {
   const uint16_t *v;
   int64_t v_st, v_sh;
   const int64_t *slots;
+  bool vec;  // every K and V row is 16-byte aligned (16-byte loads)
 };
 
 template <int DT, int D>
@@ -84,13 +85,15 @@ __device__ __forceinline__ void mfma_consume(const uint4 (&qop)[D / 32], MfmaBlo
   float mb = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
   mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
   mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-  if (__builtin_amdgcn_ballot_w64(mb > m + RESCALE_SLACK_LOG2) != 0) {
-    const float mn = fmaxf(m, mb);
-    const float corr = (mn == NEG_INF_F) ? 1.f : fast_exp2(m - mn);
+  // Each column moves its reference only when its own block max needs it, so a
+  // column's arithmetic never depends on the other columns of the tile.
+  const bool need = mb > m + RESCALE_SLACK_LOG2;
+  if (__builtin_amdgcn_ballot_w64(need) != 0) {
+    const float corr = need ? fast_exp2(m - mb) : 1.f;
     l *= corr;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) acc[c] *= corr;
-    m = mn;
+    m = need ? mb : m;
   }
   const float ms = (m == NEG_INF_F) ? 0.f : m;
   float p[4];

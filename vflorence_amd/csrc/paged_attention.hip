@@ -17,7 +17,7 @@
 //   token rows keeps its own online-softmax state, merged across rows once at the
 //   end (no cross-row traffic in the loop).
 #include "common.h"
-#include "decode_mfma.h"
+#include "decode_shared.h"
 
 namespace vfl {
 
@@ -347,7 +347,8 @@ struct AttnArgs {
   int64_t num_blocks;
   float scale_log2;
   hipStream_t stream;
-  KvWrite kvw;  // slots == nullptr: no fused KV write
+  KvWrite kvw;      // slots == nullptr: no fused KV write
+  bool own_tables;  // groups whose rows keep their own tables (paged_decode_shared_kernel)
 };
 
 // fp32 caches: VALU kernel over the logical V layout, G query rows per group.
@@ -386,10 +387,28 @@ static int valu_group(const AttnArgs &a, int gmax, int nw) {
 // bf16 / fp16 caches: matrix-core kernel over the token-interleaved V layout; the tile
 // columns hold up to 16 query rows per group, so one instantiation serves any G.
 constexpr int MFMA_STAGE_BLOCKS = 2;
+// Stage size of the own-tables group kernel (measured on MI355X, 64 x 4-beam decode
+// steps: 3 and 4 blocks per stage were no faster and cost occupancy).
+constexpr int SHARED_STAGE_BLOCKS = 2;
 
 template <int DT, int D, int NW>
 static int launch_mfma(const AttnArgs &a) {
   const dim3 grid((unsigned)(a.num_groups * a.H));
+  if (a.own_tables) {
+    if (a.kvw.slots)
+      paged_decode_shared_kernel<DT, D, NW, SHARED_STAGE_BLOCKS, true>
+          <<<grid, dim3(NW * 64), 0, a.stream>>>(
+          (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
+          (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
+          a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw);
+    else
+      paged_decode_shared_kernel<DT, D, NW, SHARED_STAGE_BLOCKS, false>
+          <<<grid, dim3(NW * 64), 0, a.stream>>>(
+          (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
+          (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
+          a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw);
+    return launch_status("attention_with_kv_cache");
+  }
   if (a.kvw.slots)
     paged_decode_mfma_kernel<DT, D, NW, MFMA_STAGE_BLOCKS, true>
         <<<grid, dim3(NW * 64), 0, a.stream>>>(
@@ -463,7 +482,7 @@ extern "C" const char *vfl_get_isa(int dtype, int block_size, int head_dim) {
 extern "C" int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_heads,
                                           int head_dim, int block_size,
                                           int64_t max_blocks_per_seq, int max_group_size,
-                                          int dtype, int waves_per_workgroup,
+                                          int dtype, int waves_per_workgroup, int group_tables,
                                           vfl_sched_meta *meta) {
   clear_error();
   if (!meta) {
@@ -487,6 +506,11 @@ extern "C" int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, 
               MAX_GROUP);
     return VFL_E_UNSUPPORTED;
   }
+  if (group_tables != VFL_GROUP_SHARED_TABLE && group_tables != VFL_GROUP_OWN_TABLES) {
+    set_error("get_scheduler_metadata: group_tables %d is not VFL_GROUP_SHARED_TABLE or "
+              "VFL_GROUP_OWN_TABLES", group_tables);
+    return VFL_E_INVALID;
+  }
   int nw = waves_per_workgroup;
   if (nw == 0) nw = default_waves(num_groups, num_heads, max_blocks_per_seq);
   if (nw != 1 && nw != 2 && nw != 4 && nw != 8) {
@@ -504,6 +528,7 @@ extern "C" int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, 
   meta->max_blocks_per_seq = (int32_t)max_blocks_per_seq;
   meta->waves_per_workgroup = nw;
   meta->max_group_size = max_group_size;
+  meta->group_tables = group_tables;
   return VFL_OK;
 }
 
@@ -550,7 +575,9 @@ static int attention_impl(const void *query, int64_t query_stride_token,
   }
   const int nw = meta->waves_per_workgroup;
   if (meta->max_group_size < 1 || meta->max_group_size > MAX_GROUP ||
-      (nw != 1 && nw != 2 && nw != 4 && nw != 8) || meta->max_blocks_per_seq < 0) {
+      (nw != 1 && nw != 2 && nw != 4 && nw != 8) || meta->max_blocks_per_seq < 0 ||
+      (meta->group_tables != VFL_GROUP_SHARED_TABLE &&
+       meta->group_tables != VFL_GROUP_OWN_TABLES)) {
     set_error("%s: inconsistent metadata", who);
     return VFL_E_INVALID;
   }
@@ -588,6 +615,17 @@ static int attention_impl(const void *query, int64_t query_stride_token,
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
   a.stream = (hipStream_t)stream;
   a.kvw = kvw;
+  a.own_tables = group_start != nullptr && meta->group_tables == VFL_GROUP_OWN_TABLES;
+  if (a.own_tables && dtype == VFL_FLOAT32) {
+    // The VALU kernel reads one table per group; with rows keeping their own tables
+    // every row is its own group instead (same results: grouping is only a sharing
+    // of loads), in natural order.
+    a.own_tables = false;
+    a.group_start = nullptr;
+    a.group_order = nullptr;
+    a.num_groups = num_rows;
+    return dispatch(a, dtype, head_dim, 1, nw);
+  }
   return dispatch(a, dtype, head_dim, meta->max_group_size, nw);
 }
 
@@ -599,7 +637,7 @@ extern "C" int vfl_attention_with_kv_cache(
     int head_dim, int block_size, int64_t num_blocks, float scale, int dtype,
     const vfl_sched_meta *meta, void *stream) {
   clear_error();
-  const KvWrite none = {nullptr, 0, 0, nullptr, 0, 0, nullptr};
+  const KvWrite none = {nullptr, 0, 0, nullptr, 0, 0, nullptr, false};
   return attention_impl(query, query_stride_token, query_stride_head, k_cache, v_cache, out,
                         seq_lens, block_table, block_table_stride, group_start, group_order,
                         num_rows, num_groups, num_heads, head_dim, block_size, num_blocks, scale,
@@ -611,12 +649,18 @@ extern "C" int vfl_self_attention_with_kv_write(
     int64_t key_stride_token, int64_t key_stride_head, const void *value,
     int64_t value_stride_token, int64_t value_stride_head, const int64_t *slot_mapping,
     void *k_cache, void *v_cache, void *out, const int32_t *seq_lens,
-    const int32_t *block_table, int64_t block_table_stride, const int32_t *group_order,
-    int64_t num_rows, int num_heads, int head_dim, int block_size, int64_t num_blocks,
-    float scale, int dtype, const vfl_sched_meta *meta, void *stream) {
+    const int32_t *block_table, int64_t block_table_stride, const int32_t *group_start,
+    const int32_t *group_order, int64_t num_rows, int64_t num_groups, int num_heads,
+    int head_dim, int block_size, int64_t num_blocks, float scale, int dtype,
+    const vfl_sched_meta *meta, void *stream) {
   clear_error();
   if (num_rows > 0 && (!key || !value || !slot_mapping)) {
     set_error("self_attention_with_kv_write: null key, value or slot_mapping");
+    return VFL_E_INVALID;
+  }
+  if (group_start != nullptr && (meta == nullptr || meta->group_tables != VFL_GROUP_OWN_TABLES)) {
+    set_error("self_attention_with_kv_write: row groups need metadata made with "
+              "VFL_GROUP_OWN_TABLES (every row keeps its own block table)");
     return VFL_E_INVALID;
   }
   if (dtype == VFL_FLOAT32) {
@@ -628,16 +672,19 @@ extern "C" int vfl_self_attention_with_kv_write(
     if (st != VFL_OK) return st;
     return vfl_attention_with_kv_cache(query, query_stride_token, query_stride_head, k_cache,
                                        v_cache, out, seq_lens, block_table, block_table_stride,
-                                       nullptr, group_order, num_rows, num_rows, num_heads,
-                                       head_dim, block_size, num_blocks, scale, dtype, meta,
-                                       stream);
+                                       group_start, group_order, num_rows, num_groups,
+                                       num_heads, head_dim, block_size, num_blocks, scale, dtype,
+                                       meta, stream);
   }
+  const bool vec = (uintptr_t)key % 16 == 0 && key_stride_token % 8 == 0 &&
+                   key_stride_head % 8 == 0 && (uintptr_t)value % 16 == 0 &&
+                   value_stride_token % 8 == 0 && value_stride_head % 8 == 0;
   const KvWrite kvw = {(const uint16_t *)key, key_stride_token, key_stride_head,
                        (const uint16_t *)value, value_stride_token, value_stride_head,
-                       slot_mapping};
+                       slot_mapping, vec};
   if (num_rows == 0) return VFL_OK;
   return attention_impl(query, query_stride_token, query_stride_head, k_cache, v_cache, out,
-                        seq_lens, block_table, block_table_stride, nullptr, group_order,
-                        num_rows, num_rows, num_heads, head_dim, block_size, num_blocks, scale,
+                        seq_lens, block_table, block_table_stride, group_start, group_order,
+                        num_rows, num_groups, num_heads, head_dim, block_size, num_blocks, scale,
                         dtype, meta, stream, kvw, "self_attention_with_kv_write");
 }

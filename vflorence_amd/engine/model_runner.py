@@ -47,15 +47,15 @@ class _StepBuffers:
 
     int32 word layout for ``rows`` sequences and tables ``width`` blocks wide:
     six int64 vectors of ``rows`` (token ids, positions, slots, copy sources, copy
-    destinations, lengths), then int32 context lengths, dispatch order and the
-    ``[rows, width]`` block tables.
+    destinations, lengths), then int32 context lengths, dispatch order, the row groups'
+    starts (``rows + 1``) and the ``[rows, width]`` block tables.
     """
 
     I64 = ("input_ids", "positions", "slots", "copy_src", "copy_dst", "lengths")
 
     def __init__(self, rows: int, width: int, device):
         self.rows, self.width = rows, width
-        words = 12 * rows + 2 * rows + rows * width
+        words = 12 * rows + 3 * rows + 1 + rows * width
         self.host = torch.zeros(words, dtype=torch.int32, pin_memory=True)
         self.dev = torch.zeros(words, dtype=torch.int32, device=device)
         self.copied = torch.cuda.Event()
@@ -70,12 +70,25 @@ class _StepBuffers:
                for i, name in enumerate(self.I64)}
         out["context_lens"] = buf[12 * r: 13 * r]
         out["order"] = buf[13 * r: 14 * r]
-        out["tables"] = buf[14 * r: 14 * r + r * w].view(r, w)
+        out["group_start"] = buf[14 * r: 15 * r + 1]
+        out["tables"] = buf[15 * r + 1: 15 * r + 1 + r * w].view(r, w)
         return out
 
     def upload(self) -> None:
         self.dev.copy_(self.host, non_blocking=True)
         self.copied.record()
+
+
+def _row_groups(seqs, max_group: int) -> list[int]:
+    """Starts of the runs of rows that belong to one request (its beams, adjacent in the
+    running list, vflorence/engine/scheduler.py:121-126), cut every ``max_group`` rows,
+    followed by the row count."""
+    starts = [0]
+    for i in range(1, len(seqs)):
+        if seqs[i].request_id != seqs[i - 1].request_id or i - starts[-1] >= max_group:
+            starts.append(i)
+    starts.append(len(seqs))
+    return starts
 
 
 def _merge_equal_beam_groups(seqs, scores, ids, keep: int):
@@ -137,7 +150,8 @@ class ModelRunner:
         self._cross_buffers = attention.CrossStagingBuffers(
             config.max_num_seqs, math.ceil(config.max_encoder_len / self.block_size), self.device)
         # decode steps captured per batch size (rows), replayed while the shapes repeat
-        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self._graphs: dict[tuple[int, bool], tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self._step_grouped = False
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
 
     # -- pools -------------------------------------------------------------------------
@@ -255,6 +269,16 @@ class ModelRunner:
         lens = [p + 1 for p in positions]
         h["context_lens"][:n] = lens
         h["order"][:n] = hip_attn.longest_first(lens)
+        # Beams of a request share their prefix blocks (copy-on-write forks): their
+        # self-attention runs as one row group that reads each shared block once.  The
+        # group list is padded with empty groups to n entries so that one launch shape
+        # serves every batch of n rows.
+        starts = _row_groups(seqs, hip_attn.MAX_GROUP_SIZE)
+        num_groups = len(starts) - 1
+        grouped = num_groups < n
+        if grouped:
+            h["group_start"][: num_groups + 1] = starts
+            h["group_start"][num_groups + 1: n + 1] = n
         tables = h["tables"]
         for i, seq in enumerate(seqs):
             tables[i, : len(seq.block_table)] = seq.block_table
@@ -267,10 +291,18 @@ class ModelRunner:
         d = buf.d
         # copy-on-write first: this step writes into the now-private blocks
         self._copy_blocks(copies, d["copy_src"][: len(copies)], d["copy_dst"][: len(copies)])
-        self_metadata = hip_attn.get_scheduler_metadata(
-            num_reqs=n, num_heads=self.num_heads, num_kv_heads=self.num_heads,
-            head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
-            group_order=d["order"][:n], fuse_kv_write=True)
+        if grouped:
+            self_metadata = hip_attn.get_scheduler_metadata(
+                num_reqs=n, num_heads=self.num_heads, num_kv_heads=self.num_heads,
+                head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
+                group_start=d["group_start"][: n + 1], max_group_size=hip_attn.MAX_GROUP_SIZE,
+                own_tables=True, fuse_kv_write=True)
+        else:
+            self_metadata = hip_attn.get_scheduler_metadata(
+                num_reqs=n, num_heads=self.num_heads, num_kv_heads=self.num_heads,
+                head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
+                group_order=d["order"][:n], fuse_kv_write=True)
+        self._step_grouped = grouped
         request_ids = tuple(seq.request_id for seq in seqs)
         if request_ids != self._cross_key:
             pages, enc_lens = zip(*(self._cross_pages[rid] for rid in request_ids))
@@ -394,7 +426,8 @@ class ModelRunner:
         if not self.config.cuda_graphs:
             return self.model(input_ids, positions)
         n = input_ids.shape[0]
-        entry = self._graphs.get(n)
+        key = (n, self._step_grouped)  # grouped steps launch another kernel
+        entry = self._graphs.get(key)
         if entry is None:
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
@@ -404,7 +437,7 @@ class ModelRunner:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, pool=self._graph_pool):
                 logits = self.model(input_ids, positions)
-            entry = self._graphs[n] = (graph, logits)
+            entry = self._graphs[key] = (graph, logits)
         graph, logits = entry
         graph.replay()
         return logits

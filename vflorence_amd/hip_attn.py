@@ -34,6 +34,9 @@ MAX_GROUP_SIZE = 8
 # beat four on both short decode-step contexts and 256 ragged rows up to 1024 tokens).
 FUSED_WAVES = 2
 FUSED_ONE_WAVE_BLOCKS = 4
+# Waves per workgroup of the fused launch over own-table row groups (beams): measured
+# best from 1 to 8 blocks of context (64 x 4 beams, MI355X); more waves cost occupancy.
+FUSED_GROUP_WAVES = 2
 
 
 def _pow2_at_least(n: int) -> int:
@@ -163,11 +166,16 @@ class SchedulerMetadata:
     """Launch plan for ``attention_with_kv_cache``: the GPU stand-in for the opaque
     tensor ``vllm_cpu_attn.get_scheduler_metadata`` returns.
 
-    ``group_start`` (device int32 [num_groups + 1]) lists row groups that share one
-    block-table row -- the beams of a request in cross-attention -- so their K/V is
-    read once.  ``group_order`` (device int32 [num_groups]) is the dispatch order,
-    longest context first.  The launch shape is fixed at call time from the block
-    table's width, which the host always knows, so no device value is read back.
+    ``group_start`` (device int32 [num_groups + 1]) lists row groups -- the beams of a
+    request.  Without ``own_tables`` a group's rows share one block-table row and
+    length (cross-attention over one encoder page list) and its K/V is read once.  With
+    ``own_tables`` every row keeps its own table and length, and a block that several
+    rows of a group list at the same position is read once for all of them (decoder
+    self-attention, where copy-on-write forks share prefix blocks); any partition of
+    the rows gives the same results.  ``group_order`` (device int32 [num_groups]) is
+    the dispatch order, longest context first.  The launch shape is fixed at call time
+    from the block table's width, which the host always knows, so no device value is
+    read back.
     """
 
     num_heads: int
@@ -179,6 +187,7 @@ class SchedulerMetadata:
     num_groups: int | None = None
     max_group_size: int = 1
     waves_per_workgroup: int = 0
+    own_tables: bool = False
     # The caller's promise that each row writes its new token at the slot of its last
     # context position, in a block no other row reads (the block manager's
     # copy-on-write invariant); lets the self-attention op fuse the KV write.
@@ -193,15 +202,19 @@ class SchedulerMetadata:
             groups = num_rows if self.group_start is None else self.num_groups
             waves = self.waves_per_workgroup
             if waves == 0 and self.fuse_kv_write:
-                # measured best for the fused write + attention kernel (MI355X, bf16, 256
-                # rows x 16 heads): one wave up to 4 blocks of context (a decode step's
-                # short contexts are latency-bound; more waves only add a merge), two
-                # beyond (ragged contexts up to 1024 tokens)
-                waves = 1 if max_blocks <= FUSED_ONE_WAVE_BLOCKS else FUSED_WAVES
+                if self.own_tables and self.group_start is not None:
+                    waves = FUSED_GROUP_WAVES
+                else:
+                    # measured best for the fused write + attention kernel (MI355X, bf16,
+                    # 256 rows x 16 heads): one wave up to 4 blocks of context (a decode
+                    # step's short contexts are latency-bound; more waves only add a
+                    # merge), two beyond (ragged contexts up to 1024 tokens)
+                    waves = 1 if max_blocks <= FUSED_ONE_WAVE_BLOCKS else FUSED_WAVES
             check(
                 lib.vfl_get_scheduler_metadata(
                     num_rows, groups, self.num_heads, self.head_dim, self.block_size,
                     max_blocks, self.max_group_size, _dtype_code(self.dtype), waves,
+                    _lib.VFL_GROUP_OWN_TABLES if self.own_tables else _lib.VFL_GROUP_SHARED_TABLE,
                     ctypes.byref(meta),
                 )
             )
@@ -232,12 +245,13 @@ def get_scheduler_metadata(
     max_group_size: int = 1,
     waves_per_workgroup: int = 0,
     fuse_kv_write: bool = False,
+    own_tables: bool = False,
 ) -> SchedulerMetadata:
     """Counterpart of ``vllm_cpu_attn.get_scheduler_metadata`` (keyword names from
     vflorence/layers/attention.py:18-29 and vflorence/engine/model_runner.py:308-319).
 
-    ``group_start``/``group_order``/``max_group_size``/``waves_per_workgroup`` are this
-    library's additions.  ``seq_lens``, ``query_start_loc``, ``causal`` and ``isa`` are
+    ``group_start``/``group_order``/``max_group_size``/``waves_per_workgroup``/
+    ``own_tables`` are this library's additions.  ``seq_lens``, ``query_start_loc``, ``causal`` and ``isa`` are
     accepted for signature compatibility; the plan does not need them (callers that
     know the lengths on the host pass ``group_order`` instead).
     """
@@ -270,6 +284,7 @@ def get_scheduler_metadata(
         max_group_size=max_group_size,
         waves_per_workgroup=waves_per_workgroup,
         fuse_kv_write=fuse_kv_write,
+        own_tables=own_tables,
     )
 
 
@@ -373,8 +388,8 @@ def self_attention_with_kv_write(
     sm = scheduler_metadata
     if not sm.fuse_kv_write:
         raise ValueError("self_attention_with_kv_write needs metadata made with fuse_kv_write=True")
-    if sm.group_start is not None:
-        raise ValueError("the fused self-attention path takes one row per group")
+    if sm.group_start is not None and not sm.own_tables:
+        raise ValueError("the fused self-attention path groups rows only with own_tables=True")
     dev = _require_gpu(query, key, value, k_cache, v_cache, out, seq_lens, slot_mapping,
                        block_table)
     if key.dim() != 3 or value.shape != key.shape or key.shape != query.shape:
@@ -403,8 +418,11 @@ def self_attention_with_kv_write(
         block_table = block_table.contiguous()
     seq_lens = seq_lens.contiguous()
     slot_mapping = slot_mapping.contiguous()
+    if sm.group_start is not None:
+        _require_gpu(query, sm.group_start)
     if sm.group_order is not None:
         _require_gpu(query, sm.group_order)
+    num_groups = num_rows if sm.group_start is None else sm.num_groups
     meta = sm.plan(num_rows, block_table.shape[1])
     check(
         lib.vfl_self_attention_with_kv_write(
@@ -412,8 +430,9 @@ def self_attention_with_kv_write(
             key.stride(1), value.data_ptr(), value.stride(0), value.stride(1),
             slot_mapping.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
             seq_lens.data_ptr(), block_table.data_ptr(), block_table.stride(0),
-            None if sm.group_order is None else sm.group_order.data_ptr(), num_rows, num_heads,
-            head_dim, block_size, num_blocks, float(scale), _dtype_code(query.dtype),
+            None if sm.group_start is None else sm.group_start.data_ptr(),
+            None if sm.group_order is None else sm.group_order.data_ptr(), num_rows, num_groups,
+            num_heads, head_dim, block_size, num_blocks, float(scale), _dtype_code(query.dtype),
             ctypes.byref(meta), _stream(dev),
         )
     )

@@ -182,6 +182,28 @@ def self_attention_bytes(context_lens: list[int], num_heads: int, head_dim: int,
             + sum(4 * math.ceil(L / block_size) for L in context_lens) + 12 * N)
 
 
+def shared_self_attention_bytes(block_tables: list[list[int]], context_lens: list[int],
+                                group_size: int, num_heads: int, head_dim: int,
+                                elem_bytes: int, block_size: int = 16) -> int:
+    """self_attention_bytes for rows taken in groups of ``group_size`` whose tables may
+    list the same blocks (the beams of a request after copy-on-write forks): a block
+    that several rows of a group list at one position is read once, for the most
+    tokens any of those rows uses from it."""
+    N = len(context_lens)
+    row = num_heads * head_dim * elem_bytes
+    tokens = 0
+    for g0 in range(0, N, group_size):
+        used: dict[tuple[int, int], int] = {}
+        for r in range(g0, min(N, g0 + group_size)):
+            L = context_lens[r]
+            for i in range(math.ceil(L / block_size)):
+                key = (i, block_tables[r][i])
+                used[key] = max(used.get(key, 0), min(block_size, L - block_size * i))
+        tokens += sum(used.values())
+    return (2 * tokens * row + 2 * N * row + 4 * N * row
+            + sum(4 * math.ceil(L / block_size) for L in context_lens) + 12 * N)
+
+
 def cross_attention_bytes(enc_lens_per_group: list[int], num_rows: int, num_heads: int,
                           head_dim: int, elem_bytes: int, block_size: int = 16) -> int:
     """Algorithmic HBM bytes of one cross-attention call: each request's encoder K/V
