@@ -196,6 +196,78 @@ def test_block_manager_invariants_under_random_forks():
     assert bm.num_free_blocks == 64 and not any(bm.ref_counts)
 
 
+class _ForkAllScheduler(Scheduler):
+    """The reference's beam bookkeeping verbatim in effect: fork every live child from
+    its parent, then deallocate every parent (vflorence/engine/scheduler.py:120-126)."""
+
+    def _postprocess_beam(self, seqs, candidates_by_request):
+        outputs = []
+        for request_id, candidates in candidates_by_request.items():
+            sp = candidates[0][0].sampling_params
+            finished = self._finished_beams[request_id]
+            live = []
+            for rank, (parent, token, cum) in enumerate(candidates):
+                if rank >= sp.num_beams and len(live) >= sp.num_beams:
+                    break
+                child = parent.fork(token, cum)
+                if token in sp.eos_ids() or child.num_generated >= sp.max_tokens:
+                    if rank < sp.num_beams:
+                        finished.append(child)
+                elif len(live) < sp.num_beams:
+                    live.append((parent, child))
+            finished.sort(key=lambda q: q.score, reverse=True)
+            del finished[sp.num_beams:]
+            best = max((c.score for _, c in live), default=float("-inf"))
+            if not live or (len(finished) >= sp.num_beams and (
+                    sp.early_stopping or finished[-1].score >= best)):
+                self._finished_beams.pop(request_id, None)
+                outputs.append((request_id, finished[0].to_output()))
+            else:
+                for parent, child in live:
+                    self.block_manager.fork(parent, child)
+                    self.running.append(child)
+        for seq in seqs:
+            self.running.remove(seq)
+            self.block_manager.deallocate(seq)
+        return outputs
+
+
+def test_beam_table_handover_keeps_the_reference_block_state():
+    """Handing a parent's table to its first live child instead of fork + deallocate
+    leaves every step's block tables, copy-on-write pairs, reference counts and free
+    list (order included) identical to forking every child."""
+    import random
+
+    def run(cls, seed):
+        rng = random.Random(seed)
+        params = SamplingParams(num_beams=4, max_tokens=60, eos_token_id=[2],
+                                early_stopping=False).with_defaults(defaults())
+        sched = cls(SimpleNamespace(max_num_seqs=24, num_blocks=160, block_size=16))
+        for r in range(6):
+            sched.add(Sequence(r, [1], [3], params))
+        trace = []
+        while not sched.is_finished():
+            seqs, copies = sched.schedule()
+            bm = sched.block_manager
+            trace.append(([list(s.block_table) for s in seqs], list(copies),
+                          list(bm.ref_counts), list(bm.free_block_ids)))
+            cands = {}
+            for s in seqs:
+                row = []
+                for _ in range(3):  # a few children per parent, EOS now and then
+                    tok = 2 if rng.random() < 0.03 else rng.randrange(3, 50)
+                    row.append((s, tok, s.cum_logprob - rng.random()))
+                cands.setdefault(s.request_id, []).extend(row)
+            for rid in cands:
+                cands[rid].sort(key=lambda c: -c[2])
+            outs = sched.postprocess(seqs, cands)
+            trace.append(sorted((rid, o.completion_token_ids) for rid, o in outs))
+        return trace
+
+    for seed in range(4):
+        assert run(Scheduler, seed) == run(_ForkAllScheduler, seed)
+
+
 def test_synthetic_checkpoint_is_deterministic_and_loads_into_transformers():
     from transformers import BartConfig, BartForConditionalGeneration
 

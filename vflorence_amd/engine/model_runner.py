@@ -79,6 +79,16 @@ class _StepBuffers:
         self.copied.record()
 
 
+def _to_host(*tensors: torch.Tensor) -> list[torch.Tensor]:
+    """Device tensors copied to host memory with one synchronisation."""
+    out = [torch.empty(t.shape, dtype=t.dtype, pin_memory=t.is_cuda) for t in tensors]
+    for o, t in zip(out, tensors):
+        o.copy_(t, non_blocking=True)
+    if any(t.is_cuda for t in tensors):
+        torch.cuda.current_stream().synchronize()
+    return out
+
+
 def _row_groups(seqs, max_group: int) -> list[int]:
     """Starts of the runs of rows that belong to one request (its beams, adjacent in the
     running list, vflorence/engine/scheduler.py:121-126), cut every ``max_group`` rows,
@@ -109,16 +119,15 @@ def _merge_equal_beam_groups(seqs, scores, ids, keep: int):
     heads = rids[::nb]
     if len(set(heads)) != len(heads) or any(rids[i] != rids[i - i % nb] for i in range(n)):
         return None
-    flat = scores.reshape(n // nb, nb * k)
+    groups = n // nb
+    flat = scores.reshape(groups, nb * k)
     order = np.argsort(-flat, axis=1, kind="stable")[:, :keep]
-    out = {}
-    for j, rid in enumerate(heads):
-        base = j * nb
-        sel = order[j].tolist()
-        vals = flat[j, order[j]].tolist()
-        out[rid] = [(seqs[base + f // k], int(ids[base + f // k, f % k]), v)
-                    for f, v in zip(sel, vals)]
-    return out
+    rows = order // k + (np.arange(groups) * nb)[:, None]
+    toks = ids[rows, order % k].tolist()
+    vals = np.take_along_axis(flat, order, axis=1).tolist()
+    rows = rows.tolist()
+    return {rid: [(seqs[r], t, v) for r, t, v in zip(rows[j], toks[j], vals[j])]
+            for j, rid in enumerate(heads)}
 
 
 class ModelRunner:
@@ -268,7 +277,6 @@ class ModelRunner:
                           for seq, p in zip(seqs, positions)]
         lens = [p + 1 for p in positions]
         h["context_lens"][:n] = lens
-        h["order"][:n] = hip_attn.longest_first(lens)
         # Beams of a request share their prefix blocks (copy-on-write forks): their
         # self-attention runs as one row group that reads each shared block once.  The
         # group list is padded with empty groups to n entries so that one launch shape
@@ -279,10 +287,10 @@ class ModelRunner:
         if grouped:
             h["group_start"][: num_groups + 1] = starts
             h["group_start"][num_groups + 1: n + 1] = n
-        tables = h["tables"]
-        for i, seq in enumerate(seqs):
-            tables[i, : len(seq.block_table)] = seq.block_table
-            tables[i, len(seq.block_table):] = 0
+        else:  # one row per workgroup: longest context first
+            h["order"][:n] = hip_attn.longest_first(lens)
+        w = buf.width
+        h["tables"][:n] = [seq.block_table + [0] * (w - len(seq.block_table)) for seq in seqs]
         if copies:
             h["copy_src"][: len(copies)] = [s for s, _ in copies]
             h["copy_dst"][: len(copies)] = [d for _, d in copies]
@@ -382,8 +390,7 @@ class ModelRunner:
     def _merge_candidates(seqs, top_scores, top_ids, keep: int) -> dict[int, list]:
         """Add each row's cumulative log-prob to its top-k and keep every request's best
         ``keep`` candidates over its rows, best first."""
-        top_scores = top_scores.float().cpu()
-        top_ids = top_ids.cpu()
+        top_scores, top_ids = _to_host(top_scores.float(), top_ids)
         top_scores += torch.tensor([s.cum_logprob for s in seqs], dtype=torch.float32).unsqueeze(-1)
         fast = _merge_equal_beam_groups(seqs, top_scores.numpy(), top_ids.numpy(), keep)
         if fast is not None:

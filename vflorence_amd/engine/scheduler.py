@@ -111,8 +111,20 @@ class Scheduler:
                 self._finished_beams.pop(request_id, None)
                 outputs.append((request_id, finished[0].to_output()))
             else:
+                # A parent's first live child takes over its block table; further
+                # children fork from that child.  The reference forks every child and
+                # then deallocates every parent (scheduler.py:120-126): per block that
+                # is +1 per child and -1 per parent, so the reference counts, the blocks
+                # freed below and their order come out the same.
+                holder: dict[int, Sequence] = {}
                 for parent, child in live:
-                    self.block_manager.fork(parent, child)
+                    owner = holder.get(id(parent))
+                    if owner is None:
+                        child.block_table = parent.block_table
+                        parent.block_table = []
+                        holder[id(parent)] = child
+                    else:
+                        self.block_manager.fork(owner, child)
                     self.running.append(child)
         # retire every parent: blocks freed in step order, one pass over ``running``
         for seq in seqs:
