@@ -127,19 +127,22 @@ def test_prepare_and_encode_follow_the_reference_formulas(small_engine):
                 seq.block_table.append(bm._allocate_block())
         ids, pos = runner._prepare(seqs)
         ctx = get_context()
+        # three sequences padded to the 4-row bucket: the padding row feeds token 0 at
+        # position 0, has an empty context and writes no slot
+        assert pos.shape[0] == ids.shape[0] == ctx.context_lens.shape[0] == 4
         want_pos = [s.num_cached_tokens for s in seqs]
-        assert pos.tolist() == want_pos
-        assert ids.tolist() == [s.token_ids[p] for s, p in zip(seqs, want_pos)]
-        assert ctx.context_lens.tolist() == [p + 1 for p in want_pos]
+        assert pos.tolist() == want_pos + [0]
+        assert ids.tolist() == [s.token_ids[p] for s, p in zip(seqs, want_pos)] + [0]
+        assert ctx.context_lens.tolist() == [p + 1 for p in want_pos] + [0]
         assert ctx.slot_mapping.tolist() == [s.block_table[p // 16] * 16 + p % 16
-                                             for s, p in zip(seqs, want_pos)]
+                                             for s, p in zip(seqs, want_pos)] + [-1]
         # 0-padded rows at the runner's fixed table width (the kernels read only
         # ceil(len / 16) entries of a row)
         width = ctx.block_tables.shape[1]
         assert width >= max(len(s.block_table) for s in seqs)
         assert ctx.block_tables.tolist() == [s.block_table + [0] * (width - len(s.block_table))
-                                             for s in seqs]
-        assert ctx.query_start_loc.tolist() == list(range(4))
+                                             for s in seqs] + [[0] * width]
+        assert ctx.query_start_loc.tolist() == list(range(5))
         # encoder pages: request i's tokens at pages[t // 16] * 16 + t % 16 hold kv_proj
         layer = runner.decoder_layers[1]
         attn = layer.encoder_attn
@@ -239,4 +242,6 @@ def test_continuous_batching_keeps_each_requests_tokens(graphs):
     assert len(done) == 30 and len(sizes) > 3
     for rid, tokens in done.items():
         assert tokens == c["tokens"][prompt_of[rid]], rid
+    if graphs:  # steps are padded to the row buckets 1, 2, 4, 8: one capture each at most
+        assert len(llm.runner._graphs) <= 4
     assert_clean(llm)

@@ -89,6 +89,18 @@ def _to_host(*tensors: torch.Tensor) -> list[torch.Tensor]:
     return out
 
 
+def row_buckets(max_rows: int) -> list[int]:
+    """Row counts a decode step is padded to: 1, 2, 4, 8, then steps of 8 up to 64, of 16
+    up to 128, of 32 beyond, and ``max_rows`` itself.  A HIP graph is captured once per
+    bucket, so a batch that changes size every step (continuous batching) replays a
+    handful of graphs instead of capturing one per size."""
+    sizes, s = [1, 2, 4, 8], 16
+    while s < max_rows:
+        sizes.append(s)
+        s += 8 if s < 64 else 16 if s < 128 else 32
+    return [b for b in sizes if b < max_rows] + [max_rows]
+
+
 def _row_groups(seqs, max_group: int) -> list[int]:
     """Starts of the runs of rows that belong to one request (its beams, adjacent in the
     running list, vflorence/engine/scheduler.py:121-126), cut every ``max_group`` rows,
@@ -161,6 +173,8 @@ class ModelRunner:
         # decode steps captured per batch size (rows), replayed while the shapes repeat
         self._graphs: dict[tuple[int, bool], tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self._step_grouped = False
+        self._buckets = row_buckets(config.max_num_seqs)
+        self._no_pages = torch.zeros(0, dtype=torch.int32)
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
 
     # -- pools -------------------------------------------------------------------------
@@ -254,7 +268,10 @@ class ModelRunner:
     def _prepare(self, seqs, copies=()):
         """Stage the step's metadata in HBM, run the copy-on-write, publish the Context.
 
-        Returns the device ``(input_ids, positions)`` of the one token fed per sequence.
+        Returns the device ``(input_ids, positions)`` of the one token fed per sequence,
+        padded to the step's row bucket (``row_buckets``): padding rows feed token 0 at
+        position 0 with a zero-length context and write no KV slot, so the rows of the
+        real sequences come out as without padding and their logits are the first rows.
         """
         bs = self.block_size
         for seq in seqs:
@@ -262,10 +279,12 @@ class ModelRunner:
             if num_new != 1:
                 raise ValueError(f"each step must feed 1 token per sequence, got {num_new}")
         n = len(seqs)
+        # rows n .. padded-1 are padding: no token written, zero-length contexts
+        padded = next((b for b in self._buckets if b >= n), n)
         buf = self._buffers
         width = max(len(seq.block_table) for seq in seqs)
-        if n > buf.rows or width > buf.width or len(copies) > buf.rows:
-            buf = self._buffers = _StepBuffers(max(n, len(copies), buf.rows),
+        if padded > buf.rows or width > buf.width or len(copies) > buf.rows:
+            buf = self._buffers = _StepBuffers(max(padded, len(copies), buf.rows),
                                                max(width, buf.width), self.device)
             self._graphs.clear()  # they read the old buffers
         buf.copied.synchronize()  # the previous step's upload has left the staging
@@ -277,18 +296,24 @@ class ModelRunner:
                           for seq, p in zip(seqs, positions)]
         lens = [p + 1 for p in positions]
         h["context_lens"][:n] = lens
+        if padded > n:
+            for name, value in (("input_ids", 0), ("positions", 0), ("slots", -1),
+                                ("context_lens", 0), ("lengths", 1)):
+                h[name][n:padded] = value
+            h["tables"][n:padded] = 0
         # Beams of a request share their prefix blocks (copy-on-write forks): their
         # self-attention runs as one row group that reads each shared block once.  The
         # group list is padded with empty groups to n entries so that one launch shape
         # serves every batch of n rows.
         starts = _row_groups(seqs, hip_attn.MAX_GROUP_SIZE)
-        num_groups = len(starts) - 1
-        grouped = num_groups < n
-        if grouped:
+        grouped = len(starts) - 1 < n
+        if grouped:  # padding rows are groups of one (zero output)
+            starts += range(n + 1, padded + 1)
+            num_groups = len(starts) - 1
             h["group_start"][: num_groups + 1] = starts
-            h["group_start"][num_groups + 1: n + 1] = n
+            h["group_start"][num_groups + 1: padded + 1] = padded
         else:  # one row per workgroup: longest context first
-            h["order"][:n] = hip_attn.longest_first(lens)
+            h["order"][:padded] = hip_attn.longest_first(lens + [0] * (padded - n))
         w = buf.width
         h["tables"][:n] = [seq.block_table + [0] * (w - len(seq.block_table)) for seq in seqs]
         if copies:
@@ -301,32 +326,34 @@ class ModelRunner:
         self._copy_blocks(copies, d["copy_src"][: len(copies)], d["copy_dst"][: len(copies)])
         if grouped:
             self_metadata = hip_attn.get_scheduler_metadata(
-                num_reqs=n, num_heads=self.num_heads, num_kv_heads=self.num_heads,
+                num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
                 head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
-                group_start=d["group_start"][: n + 1], max_group_size=hip_attn.MAX_GROUP_SIZE,
-                own_tables=True, fuse_kv_write=True)
+                group_start=d["group_start"][: padded + 1],
+                max_group_size=hip_attn.MAX_GROUP_SIZE, own_tables=True, fuse_kv_write=True)
         else:
             self_metadata = hip_attn.get_scheduler_metadata(
-                num_reqs=n, num_heads=self.num_heads, num_kv_heads=self.num_heads,
+                num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
                 head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
-                group_order=d["order"][:n], fuse_kv_write=True)
+                group_order=d["order"][:padded], fuse_kv_write=True)
         self._step_grouped = grouped
-        request_ids = tuple(seq.request_id for seq in seqs)
+        request_ids = tuple(seq.request_id for seq in seqs) + (None,) * (padded - n)
         if request_ids != self._cross_key:
-            pages, enc_lens = zip(*(self._cross_pages[rid] for rid in request_ids))
+            pages, enc_lens = zip(*(self._cross_pages[rid] for rid in request_ids[:n]))
+            pages = pages + (self._no_pages,) * (padded - n)
+            enc_lens = enc_lens + (0,) * (padded - n)
             self._cross_staged = attention.stage_cross(self.decoder_layers, pages, enc_lens, bs,
                                                        self.isa, buffers=self._cross_buffers)
             self._cross_key = request_ids
         set_context(
-            context_lens=d["context_lens"][:n],
-            block_tables=d["tables"][:n],
-            slot_mapping=d["slots"][:n],
-            query_start_loc=self._query_start_loc[: n + 1],
+            context_lens=d["context_lens"][:padded],
+            block_tables=d["tables"][:padded],
+            slot_mapping=d["slots"][:padded],
+            query_start_loc=self._query_start_loc[: padded + 1],
             self_metadata=self_metadata,
             isa=self.isa,
             cross_staged=self._cross_staged,
         )
-        return d["input_ids"][:n], d["positions"][:n]
+        return d["input_ids"][:padded], d["positions"][:padded]
 
     # -- sampling ----------------------------------------------------------------------
 
@@ -418,7 +445,8 @@ class ModelRunner:
             logits = self._forward(input_ids, positions)
         finally:
             set_context()
-        return self._sample(seqs, logits, self._buffers.d["lengths"][: len(seqs)])
+        n = len(seqs)  # the rows past n are padding
+        return self._sample(seqs, logits[:n], self._buffers.d["lengths"][:n])
 
     def _forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         """The decoder step, eager or replayed from a HIP graph of this batch size.
