@@ -40,6 +40,12 @@ SMALL = dict(vocab_size=96, d_model=128, encoder_layers=2, decoder_layers=2,
 # tied head scores the token just fed far above the rest (the residual stream keeps its
 # embedding), so generation would echo the start token, which is EOS, and stop at once.
 LARGE = dict(forced_eos_token_id=None, tie_word_embeddings=False)
+# Florence-2-base's text model is a BART of these sizes; its decoder reads 577 visual
+# tokens plus a 10-token prompt, stood in for here by 587 encoder token ids.
+FLORENCE_BASE = dict(vocab_size=51289, d_model=768, encoder_layers=6, decoder_layers=6,
+                     encoder_attention_heads=12, decoder_attention_heads=12,
+                     encoder_ffn_dim=3072, decoder_ffn_dim=3072, max_position_embeddings=1024,
+                     forced_eos_token_id=None, tie_word_embeddings=False)
 
 # every field set explicitly: nothing is inherited from a generation config
 BASE = dict(max_tokens=24, num_beams=1, repetition_penalty=1.0, eos_token_id=[2],
@@ -99,6 +105,17 @@ def build(config_kwargs: dict):
     return config, model, state_dict_checksum(sd)
 
 
+def florence2_base() -> dict:
+    config, model, checksum = build(FLORENCE_BASE)
+    reqs = prompts(config.vocab_size, [587] * 6, seed=4)
+    params = {**BASE, "max_tokens": 32}
+    outs = [hf_generate(model, ids, params) for ids in reqs]
+    print("florence2_base", [len(t) for t, _ in outs], flush=True)
+    return {"config": FLORENCE_BASE, "checksum": checksum, "prompts": reqs,
+            "cases": {"greedy32": {"params": params, "tokens": [t for t, _ in outs],
+                                   "min_gap": [gp for _, gp in outs]}}}
+
+
 def main():
     torch.set_num_threads(min(8, os.cpu_count() or 1))
     fixtures = {"_provenance": (
@@ -132,6 +149,7 @@ def main():
                               "cases": {"greedy64": {"params": params,
                                                      "tokens": [t for t, _ in outs],
                                                      "min_gap": [gp for _, gp in outs]}}}
+    fixtures["florence2_base"] = florence2_base()
     with open(OUT, "w") as f:
         json.dump(fixtures, f)
     print("wrote", OUT)

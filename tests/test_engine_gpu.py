@@ -245,3 +245,92 @@ def test_continuous_batching_keeps_each_requests_tokens(graphs):
     if graphs:  # steps are padded to the row buckets 1, 2, 4, 8: one capture each at most
         assert len(llm.runner._graphs) <= 4
     assert_clean(llm)
+
+
+@pytest.mark.parametrize("graphs", [False, True], ids=["eager", "hipgraph"])
+def test_tokens_match_transformers_florence2_base_shape_fp32(graphs):
+    """Florence-2-base text-model shapes (6+6 layers, 12 heads x 64, vocab 51289), fp32,
+    six requests reading 587 encoder tokens (577 visual + 10 prompt tokens in Florence-2),
+    32 greedy tokens each, batched."""
+    from vflorence_amd import Request, SamplingParams
+
+    fx = fixtures()["florence2_base"]
+    c = fx["cases"]["greedy32"]
+    assert all(g > 1e-4 for g in c["min_gap"])
+    llm = engine(fx["config"], fx["checksum"], max_num_seqs=6, dtype=torch.float32,
+                 max_decoder_len=32, max_encoder_len=587, cuda_graphs=graphs)
+    outs = llm.generate([Request(p) for p in fx["prompts"]], SamplingParams(**c["params"]))
+    assert [o.completion_token_ids for o in outs] == c["tokens"]
+    assert_clean(llm)
+
+
+def test_florence2_base_shape_3beam_bf16_hip_graph_equals_eager():
+    """The Florence-2-base workload shape in bf16 with 3 beams: 18 rows in beam groups of
+    three (padded to the 24-row bucket), cross-attention groups of three over 587 encoder
+    tokens; graph replays give the tokens of eager steps."""
+    from vflorence_amd import Request, SamplingParams
+
+    fx = fixtures()["florence2_base"]
+    params = SamplingParams(max_tokens=24, num_beams=3, eos_token_id=[2], length_penalty=1.0,
+                            early_stopping=False, min_length=0, repetition_penalty=1.0,
+                            no_repeat_ngram_size=0)
+    got = []
+    for graphs in (False, True):
+        llm = engine(fx["config"], fx["checksum"], max_num_seqs=18, dtype=torch.bfloat16,
+                     max_decoder_len=32, max_encoder_len=587, cuda_graphs=graphs)
+        outs = llm.generate([Request(p) for p in fx["prompts"]], params)
+        assert all(1 <= len(o.completion_token_ids) <= 24 for o in outs)
+        got.append([o.completion_token_ids for o in outs])
+        assert_clean(llm)
+    assert got[0] == got[1]
+
+
+def test_continuous_batching_stress_florence2_large_shape():
+    """The continuous-batching stress workload's shape: Florence-2-large text decoder
+    (12+12 layers, d_model 1024, 16 heads, vocab 51289), bf16, up to 512 running
+    sequences, requests arriving as a seeded Poisson process with encoder lengths from a
+    50/50 mix of 587 and U[64, 1024] and output lengths geometric (mean 96, cap 256).
+    Active requests share one SamplingParams (the reference requires it,
+    vflorence/engine/llm_engine.py:147), so each request is retired at its drawn length
+    the way a finished one is (scheduler removal + encoder pages released).  The batch
+    changes size from step to step, the graphs stay within the row buckets, every row
+    gets one token per step, and every block and page returns."""
+    from transformers import BartConfig
+
+    from vflorence_amd import LLM, Request, SamplingParams
+    from vflorence_amd.engine.model_runner import row_buckets
+
+    cfg = BartConfig(vocab_size=51289, max_position_embeddings=1024, forced_eos_token_id=None,
+                     tie_word_embeddings=False)
+    llm = LLM(cfg, max_num_seqs=512, dtype=torch.bfloat16, max_decoder_len=256,
+              max_encoder_len=1024, cuda_graphs=True)
+    rng = np.random.default_rng(5)
+    n_req = 600
+    arrive = np.cumsum(rng.poisson(0.4, size=n_req)).tolist()
+    enc = np.where(rng.random(n_req) < 0.5, 587, rng.integers(64, 1025, size=n_req)).tolist()
+    out_len = np.minimum(rng.geometric(1 / 96, size=n_req), 256).tolist()
+    sp = SamplingParams(max_tokens=256, eos_token_id=[cfg.eos_token_id],
+                        suppress_tokens=[cfg.eos_token_id])
+    target, done, sizes, step = {}, {}, set(), 0
+    pending = list(range(n_req))
+    while pending or not llm.is_finished():
+        while pending and arrive[pending[0]] <= step:
+            i = pending.pop(0)
+            ids = rng.integers(3, cfg.vocab_size, size=enc[i]).tolist()
+            target[llm.add_request(Request(ids), sp)] = out_len[i]
+        if not llm.is_finished():
+            before = {s.request_id: s.num_generated for s in llm.scheduler.running}
+            sizes.add(len(before))
+            for rid, out in llm.step():  # reached the 256-token cap: finished by the engine
+                done[rid] = len(out.completion_token_ids)
+            for seq in list(llm.scheduler.running):
+                assert seq.num_generated == before.get(seq.request_id, 0) + 1
+                if seq.num_generated >= target[seq.request_id]:
+                    llm.scheduler.remove(seq)
+                    llm.runner.clear_request(seq.request_id)
+                    done[seq.request_id] = seq.num_generated
+        step += 1
+    assert done == target
+    assert max(sizes) <= 512 and len(sizes) > 50
+    assert len(llm.runner._graphs) <= len(row_buckets(512))
+    assert_clean(llm)
