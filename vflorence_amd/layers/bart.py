@@ -44,7 +44,8 @@ def _activation(name: str):
 
 
 class BartLearnedPositionalEmbedding(nn.Embedding):
-    """Learned positions with BART's offset of 2."""
+    """Learned positions with BART's offset of 2 (read through a view of the table that
+    starts at the offset: no add kernel per step)."""
 
     OFFSET = 2
 
@@ -52,7 +53,7 @@ class BartLearnedPositionalEmbedding(nn.Embedding):
         super().__init__(num_embeddings + self.OFFSET, embedding_dim)
 
     def forward(self, positions: torch.Tensor) -> torch.Tensor:
-        return super().forward(positions + self.OFFSET)
+        return F.embedding(positions, self.weight[self.OFFSET:])
 
 
 class BartScaledWordEmbedding(nn.Embedding):
@@ -61,7 +62,8 @@ class BartScaledWordEmbedding(nn.Embedding):
         self.embed_scale = embed_scale
 
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
-        return super().forward(ids) * self.embed_scale
+        out = super().forward(ids)
+        return out if self.embed_scale == 1.0 else out * self.embed_scale
 
 
 class _Heads(nn.Module):
@@ -198,7 +200,8 @@ class BartDecoder(nn.Module):
         self.layernorm_embedding = nn.LayerNorm(d)
 
     def forward(self, input_ids, positions):
-        h = self.layernorm_embedding(self.embed_tokens(input_ids) + self.embed_positions(positions))
+        h = _residual_norm(self.embed_tokens(input_ids), self.embed_positions(positions),
+                           self.layernorm_embedding)
         for layer in self.layers:
             h = layer(h)
         return h
@@ -238,8 +241,10 @@ class BartForConditionalGeneration(nn.Module):
         return self.model.encoder(encoder_token_ids, positions)
 
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
-        """One decode step: logits [N, vocab] for one token per running sequence."""
-        return self.lm_head(self.model.decoder(input_ids, positions)) + self.final_logits_bias
+        """One decode step: logits [N, vocab] for one token per running sequence (the
+        final logits bias added by the LM-head GEMM itself)."""
+        return F.linear(self.model.decoder(input_ids, positions), self.lm_head.weight,
+                        self.final_logits_bias[0])
 
 
 def fuse_projections(model: nn.Module, state_dict: dict) -> None:
