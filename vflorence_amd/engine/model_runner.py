@@ -79,11 +79,20 @@ class _StepBuffers:
         self.copied.record()
 
 
+_HOST_STAGING: dict[tuple, torch.Tensor] = {}
+
+
 def _to_host(*tensors: torch.Tensor) -> list[torch.Tensor]:
-    """Device tensors copied to host memory with one synchronisation."""
-    out = [torch.empty(t.shape, dtype=t.dtype, pin_memory=t.is_cuda) for t in tensors]
-    for o, t in zip(out, tensors):
+    """Device tensors copied to host memory with one synchronisation (pinned staging
+    kept per shape and dtype; callers use the result before the next call)."""
+    out = []
+    for t in tensors:
+        key = (tuple(t.shape), t.dtype, t.is_cuda)
+        o = _HOST_STAGING.get(key)
+        if o is None:
+            o = _HOST_STAGING[key] = torch.empty(t.shape, dtype=t.dtype, pin_memory=t.is_cuda)
         o.copy_(t, non_blocking=True)
+        out.append(o)
     if any(t.is_cuda for t in tensors):
         torch.cuda.current_stream().synchronize()
     return out
@@ -174,6 +183,7 @@ class ModelRunner:
         self._graphs: dict[tuple[int, bool], tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self._step_grouped = False
         self._buckets = row_buckets(config.max_num_seqs)
+        self._self_metadata: dict[tuple[int, bool], hip_attn.SchedulerMetadata] = {}
         self._no_pages = torch.zeros(0, dtype=torch.int32)
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
 
@@ -287,6 +297,7 @@ class ModelRunner:
             buf = self._buffers = _StepBuffers(max(padded, len(copies), buf.rows),
                                                max(width, buf.width), self.device)
             self._graphs.clear()  # they read the old buffers
+            self._self_metadata.clear()
         buf.copied.synchronize()  # the previous step's upload has left the staging
         h = buf.np
         positions = [seq.num_cached_tokens for seq in seqs]
@@ -324,17 +335,22 @@ class ModelRunner:
         d = buf.d
         # copy-on-write first: this step writes into the now-private blocks
         self._copy_blocks(copies, d["copy_src"][: len(copies)], d["copy_dst"][: len(copies)])
-        if grouped:
-            self_metadata = hip_attn.get_scheduler_metadata(
-                num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
-                head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
-                group_start=d["group_start"][: padded + 1],
-                max_group_size=hip_attn.MAX_GROUP_SIZE, own_tables=True, fuse_kv_write=True)
-        else:
-            self_metadata = hip_attn.get_scheduler_metadata(
-                num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
-                head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
-                group_order=d["order"][:padded], fuse_kv_write=True)
+        # the plan points at fixed views of the step buffers: one per (rows, grouped)
+        self_metadata = self._self_metadata.get((padded, grouped))
+        if self_metadata is None:
+            if grouped:
+                self_metadata = hip_attn.get_scheduler_metadata(
+                    num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
+                    head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
+                    group_start=d["group_start"][: padded + 1],
+                    max_group_size=hip_attn.MAX_GROUP_SIZE, own_tables=True,
+                    fuse_kv_write=True)
+            else:
+                self_metadata = hip_attn.get_scheduler_metadata(
+                    num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
+                    head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
+                    group_order=d["order"][:padded], fuse_kv_write=True)
+            self._self_metadata[(padded, grouped)] = self_metadata
         self._step_grouped = grouped
         request_ids = tuple(seq.request_id for seq in seqs) + (None,) * (padded - n)
         if request_ids != self._cross_key:
