@@ -1,6 +1,6 @@
 """Per-step state the decoder attention ops read at call time.
 
-Same fields and functions as vflorence/utils/context.py:6-30.  On this build the
+Same fields and functions as vflorence/utils/context.py:6-30.  Here the
 tensors live in HBM: ``context_lens``/``block_tables``/``slot_mapping`` are device
 tensors built by the runner's step preparation, ``self_metadata`` is a
 ``hip_attn.SchedulerMetadata`` and each ``cross_staged`` entry is
