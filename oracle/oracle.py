@@ -1,7 +1,8 @@
 """TEST INFRASTRUCTURE, NOT PRODUCT CODE: CPU oracle of vflorence's decode attention path.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg use this
-module, as the checker and as the timed CPU baseline.  ``vflorence_amd`` never imports
+module, as the reference results the tests compare against and as the timed CPU
+baseline.  ``vflorence_amd`` never imports
 it.
 
 Two restatements of the same algorithm:

@@ -2,8 +2,8 @@
  * oracle/paged_attention.c -- TEST INFRASTRUCTURE, NOT PRODUCT CODE.
  *
  * CPU restatement of vflorence's decode-step attention path, used only by tests/,
- * __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the checker and as the
- * timed CPU baseline.  Nothing in vflorence_amd/ links or calls it.
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the reference results
+ * the tests compare against and as the timed CPU baseline.  Nothing in vflorence_amd/ links or calls it.
  *
  * The reference's arithmetic lives in the external package vllm-cpu-attn 0.1.0
  * (git 79b2eb02549b3e047bc80df51321bc7281f851c9, uv.lock:1091-1093), which is not

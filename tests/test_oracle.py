@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker of the HIP kernels.
+"""Pins the CPU oracle before the HIP kernels are compared against it.
 
 Each check is independent of the oracle's own formula: a library routine
 (torch's scaled_dot_product_attention on densely gathered K/V), closed forms,
