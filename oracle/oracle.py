@@ -2,8 +2,7 @@
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg use this
 module, as the reference results the tests compare against and as the timed CPU
-baseline.  ``vflorence_amd`` never imports
-it.
+baseline.  ``vflorence_amd`` never imports it.
 
 Two restatements of the same algorithm:
 
