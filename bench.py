@@ -351,9 +351,10 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_cross_attention_ba
 
 def counter_pass(torch, wl, reps: int):
     """What a byte-counter pass measures: the cross-attention launches over the 12 layers'
-    pools (``reps`` rounds), then two plain copies of COPY_BYTES each (a device-to-device
-    memcpy and an elementwise negation), whose counter readings calibrate the counters
-    against a known byte count."""
+    pools (``reps`` rounds); the last decode step's fused self-attention over the 12 layers,
+    with beam groups and with one row per workgroup; then two plain copies of COPY_BYTES
+    each (a device-to-device memcpy and an elementwise negation), whose counter readings
+    calibrate the counters against a known byte count."""
     from vflorence_amd import workloads
 
     launches = []
@@ -365,6 +366,38 @@ def counter_pass(torch, wl, reps: int):
         for f in launches:
             f()
     torch.cuda.synchronize()
+    # the last decode step's self-attention with its KV write over the 12 layers: beam
+    # groups (shared prefix blocks read once), then one row per workgroup
+    from vflorence_amd import hip_attn
+
+    plan, rows = wl["plans"][-1], REQUESTS * BEAMS
+    width = max(len(r) for r in plan.block_tables)
+    dev = torch.device("cuda")
+    tables = torch.tensor([r + [0] * (width - len(r)) for r in plan.block_tables],
+                          dtype=torch.int32, device=dev)
+    lens = torch.tensor(plan.context_lens, dtype=torch.int32, device=dev)
+    slots = torch.tensor(plan.slot_mapping, dtype=torch.int64, device=dev)
+    common = dict(num_reqs=rows, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS,
+                  head_dim=HEAD_DIM, dtype=torch.bfloat16, block_size=BLOCK, fuse_kv_write=True)
+    plans = {
+        "grouped": hip_attn.get_scheduler_metadata(
+            group_start=torch.arange(0, rows + 1, BEAMS, dtype=torch.int32, device=dev),
+            max_group_size=BEAMS, own_tables=True, **common),
+        "rows": hip_attn.get_scheduler_metadata(
+            group_order=torch.tensor(hip_attn.longest_first(plan.context_lens),
+                                     dtype=torch.int32, device=dev), **common),
+    }
+    out = torch.empty(rows, NUM_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    for sm in plans.values():
+        for i, layer in enumerate(wl["layers"]):
+            q, k, v = (x.reshape(rows, NUM_HEADS, HEAD_DIM)
+                       for x in wl["qkv"][i].chunk(3, dim=-1))
+            hip_attn.self_attention_with_kv_write(
+                q, k, v, layer.self_attn.k_cache, layer.self_attn.v_cache, out, lens, slots,
+                scale=HEAD_DIM**-0.5, block_table=tables, scheduler_metadata=sm)
+        torch.cuda.synchronize()
+    self_bytes = {"grouped": step_bytes(plan, wl["enc"], grouped=True)[1],
+                  "rows": step_bytes(plan, wl["enc"], grouped=False)[1]}
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
@@ -376,7 +409,11 @@ def counter_pass(torch, wl, reps: int):
                                               2, BLOCK)
     print(json.dumps({"counter_pass": True, "cross_launches": NUM_LAYERS * (reps + 1),
                       "cross_grid_threads": REQUESTS * NUM_HEADS * 64 * 4,
-                      "cross_algorithmic_bytes": int(c_bytes), "copy_bytes": COPY_BYTES,
+                      "cross_algorithmic_bytes": int(c_bytes),
+                      "self_step": len(wl["plans"]) - 1,
+                      "self_launches_each": NUM_LAYERS,
+                      "self_algorithmic_bytes": {k: int(v) for k, v in self_bytes.items()},
+                      "copy_bytes": COPY_BYTES,
                       "copies": ["hipMemcpy device-to-device", "torch.neg float32"]}),
           flush=True)
 
