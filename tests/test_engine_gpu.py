@@ -160,6 +160,15 @@ def test_prepare_and_encode_follow_the_reference_formulas(small_engine):
     from vflorence_amd.utils.context import set_context
 
     set_context()
+    # the one-token invariant (model_runner.py:277-282), and a row with no block at its
+    # write position, are refused before anything is staged
+    two_new = Sequence(7, [2, 5, 6], fx["prompts"][0], params)
+    two_new.block_table = [0]
+    with pytest.raises(ValueError, match="1 token per sequence, got 3"):
+        runner._prepare([two_new])
+    no_block = Sequence(8, [2], fx["prompts"][0], params)
+    with pytest.raises(ValueError, match="no block for its write position"):
+        runner._prepare([no_block])
     for seq in seqs:
         bm.deallocate(seq)
         runner.clear_request(seq.request_id)

@@ -232,16 +232,20 @@ class _ForkAllScheduler(Scheduler):
         return outputs
 
 
-def test_beam_table_handover_keeps_the_reference_block_state():
-    """Handing a parent's table to its first live child instead of fork + deallocate
-    leaves every step's block tables, copy-on-write pairs, reference counts and free
-    list (order included) identical to forking every child."""
+@pytest.mark.parametrize("early_stopping,length_penalty", [(False, 1.0), (True, 1.0),
+                                                             (False, 2.0), (False, -0.5)])
+def test_beam_table_handover_keeps_the_reference_block_state(early_stopping, length_penalty):
+    """Handing a parent's table to its first live child instead of fork + deallocate,
+    and forking only the candidates that are kept, leave every step's block tables,
+    copy-on-write pairs, reference counts, free list (order included) and outputs
+    identical to forking every child."""
     import random
 
     def run(cls, seed):
         rng = random.Random(seed)
         params = SamplingParams(num_beams=4, max_tokens=60, eos_token_id=[2],
-                                early_stopping=False).with_defaults(defaults())
+                                early_stopping=early_stopping,
+                                length_penalty=length_penalty).with_defaults(defaults())
         sched = cls(SimpleNamespace(max_num_seqs=24, num_blocks=160, block_size=16))
         for r in range(6):
             sched.add(Sequence(r, [1], [3], params))

@@ -138,9 +138,10 @@ def _merge_equal_beam_groups(seqs, scores, ids, keep: int):
     if n % nb:
         return None
     heads = rids[::nb]
-    if len(set(heads)) != len(heads) or any(rids[i] != rids[i - i % nb] for i in range(n)):
-        return None
     groups = n // nb
+    if len(set(heads)) != groups or not (
+            np.array(rids).reshape(groups, nb) == np.array(heads)[:, None]).all():
+        return None
     flat = scores.reshape(groups, nb * k)
     order = np.argsort(-flat, axis=1, kind="stable")[:, :keep]
     rows = order // k + (np.arange(groups) * nb)[:, None]
@@ -284,15 +285,21 @@ class ModelRunner:
         real sequences come out as without padding and their logits are the first rows.
         """
         bs = self.block_size
-        for seq in seqs:
-            num_new = len(seq.token_ids) - seq.num_cached_tokens
-            if num_new != 1:
-                raise ValueError(f"each step must feed 1 token per sequence, got {num_new}")
         n = len(seqs)
+        positions = np.fromiter((seq.num_cached_tokens for seq in seqs), np.int64, n)
+        lengths = np.fromiter((len(seq.token_ids) for seq in seqs), np.int64, n)
+        table_lens = np.fromiter((len(seq.block_table) for seq in seqs), np.int64, n)
+        bad = np.flatnonzero(lengths - positions != 1)
+        if bad.size:
+            raise ValueError("each step must feed 1 token per sequence, got "
+                             f"{lengths[bad[0]] - positions[bad[0]]}")
+        if (positions // bs >= table_lens).any():
+            raise ValueError("a sequence has no block for its write position "
+                             "(BlockManager.ensure_capacity was not called)")
         # rows n .. padded-1 are padding: no token written, zero-length contexts
         padded = next((b for b in self._buckets if b >= n), n)
         buf = self._buffers
-        width = max(len(seq.block_table) for seq in seqs)
+        width = int(table_lens.max())
         if padded > buf.rows or width > buf.width or len(copies) > buf.rows:
             buf = self._buffers = _StepBuffers(max(padded, len(copies), buf.rows),
                                                max(width, buf.width), self.device)
@@ -300,12 +307,17 @@ class ModelRunner:
             self._self_metadata.clear()
         buf.copied.synchronize()  # the previous step's upload has left the staging
         h = buf.np
-        positions = [seq.num_cached_tokens for seq in seqs]
-        h["input_ids"][:n] = [seq.token_ids[p] for seq, p in zip(seqs, positions)]
+        w = buf.width
+        tables = h["tables"]
+        tables[:n] = [seq.block_table + [0] * (w - len(seq.block_table)) for seq in seqs]
+        # the one token fed is the last of each sequence's token ids (at its position)
+        h["input_ids"][:n] = [seq.token_ids[-1] for seq in seqs]
         h["positions"][:n] = positions
-        h["slots"][:n] = [seq.block_table[p // bs] * bs + p % bs
-                          for seq, p in zip(seqs, positions)]
-        lens = [p + 1 for p in positions]
+        h["lengths"][:n] = lengths
+        # slot = block_table[pos // bs] * bs + pos % bs (model_runner.py:296-299)
+        h["slots"][:n] = (tables[np.arange(n), positions // bs].astype(np.int64) * bs
+                          + positions % bs)
+        lens = positions + 1
         h["context_lens"][:n] = lens
         if padded > n:
             for name, value in (("input_ids", 0), ("positions", 0), ("slots", -1),
@@ -324,13 +336,10 @@ class ModelRunner:
             h["group_start"][: num_groups + 1] = starts
             h["group_start"][num_groups + 1: padded + 1] = padded
         else:  # one row per workgroup: longest context first
-            h["order"][:padded] = hip_attn.longest_first(lens + [0] * (padded - n))
-        w = buf.width
-        h["tables"][:n] = [seq.block_table + [0] * (w - len(seq.block_table)) for seq in seqs]
+            h["order"][:padded] = hip_attn.longest_first(lens.tolist() + [0] * (padded - n))
         if copies:
             h["copy_src"][: len(copies)] = [s for s, _ in copies]
             h["copy_dst"][: len(copies)] = [d for _, d in copies]
-        h["lengths"][:n] = [len(seq.token_ids) for seq in seqs]
         buf.upload()
         d = buf.d
         # copy-on-write first: this step writes into the now-private blocks
@@ -434,12 +443,15 @@ class ModelRunner:
         """Add each row's cumulative log-prob to its top-k and keep every request's best
         ``keep`` candidates over its rows, best first."""
         top_scores, top_ids = _to_host(top_scores.float(), top_ids)
-        top_scores += torch.tensor([s.cum_logprob for s in seqs], dtype=torch.float32).unsqueeze(-1)
-        fast = _merge_equal_beam_groups(seqs, top_scores.numpy(), top_ids.numpy(), keep)
+        scores, ids = top_scores.numpy(), top_ids.numpy()
+        # each row's cumulative log-prob cast to float32 and added in float32
+        # (model_runner.py:394-396)
+        scores += np.array([s.cum_logprob for s in seqs], dtype=np.float32)[:, None]
+        fast = _merge_equal_beam_groups(seqs, scores, ids, keep)
         if fast is not None:
             return fast
         candidates = defaultdict(list)
-        for seq, row_scores, row_ids in zip(seqs, top_scores.tolist(), top_ids.tolist()):
+        for seq, row_scores, row_ids in zip(seqs, scores.tolist(), ids.tolist()):
             candidates[seq.request_id].extend(zip([seq] * len(row_ids), row_ids, row_scores))
         for cands in candidates.values():
             cands.sort(key=lambda c: c[2], reverse=True)

@@ -19,9 +19,12 @@ and beam selection must come out exactly as the reference's for token parity:
 from __future__ import annotations
 
 from collections import defaultdict, deque
+from operator import attrgetter
 
 from .block_manager import BlockManager
 from .sequence import RequestOut, Sequence
+
+_score = attrgetter("score")
 
 
 class Scheduler:
@@ -86,28 +89,36 @@ class Scheduler:
 
     def _postprocess_beam(self, seqs, candidates_by_request) -> list[tuple[int, RequestOut]]:
         outputs = []
+        eos_of: dict[int, set[int]] = {}
         for request_id, candidates in candidates_by_request.items():
             sp = candidates[0][0].sampling_params
             num_beams = sp.num_beams
-            eos, max_tokens = sp.eos_ids(), sp.max_tokens
+            eos = eos_of.get(id(sp))
+            if eos is None:
+                eos = eos_of[id(sp)] = sp.eos_ids()
+            max_tokens = sp.max_tokens
             finished = self._finished_beams[request_id]
             live: list[tuple[Sequence, Sequence]] = []
             for rank, (parent, token, cum_logprob) in enumerate(candidates):
                 if rank >= num_beams and len(live) >= num_beams:
                     break
-                child = parent.fork(token, cum_logprob)
-                # Sequence.is_finished, with the request's EOS set built once
-                if token in eos or child.num_generated >= max_tokens:
+                # Sequence.is_finished of the child (the parent's tokens plus ``token``),
+                # decided before the child exists: only kept candidates are forked
+                generated = len(parent.token_ids) + 1 - len(parent.decoder_token_ids)
+                if token in eos or generated >= max_tokens:
                     if rank < num_beams:
-                        finished.append(child)
+                        finished.append(parent.fork(token, cum_logprob))
                 elif len(live) < num_beams:
-                    live.append((parent, child))
-            finished.sort(key=lambda s: s.score, reverse=True)
-            del finished[num_beams:]
-            best_live = max((child.score for _, child in live), default=float("-inf"))
-            done = len(finished) >= num_beams and (
-                sp.early_stopping or finished[-1].score >= best_live)
-            if not live or done:
+                    live.append((parent, parent.fork(token, cum_logprob)))
+            if finished:
+                finished.sort(key=_score, reverse=True)
+                del finished[num_beams:]
+            # the early-stopping test compares with the best live beam only when the
+            # finished list is full (the live scores are not needed otherwise)
+            done = not live or (len(finished) >= num_beams and (
+                sp.early_stopping
+                or finished[-1].score >= max(child.score for _, child in live)))
+            if done:
                 self._finished_beams.pop(request_id, None)
                 outputs.append((request_id, finished[0].to_output()))
             else:
