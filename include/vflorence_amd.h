@@ -1,6 +1,7 @@
 /*
  * vflorence_amd.h -- C ABI of the MI355X (gfx950) decode-step attention library and the
- * decoder-step kernels around it (residual + LayerNorm, log-softmax + rules + top-k).
+ * decoder-step kernels around it (residual + LayerNorm, log-softmax + rules + top-k,
+ * the square projections of a decode step).
  *
  * Every entry point takes plain device pointers, element strides and sizes, and a
  * hipStream_t passed as `void *` (NULL = the legacy default stream).  No entry point
@@ -259,6 +260,23 @@ int vfl_logprob_topk(const void *logits, int64_t row_stride, int64_t rows, int v
                      int max_length, int begin_index, int n_eos, int n_suppress, int n_begin,
                      int n_bos, int n_forced_eos, int log_softmax, int k, float *scores,
                      int64_t *ids, void *stream);
+
+/*
+ * The decoder's square projections for a decode step's rows: the self-attention
+ * output projection and the cross-attention query and output projections
+ * (vflorence/models/bart.py:114,142,146 -- nn.Linear in the reference, no
+ * vllm_cpu_attn counterpart):
+ *   y[r][n] = sum_k x[r][k] * weight[n][k] + bias[n]        (bias may be NULL)
+ * 16-bit x / weight / bias / y (dtype VFL_BFLOAT16 or VFL_FLOAT16), fp32 sums, rounded
+ * once on the store.  in_features a multiple of 256; in_features and out_features at
+ * most 1024; rows at most 65535 * 32.  x and weight 16-byte aligned with row strides
+ * (elements) a multiple of 8; strides cover the rows.  Split-K over 8 waves of a
+ * workgroup per 32 x 32 output tile: one memory round trip for the weight, for the
+ * few hundred rows of a decode step.
+ */
+int vfl_linear(const void *x, int64_t x_stride, const void *weight, int64_t weight_stride,
+               const void *bias, void *y, int64_t y_stride, int64_t rows, int out_features,
+               int in_features, int dtype, void *stream);
 
 #ifdef __cplusplus
 }

@@ -160,6 +160,25 @@ def test_reshape_and_copy_validate_before_launch():
     assert lib.vfl_copy_blocks(None, 24, None, None, 5, 1024, 10, None, None) == -1  # nulls
 
 
+def test_linear_validates_before_launch():
+    from vflorence_amd._lib import lib
+
+    def call(rows=4, out=1024, inp=1024, dtype=1, xs=1024, ws=1024, ys=1024, ptr=None):
+        return lib.vfl_linear(ptr, xs, ptr, ws, None, ptr, ys, rows, out, inp, dtype, None)
+
+    assert call(dtype=0) == -2                  # fp32: no kernel
+    assert call(inp=768 + 128) == -2            # in_features not a multiple of 256
+    assert call(out=2048) == -2 and call(inp=2048, xs=2048, ws=2048) == -2  # > 1024
+    assert call(rows=65535 * 32 + 1) == -2
+    assert call(rows=-1) == -1 and call(out=0) == -1
+    assert call(xs=512) == -1 and call(ys=1000) == -1  # strides shorter than a row
+    assert call(rows=0) == 0                    # nothing to do, nothing dereferenced
+    assert call() == -1                         # null pointers
+    assert b"null" in lib.vfl_last_error()
+    assert call(ptr=16 * 1000 + 8) == -1        # 8-byte aligned x / weight
+    assert b"aligned" in lib.vfl_last_error()
+
+
 def test_cpu_tensors_are_rejected():
     import torch
 

@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "vfl_copy_blocks",
     "vfl_add_layer_norm",
     "vfl_logprob_topk",
+    "vfl_linear",
 )
 
 
@@ -86,6 +87,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _i64, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
          _i32, _i32, _vp, _vp, _vp],
+    ),
+    "vfl_linear": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp],
     ),
 }
 

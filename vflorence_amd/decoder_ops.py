@@ -3,9 +3,13 @@
 ``add_layer_norm`` is the decoder layer's ``layer_norm(hidden + sublayer(hidden))``
 (vflorence/models/bart.py:192-201) in one launch, registered as the custom op
 ``vflorence_amd::add_layer_norm`` so a compiled decoder keeps it whole.
+``linear`` (custom op ``vflorence_amd::linear``) is nn.Linear for a decode step's rows
+and a square weight of up to 1024 x 1024 (the decoder's attention output and
+cross-attention query projections, vflorence/models/bart.py:114,142,146);
+``linear_fits`` says when it applies.
 ``logprob_topk`` is the device half of sampling (vflorence/engine/model_runner.py:355-398):
 log-softmax, the history-free generation rules and the per-row top-k in one read of
-the logits.  Both run on the current stream; CPU tensors are rejected.
+the logits.  All run on the current stream; CPU tensors are rejected.
 """
 
 from __future__ import annotations
@@ -17,6 +21,13 @@ from .hip_attn import _dtype_code, _require_gpu, _stream
 
 # largest k of logprob_topk (each lane keeps its k best in registers)
 MAX_K = 16
+
+# vfl_linear's limits, and the row counts it is used for: measured on MI355X with the
+# weight streamed from HBM, 8.0-8.4 us against hipBLASLt's 11.0-11.7 us for a 1024 x 1024
+# weight at 64-256 rows (7.4 against 9.2-9.8 us for 768 x 768); even at 16 rows.
+LINEAR_MAX_DIM = 1024
+LINEAR_K_MULTIPLE = 256
+LINEAR_MAX_ROWS = 256
 
 
 @torch.library.custom_op("vflorence_amd::add_layer_norm", mutates_args=())
@@ -46,6 +57,44 @@ def add_layer_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor
 @add_layer_norm.register_fake
 def _(x, residual, weight, bias, eps):
     return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+def linear_fits(rows: int, weight: torch.Tensor) -> bool:
+    """Whether ``linear`` serves ``rows`` rows times ``weight``: a contiguous, 16-byte
+    aligned 16-bit device weight, in_features a multiple of 256, both feature counts at
+    most 1024, at most 256 rows."""
+    out_features, in_features = weight.shape
+    return (weight.is_cuda and weight.dtype in (torch.bfloat16, torch.float16)
+            and weight.is_contiguous() and weight.data_ptr() % 16 == 0
+            and 0 < rows <= LINEAR_MAX_ROWS and in_features % LINEAR_K_MULTIPLE == 0
+            and in_features <= LINEAR_MAX_DIM and out_features <= LINEAR_MAX_DIM)
+
+
+@torch.library.custom_op("vflorence_amd::linear", mutates_args=())
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    """``x @ weight.T + bias`` over the last dimension (nn.Linear), fp32 sums."""
+    dev = _require_gpu(x, weight) if bias is None else _require_gpu(x, weight, bias)
+    out_features, in_features = weight.shape
+    if x.shape[-1] != in_features or (bias is not None and bias.shape != (out_features,)):
+        raise ValueError("linear: x [..., in], weight [out, in], bias [out]")
+    if x.dtype != weight.dtype or (bias is not None and bias.dtype != x.dtype):
+        raise ValueError("linear: x, weight and bias must share one dtype")
+    x2 = x.reshape(-1, in_features)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    w = weight.contiguous()
+    b = None if bias is None else bias.contiguous()
+    out = torch.empty(x2.shape[0], out_features, dtype=x.dtype, device=dev)
+    check(lib.vfl_linear(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0),
+                         None if b is None else b.data_ptr(), out.data_ptr(), out.stride(0),
+                         x2.shape[0], out_features, in_features, _dtype_code(x.dtype),
+                         _stream(dev)))
+    return out.view(*x.shape[:-1], out_features)
+
+
+@linear.register_fake
+def _(x, weight, bias):
+    return x.new_empty(*x.shape[:-1], weight.shape[0])
 
 
 class TopkRules:

@@ -37,6 +37,21 @@ def _residual_norm(h: torch.Tensor, y: torch.Tensor, norm: nn.LayerNorm) -> torc
     return norm(h + y)
 
 
+class DecodeLinear(nn.Linear):
+    """nn.Linear whose decode-step calls -- a few hundred rows on the GPU times a weight
+    of up to 1024 x 1024 -- run on the split-K kernel (vflorence_amd::linear); other
+    shapes, fp32 and host tensors go through F.linear (hipBLASLt on the GPU)."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda:
+            from ..decoder_ops import linear, linear_fits
+
+            if x.dtype == self.weight.dtype and linear_fits(x.numel() // x.shape[-1],
+                                                            self.weight):
+                return linear(x, self.weight, self.bias)
+        return F.linear(x, self.weight, self.bias)
+
+
 def _activation(name: str):
     from transformers.activations import ACT2FN
 
@@ -101,7 +116,7 @@ class BartDecoderSelfAttention(_Heads):
     def __init__(self, embed_dim: int, num_heads: int):
         super().__init__(embed_dim, num_heads)
         self.qkv_proj = nn.Linear(embed_dim, 3 * embed_dim)
-        self.out_proj = nn.Linear(embed_dim, embed_dim)
+        self.out_proj = DecodeLinear(embed_dim, embed_dim)
         self.k_cache = self.v_cache = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -119,9 +134,9 @@ class BartDecoderCrossAttention(_Heads):
 
     def __init__(self, embed_dim: int, num_heads: int, layer_idx: int):
         super().__init__(embed_dim, num_heads)
-        self.q_proj = nn.Linear(embed_dim, embed_dim)
+        self.q_proj = DecodeLinear(embed_dim, embed_dim)
         self.kv_proj = nn.Linear(embed_dim, 2 * embed_dim)
-        self.out_proj = nn.Linear(embed_dim, embed_dim)
+        self.out_proj = DecodeLinear(embed_dim, embed_dim)
         self.layer_idx = layer_idx
         self.k_cache = self.v_cache = None
 
