@@ -1,7 +1,7 @@
 /*
  * vflorence_amd.h -- C ABI of the MI355X (gfx950) decode-step attention library and the
  * decoder-step kernels around it (residual + LayerNorm, log-softmax + rules + top-k,
- * the square projections of a decode step).
+ * the decoder's projections for a decode step's rows).
  *
  * Every entry point takes plain device pointers, element strides and sizes, and a
  * hipStream_t passed as `void *` (NULL = the legacy default stream).  No entry point
@@ -262,21 +262,28 @@ int vfl_logprob_topk(const void *logits, int64_t row_stride, int64_t rows, int v
                      int64_t *ids, void *stream);
 
 /*
- * The decoder's square projections for a decode step's rows: the self-attention
- * output projection and the cross-attention query and output projections
- * (vflorence/models/bart.py:114,142,146 -- nn.Linear in the reference, no
+ * The decoder's projections for a decode step's rows: the fused q|k|v, the
+ * self-attention output and the cross-attention query and output projections
+ * (vflorence/models/bart.py:111,114,142,146 -- nn.Linear in the reference, no
  * vllm_cpu_attn counterpart):
  *   y[r][n] = sum_k x[r][k] * weight[n][k] + bias[n]        (bias may be NULL)
  * 16-bit x / weight / bias / y (dtype VFL_BFLOAT16 or VFL_FLOAT16), fp32 sums, rounded
- * once on the store.  in_features a multiple of 256; in_features and out_features at
- * most 1024; rows at most 65535 * 32.  x and weight 16-byte aligned with row strides
- * (elements) a multiple of 8; strides cover the rows.  Split-K over 8 waves of a
- * workgroup per 32 x 32 output tile: one memory round trip for the weight, for the
- * few hundred rows of a decode step.
+ * once on the store.  The weight is first re-laid out once by vfl_pack_linear_weight
+ * into `packed` (vfl_linear_packed_elems(out_features, in_features) elements):
+ * 1024-byte blocks of 16 rows x 32 k in the matrix cores' operand order -- block
+ * (r, c), at element (r * in_features / 32 + c) * 512, holds row 16 r + l % 16,
+ * k = 32 c + 8 (l / 16) .. +7 at element 8 l for l < 64 -- rows zero-padded to a
+ * multiple of 32.  in_features a multiple of 256; rows at most 65535 * 32.  x and
+ * `packed` 16-byte aligned, the x row stride (elements) a multiple of 8 and at least
+ * in_features.  Split-K over the 8 waves of a workgroup per 32 x 32 output tile: one
+ * memory round trip for the weight when in_features <= 1024.
  */
-int vfl_linear(const void *x, int64_t x_stride, const void *weight, int64_t weight_stride,
-               const void *bias, void *y, int64_t y_stride, int64_t rows, int out_features,
-               int in_features, int dtype, void *stream);
+int64_t vfl_linear_packed_elems(int out_features, int in_features);
+int vfl_pack_linear_weight(const void *weight, int64_t weight_stride, int out_features,
+                           int in_features, void *packed, int dtype, void *stream);
+int vfl_linear(const void *x, int64_t x_stride, const void *packed_weight, const void *bias,
+               void *y, int64_t y_stride, int64_t rows, int out_features, int in_features,
+               int dtype, void *stream);
 
 #ifdef __cplusplus
 }

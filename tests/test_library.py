@@ -163,12 +163,14 @@ def test_reshape_and_copy_validate_before_launch():
 def test_linear_validates_before_launch():
     from vflorence_amd._lib import lib
 
-    def call(rows=4, out=1024, inp=1024, dtype=1, xs=1024, ws=1024, ys=1024, ptr=None):
-        return lib.vfl_linear(ptr, xs, ptr, ws, None, ptr, ys, rows, out, inp, dtype, None)
+    assert lib.vfl_linear_packed_elems(1000, 512) == 1024 * 512  # rows padded to 32
+    assert lib.vfl_linear_packed_elems(0, 512) == 0
+
+    def call(rows=4, out=1024, inp=1024, dtype=1, xs=1024, ys=1024, ptr=None):
+        return lib.vfl_linear(ptr, xs, ptr, None, ptr, ys, rows, out, inp, dtype, None)
 
     assert call(dtype=0) == -2                  # fp32: no kernel
     assert call(inp=768 + 128) == -2            # in_features not a multiple of 256
-    assert call(out=2048) == -2 and call(inp=2048, xs=2048, ws=2048) == -2  # > 1024
     assert call(rows=65535 * 32 + 1) == -2
     assert call(rows=-1) == -1 and call(out=0) == -1
     assert call(xs=512) == -1 and call(ys=1000) == -1  # strides shorter than a row
@@ -177,6 +179,13 @@ def test_linear_validates_before_launch():
     assert b"null" in lib.vfl_last_error()
     assert call(ptr=16 * 1000 + 8) == -1        # 8-byte aligned x / weight
     assert b"aligned" in lib.vfl_last_error()
+
+    def pack(out=1024, inp=1024, stride=1024, dtype=1, ptr=None):
+        return lib.vfl_pack_linear_weight(ptr, stride, out, inp, ptr, dtype, None)
+
+    assert pack(dtype=2 + 5) == -2 and pack(inp=300) == -2
+    assert pack(stride=1000) == -1 and pack() == -1
+    assert pack(ptr=16 * 1000 + 8) == -1
 
 
 def test_cpu_tensors_are_rejected():

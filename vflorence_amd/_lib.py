@@ -30,6 +30,8 @@ EXPORTED_SYMBOLS = (
     "vfl_copy_blocks",
     "vfl_add_layer_norm",
     "vfl_logprob_topk",
+    "vfl_linear_packed_elems",
+    "vfl_pack_linear_weight",
     "vfl_linear",
 )
 
@@ -88,9 +90,11 @@ _SIGNATURES = {
         [_vp, _i64, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
          _i32, _i32, _vp, _vp, _vp],
     ),
+    "vfl_linear_packed_elems": (ctypes.c_int64, [_i32, _i32]),
+    "vfl_pack_linear_weight": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, _i32, _vp]),
     "vfl_linear": (
         ctypes.c_int,
-        [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp],
+        [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp],
     ),
 }
 

@@ -1,23 +1,30 @@
-// Decode-step linear layer on the matrix cores (gfx950), 16-bit inputs and output,
+// Decode-step linear layers on the matrix cores (gfx950), 16-bit inputs and output,
 // fp32 sums:
 //
 //   y[m][n] = sum_k x[m][k] * w[n][k] + bias[n]        (w: nn.Linear's [out, in])
 //
-// for the few hundred token rows of a decode step times a weight of up to 1024 x 1024
-// (the decoder's attention output and cross-attention query projections,
-// vflorence/models/bart.py:114,142,146).  Each step streams the weight from HBM
-// once (a decoder's weights exceed the last-level cache), so the time goes to
+// for the few hundred token rows of a decode step times the decoder's projection
+// weights (vflorence/models/bart.py:111,114,142,146: the fused q|k|v, the attention
+// output and the cross-attention query projections).  Each step streams every weight
+// from HBM once (a decoder's weights exceed the last-level cache), so the time goes to
 // memory round trips, not arithmetic: a GEMM that walks K in a loop pays one round
-// trip per K step.  Here a workgroup
-// owns a 32-feature x 32-token output tile and splits K over its 8 waves.  Each wave
-// loads the operands of up to 4 K steps of 32 in one batch (16-byte chunks straight
-// into the MFMA operand registers, no LDS staging), so K <= 1024 costs one round
-// trip.  The waves' partial tiles are summed through LDS in a 3-level tree, and wave
-// 0 adds the bias and stores.
+// trip per K step.  Here a workgroup owns a 32-feature x 32-token output tile and
+// splits K over its 8 waves.  Each wave loads the operands of up to 4 K steps of 32 in
+// one batch, so K <= 1024 costs one round trip.  The waves' partial tiles are summed
+// through LDS in a 3-level tree, and wave 0 adds the bias and stores.
 //
-// Product per 32-wide K step (mfma_f32_16x16x32): A = 16 weight rows (features),
-// B = 16 token rows, D[feature][token]; a lane's four D registers are four consecutive
-// features of one token -- one 8-byte store.
+// Operand order.  The product per 32-wide K step is mfma_f32_16x16x32 with A = 16
+// weight rows (features) and B = 16 token rows, giving D[feature][token]; a lane's four
+// D registers are four consecutive features of one token -- one 8-byte store.  Lane l
+// holds row l % 16 and k = 8 (l / 16) .. +7 of both operands, so neighbouring lanes read
+// rows 2 KB apart.  Loaded that way, every 16-byte chunk is a separate cache access.
+// The operands are therefore brought in contiguously instead:
+// - The weight is re-laid out once (vfl_pack_linear_weight) into 1 KB blocks of 16
+//   rows x 32 k, each stored in lane order: block (r, c) holds, for lane l, row
+//   16 r + l % 16 and k = 32 c + 8 (l / 16) .. +7 at byte 16 l.  One wave load is then
+//   one contiguous KB.  Rows are padded with zeros to a multiple of 32.
+// - Activation rows are read as 64-byte runs (lanes 4 i .. 4 i + 3 take row i) and
+//   moved into operand order with ds_bpermute (lane l takes lane 4 (l % 16) + l / 16).
 #include "common.h"
 #include "mfma_ops.h"
 
@@ -27,11 +34,33 @@ constexpr int LIN_WAVES = 8;   // waves splitting K
 constexpr int LIN_TILE = 32;   // features and tokens per workgroup
 constexpr int LIN_BATCH = 4;   // K steps whose operands are loaded together
 constexpr int LIN_K_MULTIPLE = 32 * LIN_WAVES;
-constexpr int LIN_MAX_DIM = 1024;
+constexpr int LIN_BLOCK = 16 * 32;  // elements of one packed 16-row x 32-k weight block
+
+__host__ __device__ constexpr int64_t packed_rows(int64_t out_features) {
+  return (out_features + LIN_TILE - 1) / LIN_TILE * LIN_TILE;
+}
+
+// One thread per 16-byte chunk of the packed weight: chunk t is lane t % 64 of block
+// t / 64 = (row block r, k block c).
+__global__ __launch_bounds__(256) void pack_linear_weight_kernel(
+    const uint16_t *__restrict__ w, int64_t ldw, int N, int K, uint16_t *__restrict__ packed,
+    int64_t chunks) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= chunks) return;
+  const int l = (int)(t & 63);
+  const int64_t blk = t >> 6;
+  const int ks = K / 32;
+  const int64_t r = blk / ks;
+  const int c = (int)(blk % ks);
+  const int64_t row = 16 * r + (l & 15);
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (row < N) v = *reinterpret_cast<const uint4 *>(w + row * ldw + 32 * c + 8 * (l >> 4));
+  *reinterpret_cast<uint4 *>(packed + t * 8) = v;
+}
 
 template <int DT>
 __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
-    const uint16_t *__restrict__ x, int64_t ldx, const uint16_t *__restrict__ w, int64_t ldw,
+    const uint16_t *__restrict__ x, int64_t ldx, const uint16_t *__restrict__ wp,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, int64_t ldy, int M, int N,
     int K, bool vec_store) {
   constexpr int FT = LIN_TILE / 16, TT = LIN_TILE / 16;
@@ -40,19 +69,23 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int n0 = blockIdx.x * LIN_TILE, m0 = blockIdx.y * LIN_TILE;
+  const int ks = K / 32;
   const int kq = K / LIN_WAVES;  // this wave's K range: [wv * kq, (wv + 1) * kq)
   const int kb = wv * kq;
-  const int col = lane & 15, chunk = 8 * (lane >> 4);
+  const int col = lane & 15;
+  // byte address of the lane whose 64-byte run holds this lane's operand chunk
+  const int src = 4 * (4 * (lane & 15) + (lane >> 4));
 
-  // Operand rows; rows past M / N read the last row and their results are dropped.
-  const uint16_t *wrow[FT];
+  // Packed weight blocks of this wave's first K step; activation runs (rows past M read
+  // the last row; their results are dropped).
+  const uint16_t *wblk[FT];
   const uint16_t *xrow[TT];
 #pragma unroll
   for (int f = 0; f < FT; ++f)
-    wrow[f] = w + (int64_t)min(n0 + 16 * f + col, N - 1) * ldw + kb + chunk;
+    wblk[f] = wp + ((int64_t)(n0 / 16 + f) * ks + kb / 32) * LIN_BLOCK + lane * 8;
 #pragma unroll
   for (int t = 0; t < TT; ++t)
-    xrow[t] = x + (int64_t)min(m0 + 16 * t + col, M - 1) * ldx + kb + chunk;
+    xrow[t] = x + (int64_t)min(m0 + 16 * t + (lane >> 2), M - 1) * ldx + kb + 8 * (lane & 3);
 
   floatx4_t acc[FT][TT];
 #pragma unroll
@@ -68,7 +101,7 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
       if (s0 + g < steps) {
 #pragma unroll
         for (int f = 0; f < FT; ++f)
-          a[g][f] = *reinterpret_cast<const uint4 *>(wrow[f] + 32 * (s0 + g));
+          a[g][f] = *reinterpret_cast<const uint4 *>(wblk[f] + LIN_BLOCK * (s0 + g));
 #pragma unroll
         for (int t = 0; t < TT; ++t)
           b[g][t] = *reinterpret_cast<const uint4 *>(xrow[t] + 32 * (s0 + g));
@@ -77,6 +110,13 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
 #pragma unroll
     for (int g = 0; g < LIN_BATCH; ++g) {
       if (s0 + g < steps) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+          b[g][t].x = __builtin_amdgcn_ds_bpermute(src, (int)b[g][t].x);
+          b[g][t].y = __builtin_amdgcn_ds_bpermute(src, (int)b[g][t].y);
+          b[g][t].z = __builtin_amdgcn_ds_bpermute(src, (int)b[g][t].z);
+          b[g][t].w = __builtin_amdgcn_ds_bpermute(src, (int)b[g][t].w);
+        }
 #pragma unroll
         for (int f = 0; f < FT; ++f)
 #pragma unroll
@@ -139,65 +179,98 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
   }
 }
 
+static int check_features(int out_features, int in_features, int dtype, const char *who) {
+  if (dtype != VFL_BFLOAT16 && dtype != VFL_FLOAT16) {
+    set_error("%s: dtype %d has no kernel (bf16 and fp16 only)", who, dtype);
+    return VFL_E_UNSUPPORTED;
+  }
+  if (out_features <= 0 || in_features <= 0) {
+    set_error("%s: bad sizes (out %d in %d)", who, out_features, in_features);
+    return VFL_E_INVALID;
+  }
+  if (in_features % LIN_K_MULTIPLE != 0) {
+    set_error("%s: in_features must be a multiple of %d (got %d)", who, LIN_K_MULTIPLE,
+              in_features);
+    return VFL_E_UNSUPPORTED;
+  }
+  return VFL_OK;
+}
+
 }  // namespace vfl
 
 using namespace vfl;
 
-extern "C" int vfl_linear(const void *x, int64_t x_stride, const void *weight,
-                          int64_t weight_stride, const void *bias, void *y, int64_t y_stride,
-                          int64_t rows, int out_features, int in_features, int dtype,
-                          void *stream) {
+extern "C" int64_t vfl_linear_packed_elems(int out_features, int in_features) {
+  if (out_features <= 0 || in_features <= 0) return 0;
+  return packed_rows(out_features) * in_features;
+}
+
+extern "C" int vfl_pack_linear_weight(const void *weight, int64_t weight_stride,
+                                      int out_features, int in_features, void *packed,
+                                      int dtype, void *stream) {
   clear_error();
-  if (dtype != VFL_BFLOAT16 && dtype != VFL_FLOAT16) {
-    set_error("linear: dtype %d has no kernel (bf16 and fp16 only)", dtype);
-    return VFL_E_UNSUPPORTED;
-  }
-  if (rows < 0 || out_features <= 0 || in_features <= 0) {
-    set_error("linear: bad sizes (rows %lld out %d in %d)", (long long)rows, out_features,
-              in_features);
+  int st = check_features(out_features, in_features, dtype, "pack_linear_weight");
+  if (st != VFL_OK) return st;
+  if (weight_stride < in_features) {
+    set_error("pack_linear_weight: weight_stride %lld < in_features %d",
+              (long long)weight_stride, in_features);
     return VFL_E_INVALID;
   }
-  if (in_features % LIN_K_MULTIPLE != 0 || in_features > LIN_MAX_DIM ||
-      out_features > LIN_MAX_DIM) {
-    set_error("linear: in_features must be a multiple of %d and both feature counts at most "
-              "%d (got out %d in %d)",
-              LIN_K_MULTIPLE, LIN_MAX_DIM, out_features, in_features);
-    return VFL_E_UNSUPPORTED;
+  if (!weight || !packed) {
+    set_error("pack_linear_weight: null pointer argument");
+    return VFL_E_INVALID;
   }
-  if (rows > 65535LL * LIN_TILE) {
-    set_error("linear: at most %lld rows per call (got %lld)", 65535LL * LIN_TILE,
+  if (((uintptr_t)weight | (uintptr_t)packed) % 16 != 0 || weight_stride % 8 != 0) {
+    set_error("pack_linear_weight: weight and packed must be 16-byte aligned, the weight "
+              "row stride a multiple of 8 elements");
+    return VFL_E_INVALID;
+  }
+  const int64_t chunks = packed_rows(out_features) * in_features / 8;
+  pack_linear_weight_kernel<<<dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                              (hipStream_t)stream>>>(
+      (const uint16_t *)weight, weight_stride, out_features, in_features, (uint16_t *)packed,
+      chunks);
+  return launch_status("pack_linear_weight");
+}
+
+extern "C" int vfl_linear(const void *x, int64_t x_stride, const void *packed_weight,
+                          const void *bias, void *y, int64_t y_stride, int64_t rows,
+                          int out_features, int in_features, int dtype, void *stream) {
+  clear_error();
+  int st = check_features(out_features, in_features, dtype, "linear");
+  if (st != VFL_OK) return st;
+  if (rows < 0 || rows > 65535LL * LIN_TILE) {
+    set_error("linear: rows must be in [0, %lld] (got %lld)", 65535LL * LIN_TILE,
               (long long)rows);
-    return VFL_E_UNSUPPORTED;
+    return rows < 0 ? VFL_E_INVALID : VFL_E_UNSUPPORTED;
   }
-  if (x_stride < in_features || weight_stride < in_features || y_stride < out_features) {
-    set_error("linear: row strides must cover the rows (x %lld weight %lld y %lld)",
-              (long long)x_stride, (long long)weight_stride, (long long)y_stride);
+  if (x_stride < in_features || y_stride < out_features) {
+    set_error("linear: row strides must cover the rows (x %lld y %lld)", (long long)x_stride,
+              (long long)y_stride);
     return VFL_E_INVALID;
   }
   if (rows == 0) return VFL_OK;
-  if (!x || !weight || !y) {
+  if (!x || !packed_weight || !y) {
     set_error("linear: null pointer argument");
     return VFL_E_INVALID;
   }
-  if (((uintptr_t)x | (uintptr_t)weight) % 16 != 0 || x_stride % 8 != 0 ||
-      weight_stride % 8 != 0 || (uintptr_t)y % 2 != 0 || (uintptr_t)bias % 2 != 0) {
-    set_error("linear: x and weight must be 16-byte aligned with row strides a multiple of "
-              "8 elements");
+  if (((uintptr_t)x | (uintptr_t)packed_weight) % 16 != 0 || x_stride % 8 != 0 ||
+      (uintptr_t)y % 2 != 0 || (uintptr_t)bias % 2 != 0) {
+    set_error("linear: x and the packed weight must be 16-byte aligned, the x row stride a "
+              "multiple of 8 elements");
     return VFL_E_INVALID;
   }
   const bool vec_store = (uintptr_t)y % 8 == 0 && y_stride % 4 == 0;
-  const dim3 grid((unsigned)((out_features + LIN_TILE - 1) / LIN_TILE),
+  const dim3 grid((unsigned)(packed_rows(out_features) / LIN_TILE),
                   (unsigned)((rows + LIN_TILE - 1) / LIN_TILE));
   hipStream_t s = (hipStream_t)stream;
   if (dtype == VFL_BFLOAT16)
     decode_linear_kernel<VFL_BFLOAT16><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
-        (const uint16_t *)x, x_stride, (const uint16_t *)weight, weight_stride,
-        (const uint16_t *)bias, (uint16_t *)y, y_stride, (int)rows, out_features, in_features,
-        vec_store);
+        (const uint16_t *)x, x_stride, (const uint16_t *)packed_weight, (const uint16_t *)bias,
+        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
   else
     decode_linear_kernel<VFL_FLOAT16><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
-        (const uint16_t *)x, x_stride, (const uint16_t *)weight, weight_stride,
-        (const uint16_t *)bias, (uint16_t *)y, y_stride, (int)rows, out_features, in_features,
-        vec_store);
+        (const uint16_t *)x, x_stride, (const uint16_t *)packed_weight, (const uint16_t *)bias,
+        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
   return launch_status("linear");
 }

@@ -4,9 +4,9 @@
 (vflorence/models/bart.py:192-201) in one launch, registered as the custom op
 ``vflorence_amd::add_layer_norm`` so a compiled decoder keeps it whole.
 ``linear`` (custom op ``vflorence_amd::linear``) is nn.Linear for a decode step's rows
-and a square weight of up to 1024 x 1024 (the decoder's attention output and
-cross-attention query projections, vflorence/models/bart.py:114,142,146);
-``linear_fits`` says when it applies.
+times a weight re-laid out once by ``pack_linear_weight`` (the decoder's q|k|v,
+attention output and cross-attention query projections,
+vflorence/models/bart.py:111,114,142,146); ``linear_fits`` says when it applies.
 ``logprob_topk`` is the device half of sampling (vflorence/engine/model_runner.py:355-398):
 log-softmax, the history-free generation rules and the per-row top-k in one read of
 the logits.  All run on the current stream; CPU tensors are rejected.
@@ -22,11 +22,13 @@ from .hip_attn import _dtype_code, _require_gpu, _stream
 # largest k of logprob_topk (each lane keeps its k best in registers)
 MAX_K = 16
 
-# vfl_linear's limits, and the row counts it is used for: measured on MI355X with the
-# weight streamed from HBM, 8.0-8.4 us against hipBLASLt's 11.0-11.7 us for a 1024 x 1024
-# weight at 64-256 rows (7.4 against 9.2-9.8 us for 768 x 768); even at 16 rows.
-LINEAR_MAX_DIM = 1024
+# Where vfl_linear is used: measured on MI355X at 256 rows with the weight streamed
+# from HBM, 6.8 us against hipBLASLt's 11.0 us for 1024 x 1024 and 10.8 against 12.4 us
+# for the 3072 x 1024 q|k|v; 4096-wide and 4096-deep weights (the feed-forward layers)
+# run no faster than hipBLASLt and stay there.
 LINEAR_K_MULTIPLE = 256
+LINEAR_MAX_IN = 1024
+LINEAR_MAX_OUT = 3072
 LINEAR_MAX_ROWS = 256
 
 
@@ -61,31 +63,50 @@ def _(x, residual, weight, bias, eps):
 
 def linear_fits(rows: int, weight: torch.Tensor) -> bool:
     """Whether ``linear`` serves ``rows`` rows times ``weight``: a contiguous, 16-byte
-    aligned 16-bit device weight, in_features a multiple of 256, both feature counts at
-    most 1024, at most 256 rows."""
+    aligned 16-bit device weight, in_features a multiple of 256 and at most 1024,
+    out_features at most 3072, at most 256 rows."""
     out_features, in_features = weight.shape
     return (weight.is_cuda and weight.dtype in (torch.bfloat16, torch.float16)
             and weight.is_contiguous() and weight.data_ptr() % 16 == 0
             and 0 < rows <= LINEAR_MAX_ROWS and in_features % LINEAR_K_MULTIPLE == 0
-            and in_features <= LINEAR_MAX_DIM and out_features <= LINEAR_MAX_DIM)
+            and in_features <= LINEAR_MAX_IN and out_features <= LINEAR_MAX_OUT)
+
+
+def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
+    """``weight`` ([out, in], 16-bit, on the GPU) re-laid out in the matrix cores' operand
+    order for ``linear`` (1 KB blocks of 16 rows x 32 inputs in lane order, rows padded
+    to a multiple of 32): a new 1-D tensor of the same dtype."""
+    dev = _require_gpu(weight)
+    out_features, in_features = weight.shape
+    w = weight.contiguous()
+    packed = torch.empty(max(1, lib.vfl_linear_packed_elems(out_features, in_features)),
+                         dtype=weight.dtype, device=dev)
+    check(lib.vfl_pack_linear_weight(w.data_ptr(), w.stride(0), out_features, in_features,
+                                     packed.data_ptr(), _dtype_code(weight.dtype), _stream(dev)))
+    return packed
 
 
 @torch.library.custom_op("vflorence_amd::linear", mutates_args=())
-def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
-    """``x @ weight.T + bias`` over the last dimension (nn.Linear), fp32 sums."""
-    dev = _require_gpu(x, weight) if bias is None else _require_gpu(x, weight, bias)
-    out_features, in_features = weight.shape
-    if x.shape[-1] != in_features or (bias is not None and bias.shape != (out_features,)):
-        raise ValueError("linear: x [..., in], weight [out, in], bias [out]")
-    if x.dtype != weight.dtype or (bias is not None and bias.dtype != x.dtype):
+def linear(x: torch.Tensor, packed_weight: torch.Tensor, bias: torch.Tensor | None,
+           out_features: int) -> torch.Tensor:
+    """``x @ weight.T + bias`` over the last dimension (nn.Linear), fp32 sums, with the
+    weight given as ``pack_linear_weight(weight)``."""
+    dev = _require_gpu(x, packed_weight) if bias is None else _require_gpu(x, packed_weight,
+                                                                          bias)
+    in_features = x.shape[-1]
+    if packed_weight.numel() != lib.vfl_linear_packed_elems(out_features, in_features):
+        raise ValueError("linear: packed_weight does not hold a packed "
+                         f"[{out_features}, {in_features}] weight")
+    if bias is not None and bias.shape != (out_features,):
+        raise ValueError("linear: bias must be [out_features]")
+    if x.dtype != packed_weight.dtype or (bias is not None and bias.dtype != x.dtype):
         raise ValueError("linear: x, weight and bias must share one dtype")
     x2 = x.reshape(-1, in_features)
     if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
         x2 = x2.contiguous()
-    w = weight.contiguous()
     b = None if bias is None else bias.contiguous()
     out = torch.empty(x2.shape[0], out_features, dtype=x.dtype, device=dev)
-    check(lib.vfl_linear(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0),
+    check(lib.vfl_linear(x2.data_ptr(), x2.stride(0), packed_weight.data_ptr(),
                          None if b is None else b.data_ptr(), out.data_ptr(), out.stride(0),
                          x2.shape[0], out_features, in_features, _dtype_code(x.dtype),
                          _stream(dev)))
@@ -93,8 +114,8 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> 
 
 
 @linear.register_fake
-def _(x, weight, bias):
-    return x.new_empty(*x.shape[:-1], weight.shape[0])
+def _(x, packed_weight, bias, out_features):
+    return x.new_empty(*x.shape[:-1], out_features)
 
 
 class TopkRules:

@@ -38,17 +38,27 @@ def _residual_norm(h: torch.Tensor, y: torch.Tensor, norm: nn.LayerNorm) -> torc
 
 
 class DecodeLinear(nn.Linear):
-    """nn.Linear whose decode-step calls -- a few hundred rows on the GPU times a weight
-    of up to 1024 x 1024 -- run on the split-K kernel (vflorence_amd::linear); other
-    shapes, fp32 and host tensors go through F.linear (hipBLASLt on the GPU)."""
+    """nn.Linear whose decode-step calls -- at most 256 rows on the GPU times a 16-bit
+    weight of up to 3072 x 1024 -- run on the split-K kernel (vflorence_amd::linear)
+    with a copy of the weight re-laid out for it, made on the first such call and again
+    whenever the weight changes; other shapes, fp32 and host tensors go through F.linear
+    (hipBLASLt on the GPU)."""
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        self._packed = None
+        self._packed_key = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if x.is_cuda:
-            from ..decoder_ops import linear, linear_fits
+        if x.is_cuda and x.dtype == self.weight.dtype:
+            from .. import decoder_ops
 
-            if x.dtype == self.weight.dtype and linear_fits(x.numel() // x.shape[-1],
-                                                            self.weight):
-                return linear(x, self.weight, self.bias)
+            if decoder_ops.linear_fits(x.numel() // x.shape[-1], self.weight):
+                key = (self.weight.data_ptr(), self.weight._version, self.weight.dtype)
+                if key != self._packed_key:
+                    self._packed = decoder_ops.pack_linear_weight(self.weight)
+                    self._packed_key = key
+                return decoder_ops.linear(x, self._packed, self.bias, self.out_features)
         return F.linear(x, self.weight, self.bias)
 
 
@@ -115,7 +125,7 @@ class BartDecoderSelfAttention(_Heads):
 
     def __init__(self, embed_dim: int, num_heads: int):
         super().__init__(embed_dim, num_heads)
-        self.qkv_proj = nn.Linear(embed_dim, 3 * embed_dim)
+        self.qkv_proj = DecodeLinear(embed_dim, 3 * embed_dim)
         self.out_proj = DecodeLinear(embed_dim, embed_dim)
         self.k_cache = self.v_cache = None
 
