@@ -261,29 +261,43 @@ int vfl_logprob_topk(const void *logits, int64_t row_stride, int64_t rows, int v
                      int n_bos, int n_forced_eos, int log_softmax, int k, float *scores,
                      int64_t *ids, void *stream);
 
+/* vfl_linear flags */
+enum vfl_linear_flags {
+  VFL_LINEAR_GELU = 1,     /* exact GELU after the bias (on the value rounded to the dtype) */
+  VFL_LINEAR_X_PACKED = 2, /* x is a packed activation (layout below); x_stride ignored    */
+  VFL_LINEAR_Y_PACKED = 4  /* y is written as a packed activation; y_stride ignored        */
+};
+
 /*
  * The decoder's projections for a decode step's rows: the fused q|k|v, the
- * self-attention output and the cross-attention query and output projections
- * (vflorence/models/bart.py:111,114,142,146 -- nn.Linear in the reference, no
- * vllm_cpu_attn counterpart):
- *   y[r][n] = sum_k x[r][k] * weight[n][k] + bias[n]        (bias may be NULL)
+ * self-attention output and the cross-attention query and output projections, and the
+ * feed-forward block fc2(gelu(fc1(h))) (vflorence/models/bart.py:111,114,142,146 and
+ * :192-201 -- nn.Linear in the reference, no vllm_cpu_attn counterpart):
+ *   y[r][n] = act(sum_k x[r][k] * weight[n][k] + bias[n])     (bias may be NULL)
  * 16-bit x / weight / bias / y (dtype VFL_BFLOAT16 or VFL_FLOAT16), fp32 sums, rounded
- * once on the store.  The weight is first re-laid out once by vfl_pack_linear_weight
- * into `packed` (vfl_linear_packed_elems(out_features, in_features) elements):
- * 1024-byte blocks of 16 rows x 32 k in the matrix cores' operand order -- block
- * (r, c), at element (r * in_features / 32 + c) * 512, holds row 16 r + l % 16,
- * k = 32 c + 8 (l / 16) .. +7 at element 8 l for l < 64 -- rows zero-padded to a
- * multiple of 32.  in_features a multiple of 256; rows at most 65535 * 32.  x and
- * `packed` 16-byte aligned, the x row stride (elements) a multiple of 8 and at least
- * in_features.  Split-K over the 8 waves of a workgroup per 32 x 32 output tile: one
- * memory round trip for the weight when in_features <= 1024.
+ * once on the store (with VFL_LINEAR_GELU: rounded, then GELU in fp32, rounded again --
+ * what a separate activation kernel computes).
+ *
+ * Packed layout (weights always; activations with the X/Y_PACKED flags): an [R][C]
+ * array stored as 1024-byte blocks of 16 rows x 32 columns in the matrix cores' operand
+ * order -- block (r, c), at element (r * C / 32 + c) * 512, holds row 16 r + l % 16,
+ * columns 32 c + 8 (l / 16) .. +7 at element 8 l for l < 64 -- with R padded to a
+ * multiple of 32: vfl_linear_packed_elems(R, C) elements.  vfl_pack_linear_weight
+ * writes it for a weight (padding rows zero); a packed output leaves its padding rows
+ * unwritten (they only reach output rows that are dropped).
+ *
+ * in_features a multiple of 256 (and out_features of 32 for a packed output); rows at
+ * most 65535 * 32.  x and `packed` 16-byte aligned; an unpacked x has a row stride
+ * (elements) that is a multiple of 8 and at least in_features.  Split-K over the 8
+ * waves of a workgroup per 32 x 32 output tile: one memory round trip for the weight
+ * when in_features <= 1024.
  */
-int64_t vfl_linear_packed_elems(int out_features, int in_features);
+int64_t vfl_linear_packed_elems(int rows, int cols);
 int vfl_pack_linear_weight(const void *weight, int64_t weight_stride, int out_features,
                            int in_features, void *packed, int dtype, void *stream);
 int vfl_linear(const void *x, int64_t x_stride, const void *packed_weight, const void *bias,
                void *y, int64_t y_stride, int64_t rows, int out_features, int in_features,
-               int dtype, void *stream);
+               int flags, int dtype, void *stream);
 
 #ifdef __cplusplus
 }

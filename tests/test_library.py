@@ -166,8 +166,8 @@ def test_linear_validates_before_launch():
     assert lib.vfl_linear_packed_elems(1000, 512) == 1024 * 512  # rows padded to 32
     assert lib.vfl_linear_packed_elems(0, 512) == 0
 
-    def call(rows=4, out=1024, inp=1024, dtype=1, xs=1024, ys=1024, ptr=None):
-        return lib.vfl_linear(ptr, xs, ptr, None, ptr, ys, rows, out, inp, dtype, None)
+    def call(rows=4, out=1024, inp=1024, dtype=1, xs=1024, ys=1024, ptr=None, flags=0):
+        return lib.vfl_linear(ptr, xs, ptr, None, ptr, ys, rows, out, inp, flags, dtype, None)
 
     assert call(dtype=0) == -2                  # fp32: no kernel
     assert call(inp=768 + 128) == -2            # in_features not a multiple of 256
@@ -179,6 +179,10 @@ def test_linear_validates_before_launch():
     assert b"null" in lib.vfl_last_error()
     assert call(ptr=16 * 1000 + 8) == -1        # 8-byte aligned x / weight
     assert b"aligned" in lib.vfl_last_error()
+    assert call(flags=8) == -1                  # unknown flag
+    assert call(out=1000, flags=4) == -2        # packed output needs out % 32 == 0
+    assert call(xs=0, flags=2) == -1            # packed x: stride ignored, nulls caught
+    assert b"null" in lib.vfl_last_error()
 
     def pack(out=1024, inp=1024, stride=1024, dtype=1, ptr=None):
         return lib.vfl_pack_linear_weight(ptr, stride, out, inp, ptr, dtype, None)

@@ -84,7 +84,9 @@ def test_linear_rejects_bad_arguments():
     w = torch.zeros(64, 1024, device=DEV, dtype=torch.bfloat16)
     packed = ops().pack_linear_weight(w)
     with pytest.raises(ValueError, match="does not hold"):
-        ops().linear(x, packed, None, 128)
+        ops().linear(x, packed, None, 96)  # 64 x 1024 elements: not a padded 96-row weight
+    with pytest.raises(ValueError, match="1024 features, the weight 512"):
+        ops().linear(x, packed, None, 128)  # read as a 128 x 512 weight
     with pytest.raises(ValueError, match="one dtype"):
         ops().linear(x.half(), packed, None, 64)
     with pytest.raises(HipAttnError, match="multiple of 256"):
@@ -116,3 +118,80 @@ def test_decoder_projections_use_the_kernel_where_it_fits():
     lin32 = DecodeLinear(1024, 1024).to(DEV)
     x32 = torch.randn(8, 1024, device=DEV)
     assert torch.equal(lin32(x32), F.linear(x32, lin32.weight, lin32.bias))
+
+
+def unpack(packed, rows, cols):
+    """The documented packed layout back to [rows, cols] (rows padded to 32 dropped)."""
+    pr = (rows + 31) // 32 * 32
+    t = packed.view(pr // 16, cols // 32, 4, 16, 8).permute(0, 3, 1, 2, 4)
+    return t.reshape(pr, cols)[:rows]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 37, 256])
+def test_feed_forward_pair_gelu_and_packed_activation(dtype, rows):
+    """fc1 with VFL_LINEAR_GELU | VFL_LINEAR_Y_PACKED, then fc2 with VFL_LINEAR_X_PACKED:
+    the packed activation holds exactly the unpacked call's rows, fc2 over it equals fc2
+    over the unpacked rows bit for bit, and the pair is within rounding of float64."""
+    d, ffn = 1024, 4096
+    g = torch.Generator(device=DEV).manual_seed(rows)
+    h = torch.randn(rows, d, device=DEV, generator=g).to(dtype)
+    w1 = (torch.randn(ffn, d, device=DEV, generator=g) / d**0.5).to(dtype)
+    b1 = (0.5 * torch.randn(ffn, device=DEV, generator=g)).to(dtype)
+    w2 = (torch.randn(d, ffn, device=DEV, generator=g) / ffn**0.5).to(dtype)
+    b2 = torch.randn(d, device=DEV, generator=g).to(dtype)
+    o = ops()
+    p1, p2 = o.pack_linear_weight(w1), o.pack_linear_weight(w2)
+    mid = o.linear(h, p1, b1, ffn, flags=o.LINEAR_GELU)
+    mid_packed = o.linear(h, p1, b1, ffn, flags=o.LINEAR_GELU | o.LINEAR_Y_PACKED)
+    assert mid_packed.numel() == o.packed_elems(rows, ffn)
+    assert torch.equal(unpack(mid_packed, rows, ffn), mid)
+    out = o.linear(mid_packed, p2, b2, d, rows=rows, flags=o.LINEAR_X_PACKED)
+    assert torch.equal(out, o.linear(mid, p2, b2, d))
+    # GELU on the rounded pre-activation, as a separate activation kernel would see it
+    pre = reference(h, w1, b1)
+    want_mid = F.gelu(pre.to(dtype).double())
+    ulp = 2**-8 if dtype == torch.bfloat16 else 2**-11
+    err = (mid.double() - want_mid).abs()
+    # a pre-activation one unit in the last place off (fp32 sums near a rounding
+    # boundary), through GELU's slope (at most 1.13), plus the final rounding
+    assert (err <= 2.5 * ulp * pre.abs() + ulp * want_mid.abs() + 1e-4).all()
+    assert_one_rounding(out, reference(mid, w2, b2), dtype)
+
+
+def test_decoder_feed_forward_matches_the_torch_ops():
+    """BartDecoderLayer._feed_forward on a decode step's rows (the fused pair) against
+    fc2(gelu(fc1(h))) through F.linear and torch's GELU, and the host path unchanged."""
+    from transformers import BartConfig
+
+    from vflorence_amd.layers.bart import BartDecoderLayer
+
+    cfg = BartConfig(d_model=1024, decoder_ffn_dim=4096, decoder_attention_heads=16)
+    torch.manual_seed(1)
+    layer = BartDecoderLayer(cfg, 0).to(DEV, torch.bfloat16)
+    h = torch.randn(200, 1024, device=DEV).to(torch.bfloat16)
+    got = layer._feed_forward(h)
+    want = F.linear(F.gelu(F.linear(h, layer.fc1.weight, layer.fc1.bias)), layer.fc2.weight,
+                    layer.fc2.bias)
+    torch.testing.assert_close(got.float(), want.float(), rtol=2e-2, atol=2e-2)
+    # more rows than a decode step: the torch ops themselves
+    hl = torch.randn(300, 1024, device=DEV).to(torch.bfloat16)
+    wantl = F.linear(F.gelu(F.linear(hl, layer.fc1.weight, layer.fc1.bias)), layer.fc2.weight,
+                     layer.fc2.bias)
+    assert torch.equal(layer._feed_forward(hl), wantl)
+
+
+def test_linear_rejects_bad_flags_and_packed_shapes():
+    from vflorence_amd._lib import HipAttnError
+
+    o = ops()
+    w = torch.zeros(96, 256, device=DEV, dtype=torch.bfloat16)
+    p = o.pack_linear_weight(w)
+    x = torch.zeros(4, 256, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(HipAttnError, match="unknown flags"):
+        o.linear(x, p, None, 96, flags=8)
+    with pytest.raises(ValueError, match="not a packed"):
+        o.linear(x.flatten(), p, None, 96, rows=4, flags=o.LINEAR_X_PACKED)
+    w_odd = torch.zeros(100, 256, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(HipAttnError, match="packed output"):
+        o.linear(x, o.pack_linear_weight(w_odd), None, 100, flags=o.LINEAR_Y_PACKED)

@@ -94,7 +94,7 @@ _SIGNATURES = {
     "vfl_pack_linear_weight": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, _i32, _vp]),
     "vfl_linear": (
         ctypes.c_int,
-        [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp],
+        [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp],
     ),
 }
 

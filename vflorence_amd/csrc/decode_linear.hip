@@ -25,6 +25,10 @@
 //   one contiguous KB.  Rows are padded with zeros to a multiple of 32.
 // - Activation rows are read as 64-byte runs (lanes 4 i .. 4 i + 3 take row i) and
 //   moved into operand order with ds_bpermute (lane l takes lane 4 (l % 16) + l / 16).
+//   Activations that one call produces for another can skip that: the feed-forward
+//   block (bart.py:192-201, fc2(gelu(fc1(h)))) runs fc1 with the exact GELU in its
+//   epilogue and its output written in the packed layout (token rows as the weight's
+//   rows), which fc2 then reads as one contiguous KB per wave load.
 #include "common.h"
 #include "mfma_ops.h"
 
@@ -58,7 +62,22 @@ __global__ __launch_bounds__(256) void pack_linear_weight_kernel(
   *reinterpret_cast<uint4 *>(packed + t * 8) = v;
 }
 
-template <int DT>
+// Element offset of (row m, column k) in a packed [rows][K] array (weight or activation).
+__device__ __forceinline__ int64_t packed_offset(int m, int k, int K) {
+  return ((int64_t)(m / 16) * (K / 32) + k / 32) * LIN_BLOCK + (16 * ((k % 32) / 8) + m % 16) * 8 +
+         k % 8;
+}
+
+// torch's exact GELU (x / 2 * (1 + erf(x / sqrt(2)))) in fp32 on a value already rounded to
+// the element type, as the separate activation kernel would see it.
+template <int DT> __device__ __forceinline__ float gelu_of_stored(float v) {
+  const float x = Mfma<DT>::widen(Mfma<DT>::narrow(v));
+  return x * 0.5f * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+// XP: x is packed (no ds_bpermute); GELU: exact GELU after the bias; YP: y is written
+// packed (rows padded to 32; padding rows are left unwritten).
+template <int DT, bool XP, bool GELU, bool YP>
 __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
     const uint16_t *__restrict__ x, int64_t ldx, const uint16_t *__restrict__ wp,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, int64_t ldy, int M, int N,
@@ -85,7 +104,10 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
     wblk[f] = wp + ((int64_t)(n0 / 16 + f) * ks + kb / 32) * LIN_BLOCK + lane * 8;
 #pragma unroll
   for (int t = 0; t < TT; ++t)
-    xrow[t] = x + (int64_t)min(m0 + 16 * t + (lane >> 2), M - 1) * ldx + kb + 8 * (lane & 3);
+    xrow[t] = XP ? x + ((int64_t)(m0 / 16 + t) * ks + kb / 32) * LIN_BLOCK + lane * 8
+                 : x + (int64_t)min(m0 + 16 * t + (lane >> 2), M - 1) * ldx + kb +
+                       8 * (lane & 3);
+  constexpr int XSTEP = XP ? LIN_BLOCK : 32;
 
   floatx4_t acc[FT][TT];
 #pragma unroll
@@ -104,14 +126,14 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
           a[g][f] = *reinterpret_cast<const uint4 *>(wblk[f] + LIN_BLOCK * (s0 + g));
 #pragma unroll
         for (int t = 0; t < TT; ++t)
-          b[g][t] = *reinterpret_cast<const uint4 *>(xrow[t] + 32 * (s0 + g));
+          b[g][t] = *reinterpret_cast<const uint4 *>(xrow[t] + XSTEP * (s0 + g));
       }
     }
 #pragma unroll
     for (int g = 0; g < LIN_BATCH; ++g) {
       if (s0 + g < steps) {
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
+        for (int t = 0; t < TT && !XP; ++t) {
           b[g][t].x = __builtin_amdgcn_ds_bpermute(src, (int)b[g][t].x);
           b[g][t].y = __builtin_amdgcn_ds_bpermute(src, (int)b[g][t].y);
           b[g][t].z = __builtin_amdgcn_ds_bpermute(src, (int)b[g][t].z);
@@ -166,7 +188,15 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
       if (m >= M) continue;
       uint32_t h[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) h[j] = Mfma<DT>::narrow(acc[f][t][j] + bv[j]);
+      for (int j = 0; j < 4; ++j) {
+        const float v = acc[f][t][j] + bv[j];
+        h[j] = Mfma<DT>::narrow(GELU ? gelu_of_stored<DT>(v) : v);
+      }
+      if constexpr (YP) {  // 4 consecutive columns of one row: 8 bytes of one lane's chunk
+        *reinterpret_cast<uint2 *>(y + packed_offset(m, n, N)) =
+            make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        continue;
+      }
       uint16_t *dst = y + (int64_t)m * ldy + n;
       if (vec_store && n + 3 < N) {
         *reinterpret_cast<uint2 *>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
@@ -200,9 +230,9 @@ static int check_features(int out_features, int in_features, int dtype, const ch
 
 using namespace vfl;
 
-extern "C" int64_t vfl_linear_packed_elems(int out_features, int in_features) {
-  if (out_features <= 0 || in_features <= 0) return 0;
-  return packed_rows(out_features) * in_features;
+extern "C" int64_t vfl_linear_packed_elems(int rows, int cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return packed_rows(rows) * cols;
 }
 
 extern "C" int vfl_pack_linear_weight(const void *weight, int64_t weight_stride,
@@ -233,9 +263,25 @@ extern "C" int vfl_pack_linear_weight(const void *weight, int64_t weight_stride,
   return launch_status("pack_linear_weight");
 }
 
+template <bool XP, bool GELU, bool YP>
+static void launch_linear(const dim3 &grid, hipStream_t s, int dtype, const void *x,
+                          int64_t x_stride, const void *wp, const void *bias, void *y,
+                          int64_t y_stride, int64_t rows, int out_features, int in_features,
+                          bool vec_store) {
+  if (dtype == VFL_BFLOAT16)
+    decode_linear_kernel<VFL_BFLOAT16, XP, GELU, YP><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
+        (const uint16_t *)x, x_stride, (const uint16_t *)wp, (const uint16_t *)bias,
+        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+  else
+    decode_linear_kernel<VFL_FLOAT16, XP, GELU, YP><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
+        (const uint16_t *)x, x_stride, (const uint16_t *)wp, (const uint16_t *)bias,
+        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+}
+
 extern "C" int vfl_linear(const void *x, int64_t x_stride, const void *packed_weight,
                           const void *bias, void *y, int64_t y_stride, int64_t rows,
-                          int out_features, int in_features, int dtype, void *stream) {
+                          int out_features, int in_features, int flags, int dtype,
+                          void *stream) {
   clear_error();
   int st = check_features(out_features, in_features, dtype, "linear");
   if (st != VFL_OK) return st;
@@ -244,18 +290,28 @@ extern "C" int vfl_linear(const void *x, int64_t x_stride, const void *packed_we
               (long long)rows);
     return rows < 0 ? VFL_E_INVALID : VFL_E_UNSUPPORTED;
   }
-  if (x_stride < in_features || y_stride < out_features) {
+  if (flags & ~(VFL_LINEAR_GELU | VFL_LINEAR_X_PACKED | VFL_LINEAR_Y_PACKED)) {
+    set_error("linear: unknown flags 0x%x", flags);
+    return VFL_E_INVALID;
+  }
+  const bool xp = flags & VFL_LINEAR_X_PACKED, yp = flags & VFL_LINEAR_Y_PACKED;
+  if ((!xp && x_stride < in_features) || (!yp && y_stride < out_features)) {
     set_error("linear: row strides must cover the rows (x %lld y %lld)", (long long)x_stride,
               (long long)y_stride);
     return VFL_E_INVALID;
+  }
+  if (yp && out_features % LIN_TILE != 0) {
+    set_error("linear: a packed output needs out_features a multiple of %d (got %d)", LIN_TILE,
+              out_features);
+    return VFL_E_UNSUPPORTED;
   }
   if (rows == 0) return VFL_OK;
   if (!x || !packed_weight || !y) {
     set_error("linear: null pointer argument");
     return VFL_E_INVALID;
   }
-  if (((uintptr_t)x | (uintptr_t)packed_weight) % 16 != 0 || x_stride % 8 != 0 ||
-      (uintptr_t)y % 2 != 0 || (uintptr_t)bias % 2 != 0) {
+  if (((uintptr_t)x | (uintptr_t)packed_weight) % 16 != 0 || (!xp && x_stride % 8 != 0) ||
+      (uintptr_t)y % (yp ? 8 : 2) != 0 || (uintptr_t)bias % 2 != 0) {
     set_error("linear: x and the packed weight must be 16-byte aligned, the x row stride a "
               "multiple of 8 elements");
     return VFL_E_INVALID;
@@ -264,13 +320,26 @@ extern "C" int vfl_linear(const void *x, int64_t x_stride, const void *packed_we
   const dim3 grid((unsigned)(packed_rows(out_features) / LIN_TILE),
                   (unsigned)((rows + LIN_TILE - 1) / LIN_TILE));
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == VFL_BFLOAT16)
-    decode_linear_kernel<VFL_BFLOAT16><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
-        (const uint16_t *)x, x_stride, (const uint16_t *)packed_weight, (const uint16_t *)bias,
-        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+  const bool gelu = flags & VFL_LINEAR_GELU;
+#define VFL_LIN(XP, G, YP)                                                                   \
+  launch_linear<XP, G, YP>(grid, s, dtype, x, x_stride, packed_weight, bias, y, y_stride, rows, \
+                           out_features, in_features, vec_store)
+  if (!xp && !gelu && !yp)
+    VFL_LIN(false, false, false);
+  else if (!xp && gelu && yp)
+    VFL_LIN(false, true, true);
+  else if (xp && !gelu && !yp)
+    VFL_LIN(true, false, false);
+  else if (!xp && gelu && !yp)
+    VFL_LIN(false, true, false);
+  else if (!xp && !gelu && yp)
+    VFL_LIN(false, false, true);
+  else if (xp && gelu && !yp)
+    VFL_LIN(true, true, false);
+  else if (xp && !gelu && yp)
+    VFL_LIN(true, false, true);
   else
-    decode_linear_kernel<VFL_FLOAT16><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
-        (const uint16_t *)x, x_stride, (const uint16_t *)packed_weight, (const uint16_t *)bias,
-        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+    VFL_LIN(true, true, true);
+#undef VFL_LIN
   return launch_status("linear");
 }

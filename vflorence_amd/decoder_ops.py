@@ -24,8 +24,9 @@ MAX_K = 16
 
 # Where vfl_linear is used: measured on MI355X at 256 rows with the weight streamed
 # from HBM, 6.8 us against hipBLASLt's 11.0 us for 1024 x 1024 and 10.8 against 12.4 us
-# for the 3072 x 1024 q|k|v; 4096-wide and 4096-deep weights (the feed-forward layers)
-# run no faster than hipBLASLt and stay there.
+# for the 3072 x 1024 q|k|v.  A lone 4096-wide or 4096-deep projection runs no faster
+# than hipBLASLt; the feed-forward pair goes through it as one unit (fc1 with the GELU
+# fused and a packed output that fc2 reads without re-ordering).
 LINEAR_K_MULTIPLE = 256
 LINEAR_MAX_IN = 1024
 LINEAR_MAX_OUT = 3072
@@ -61,15 +62,19 @@ def _(x, residual, weight, bias, eps):
     return torch.empty_like(x, memory_format=torch.contiguous_format)
 
 
-def linear_fits(rows: int, weight: torch.Tensor) -> bool:
+def linear_fits(rows: int, weight: torch.Tensor, *, max_in: int | None = LINEAR_MAX_IN,
+                max_out: int | None = LINEAR_MAX_OUT) -> bool:
     """Whether ``linear`` serves ``rows`` rows times ``weight``: a contiguous, 16-byte
-    aligned 16-bit device weight, in_features a multiple of 256 and at most 1024,
-    out_features at most 3072, at most 256 rows."""
+    aligned 16-bit device weight, in_features a multiple of 256, at most 256 rows, and
+    in / out features within ``max_in`` / ``max_out`` (None: no bound; the defaults are
+    where a lone projection beats hipBLASLt -- the feed-forward pair, which fuses its
+    activation, lifts them)."""
     out_features, in_features = weight.shape
     return (weight.is_cuda and weight.dtype in (torch.bfloat16, torch.float16)
             and weight.is_contiguous() and weight.data_ptr() % 16 == 0
             and 0 < rows <= LINEAR_MAX_ROWS and in_features % LINEAR_K_MULTIPLE == 0
-            and in_features <= LINEAR_MAX_IN and out_features <= LINEAR_MAX_OUT)
+            and (max_in is None or in_features <= max_in)
+            and (max_out is None or out_features <= max_out))
 
 
 def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
@@ -86,36 +91,66 @@ def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
     return packed
 
 
+# vfl_linear flags (include/vflorence_amd.h)
+LINEAR_GELU, LINEAR_X_PACKED, LINEAR_Y_PACKED = 1, 2, 4
+
+
+def packed_elems(rows: int, cols: int) -> int:
+    """Elements of a packed [rows, cols] array (rows padded to a multiple of 32)."""
+    return (rows + 31) // 32 * 32 * cols
+
+
 @torch.library.custom_op("vflorence_amd::linear", mutates_args=())
 def linear(x: torch.Tensor, packed_weight: torch.Tensor, bias: torch.Tensor | None,
-           out_features: int) -> torch.Tensor:
-    """``x @ weight.T + bias`` over the last dimension (nn.Linear), fp32 sums, with the
-    weight given as ``pack_linear_weight(weight)``."""
+           out_features: int, rows: int = -1, flags: int = 0) -> torch.Tensor:
+    """``act(x @ weight.T + bias)`` (nn.Linear, then GELU with ``LINEAR_GELU``), fp32
+    sums, with the weight given as ``pack_linear_weight(weight)``.  ``x`` is ``[..., in]``,
+    or with ``LINEAR_X_PACKED`` the packed output of an earlier call for ``rows`` rows.
+    The result is ``[..., out_features]``, or with ``LINEAR_Y_PACKED`` a packed 1-D
+    activation for the next call."""
     dev = _require_gpu(x, packed_weight) if bias is None else _require_gpu(x, packed_weight,
                                                                           bias)
-    in_features = x.shape[-1]
-    if packed_weight.numel() != lib.vfl_linear_packed_elems(out_features, in_features):
-        raise ValueError("linear: packed_weight does not hold a packed "
-                         f"[{out_features}, {in_features}] weight")
+    padded_out = (out_features + 31) // 32 * 32
+    if out_features <= 0 or packed_weight.dim() != 1 or packed_weight.numel() % padded_out:
+        raise ValueError(f"linear: packed_weight does not hold a packed [{out_features}, in] "
+                         "weight")
+    in_features = packed_weight.numel() // padded_out
     if bias is not None and bias.shape != (out_features,):
         raise ValueError("linear: bias must be [out_features]")
     if x.dtype != packed_weight.dtype or (bias is not None and bias.dtype != x.dtype):
         raise ValueError("linear: x, weight and bias must share one dtype")
-    x2 = x.reshape(-1, in_features)
-    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
-        x2 = x2.contiguous()
+    if flags & LINEAR_X_PACKED:
+        if rows <= 0 or x.dim() != 1 or x.numel() != packed_elems(rows, in_features):
+            raise ValueError(f"linear: x is not a packed [{rows}, {in_features}] activation")
+        x2, lead = x, (rows,)
+    else:
+        if x.shape[-1] != in_features:
+            raise ValueError(f"linear: x has {x.shape[-1]} features, the weight {in_features}")
+        x2 = x.reshape(-1, in_features)
+        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        rows, lead = x2.shape[0], x.shape[:-1]
     b = None if bias is None else bias.contiguous()
-    out = torch.empty(x2.shape[0], out_features, dtype=x.dtype, device=dev)
-    check(lib.vfl_linear(x2.data_ptr(), x2.stride(0), packed_weight.data_ptr(),
-                         None if b is None else b.data_ptr(), out.data_ptr(), out.stride(0),
-                         x2.shape[0], out_features, in_features, _dtype_code(x.dtype),
-                         _stream(dev)))
-    return out.view(*x.shape[:-1], out_features)
+    if flags & LINEAR_Y_PACKED:
+        out = torch.empty(packed_elems(rows, out_features), dtype=x.dtype, device=dev)
+        y_stride = 0
+    else:
+        out = torch.empty(rows, out_features, dtype=x.dtype, device=dev)
+        y_stride = out.stride(0)
+    x_stride = 0 if flags & LINEAR_X_PACKED else x2.stride(0)
+    check(lib.vfl_linear(x2.data_ptr(), x_stride, packed_weight.data_ptr(),
+                         None if b is None else b.data_ptr(), out.data_ptr(), y_stride, rows,
+                         out_features, in_features, flags, _dtype_code(x.dtype), _stream(dev)))
+    return out if flags & LINEAR_Y_PACKED else out.view(*lead, out_features)
 
 
 @linear.register_fake
-def _(x, packed_weight, bias, out_features):
-    return x.new_empty(*x.shape[:-1], out_features)
+def _(x, packed_weight, bias, out_features, rows=-1, flags=0):
+    if flags & LINEAR_Y_PACKED:
+        n = rows if flags & LINEAR_X_PACKED else x.numel() // x.shape[-1]
+        return x.new_empty(packed_elems(n, out_features))
+    lead = (rows,) if flags & LINEAR_X_PACKED else x.shape[:-1]
+    return x.new_empty(*lead, out_features)
 
 
 class TopkRules:

@@ -49,16 +49,22 @@ class DecodeLinear(nn.Linear):
         self._packed = None
         self._packed_key = None
 
+    def packed_weight(self) -> torch.Tensor:
+        """The weight in the kernel's packed layout (remade when the weight changes)."""
+        from .. import decoder_ops
+
+        key = (self.weight.data_ptr(), self.weight._version, self.weight.dtype)
+        if key != self._packed_key:
+            self._packed = decoder_ops.pack_linear_weight(self.weight)
+            self._packed_key = key
+        return self._packed
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.is_cuda and x.dtype == self.weight.dtype:
             from .. import decoder_ops
 
             if decoder_ops.linear_fits(x.numel() // x.shape[-1], self.weight):
-                key = (self.weight.data_ptr(), self.weight._version, self.weight.dtype)
-                if key != self._packed_key:
-                    self._packed = decoder_ops.pack_linear_weight(self.weight)
-                    self._packed_key = key
-                return decoder_ops.linear(x, self._packed, self.bias, self.out_features)
+                return decoder_ops.linear(x, self.packed_weight(), self.bias, self.out_features)
         return F.linear(x, self.weight, self.bias)
 
 
@@ -182,14 +188,35 @@ class BartDecoderLayer(nn.Module):
         self.encoder_attn = BartDecoderCrossAttention(d, heads, layer_idx)
         self.encoder_attn_layer_norm = nn.LayerNorm(d)
         self.activation_fn = _activation(config.activation_function)
-        self.fc1 = nn.Linear(d, config.decoder_ffn_dim)
-        self.fc2 = nn.Linear(config.decoder_ffn_dim, d)
+        # the fused feed-forward path computes the exact GELU (transformers' "gelu")
+        self._exact_gelu = config.activation_function == "gelu"
+        self.fc1 = DecodeLinear(d, config.decoder_ffn_dim)
+        self.fc2 = DecodeLinear(config.decoder_ffn_dim, d)
         self.final_layer_norm = nn.LayerNorm(d)
+
+    def _feed_forward(self, h: torch.Tensor) -> torch.Tensor:
+        """fc2(gelu(fc1(h))) (vflorence/models/bart.py:192-201).  For a decode step's rows
+        in bf16/fp16 on the GPU: two vfl_linear launches -- fc1 with the GELU in its
+        epilogue writing the packed layout, fc2 reading it -- else the three torch ops."""
+        if h.is_cuda and self._exact_gelu and h.dtype == self.fc1.weight.dtype:
+            from .. import decoder_ops as ops
+
+            rows = h.numel() // h.shape[-1]
+            w1, w2 = self.fc1.weight, self.fc2.weight
+            if (0 < rows <= ops.LINEAR_MAX_ROWS and ops.linear_fits(rows, w1, max_out=None)
+                    and ops.linear_fits(rows, w2, max_in=None)):
+                mid = ops.linear(h, self.fc1.packed_weight(), self.fc1.bias,
+                                 self.fc1.out_features,
+                                 flags=ops.LINEAR_GELU | ops.LINEAR_Y_PACKED)
+                out = ops.linear(mid, self.fc2.packed_weight(), self.fc2.bias,
+                                 self.fc2.out_features, rows=rows, flags=ops.LINEAR_X_PACKED)
+                return out.view(*h.shape[:-1], self.fc2.out_features)
+        return self.fc2(self.activation_fn(self.fc1(h)))
 
     def forward(self, h: torch.Tensor) -> torch.Tensor:
         h = _residual_norm(h, self.self_attn(h), self.self_attn_layer_norm)
         h = _residual_norm(h, self.encoder_attn(h), self.encoder_attn_layer_norm)
-        return _residual_norm(h, self.fc2(self.activation_fn(self.fc1(h))), self.final_layer_norm)
+        return _residual_norm(h, self._feed_forward(h), self.final_layer_norm)
 
 
 def _embed_scale(config) -> float:
