@@ -53,7 +53,11 @@ class DecodeLinear(nn.Linear):
         """The weight in the kernel's packed layout (remade when the weight changes)."""
         from .. import decoder_ops
 
-        key = (self.weight.data_ptr(), self.weight._version, self.weight.dtype)
+        try:
+            version = self.weight._version
+        except RuntimeError:  # an inference tensor has no version counter
+            version = 0
+        key = (self.weight.data_ptr(), version, self.weight.dtype)
         if key != self._packed_key:
             self._packed = decoder_ops.pack_linear_weight(self.weight)
             self._packed_key = key
