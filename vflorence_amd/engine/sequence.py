@@ -8,7 +8,6 @@ then points at the parent's blocks.
 
 from __future__ import annotations
 
-import copy
 from dataclasses import dataclass, field
 
 import torch
