@@ -82,8 +82,9 @@ def test_tokens_match_transformers_bart_large_fp32(graphs):
     assert_clean(llm)
 
 
-def test_bf16_hip_graph_steps_equal_eager_steps():
-    """bf16 beam search: replayed decode steps give the same tokens as eager ones
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_16bit_hip_graph_steps_equal_eager_steps(dtype):
+    """bf16 / fp16 beam search: replayed decode steps give the same tokens as eager ones
     (every replay reads fresh metadata from the fixed buffers)."""
     from vflorence_amd import Request, SamplingParams
 
@@ -91,7 +92,7 @@ def test_bf16_hip_graph_steps_equal_eager_steps():
     params = SamplingParams(**fx["cases"]["beam4_early"]["params"])
     got = []
     for graphs in (False, True):
-        llm = engine(fx["config"], fx["checksum"], max_num_seqs=24, dtype=torch.bfloat16,
+        llm = engine(fx["config"], fx["checksum"], max_num_seqs=24, dtype=dtype,
                      max_decoder_len=32, max_encoder_len=128, cuda_graphs=graphs)
         outs = llm.generate([Request(p) for p in fx["prompts"]], params)
         assert all(1 <= len(o.completion_token_ids) <= params.max_tokens for o in outs)
