@@ -54,12 +54,14 @@ class Scheduler:
     def schedule(self) -> tuple[list[Sequence], list[tuple[int, int]]]:
         """Admit waiting requests, give every running sequence a slot; return the step's
         sequences and its copy-on-write pairs."""
-        beams = {seq.request_id: seq.sampling_params.num_beams for seq in self.running}
-        used = sum(beams.values())
-        while self.waiting and used + self.waiting[0].sampling_params.num_beams <= self.max_num_seqs:
-            seq = self.waiting.popleft()
-            self.running.append(seq)
-            used += seq.sampling_params.num_beams
+        if self.waiting:  # admission needs the running requests' beam counts
+            beams = {seq.request_id: seq.sampling_params.num_beams for seq in self.running}
+            used = sum(beams.values())
+            while (self.waiting
+                   and used + self.waiting[0].sampling_params.num_beams <= self.max_num_seqs):
+                seq = self.waiting.popleft()
+                self.running.append(seq)
+                used += seq.sampling_params.num_beams
         seqs = list(self.running)
         bm = self.block_manager
         if bm.required_new_blocks(seqs) > bm.num_free_blocks:
