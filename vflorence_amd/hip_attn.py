@@ -39,13 +39,6 @@ FUSED_ONE_WAVE_BLOCKS = 4
 FUSED_GROUP_WAVES = 2
 
 
-def _pow2_at_least(n: int) -> int:
-    p = 1
-    while p < n:
-        p *= 2
-    return p
-
-
 def v_tile_interleaved(dtype: torch.dtype) -> bool:
     """Whether V pools of ``dtype`` store each [block][head] slice token-interleaved.
 
