@@ -49,7 +49,8 @@ def test_packed_layout_is_the_documented_operand_order():
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows,out_f,in_f", [
     (1, 1024, 1024), (7, 1024, 1024), (64, 768, 768), (256, 1024, 1024), (256, 3072, 1024),
-    (100, 1000, 512), (33, 1021, 256), (300, 96, 256), (5, 64, 4096)])
+    (100, 1000, 512), (33, 1021, 256), (300, 96, 256), (5, 64, 4096), (40, 512, 1280),
+    (17, 256, 2560), (256, 1024, 4096)])
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_linear_matches_float64(dtype, rows, out_f, in_f, with_bias):
     g = torch.Generator(device=DEV).manual_seed(rows * 7 + out_f)
@@ -96,7 +97,7 @@ def test_linear_rejects_bad_arguments():
 
 
 def test_decoder_projections_use_the_kernel_where_it_fits():
-    """DecodeLinear: decode-step rows on a 16-bit weight of up to 3072 x 1024 go through
+    """DecodeLinear: decode-step rows on a 16-bit weight of up to 3072 x 4096 go through
     the kernel (identical to calling it directly, within one rounding of float64), and
     a changed weight is re-laid out; more rows, fp32 and other shapes take F.linear."""
     from vflorence_amd.layers.bart import DecodeLinear
@@ -115,6 +116,11 @@ def test_decoder_projections_use_the_kernel_where_it_fits():
     assert torch.equal(lin(xl), F.linear(xl, lin.weight, lin.bias))
     wide = DecodeLinear(1024, 4096).to(DEV, torch.bfloat16)
     assert not ops().linear_fits(8, wide.weight)
+    deep = DecodeLinear(4096, 1024).to(DEV, torch.bfloat16)
+    xd = torch.randn(256, 4096, device=DEV).to(torch.bfloat16)
+    assert ops().linear_fits(256, deep.weight)
+    assert torch.equal(deep(xd), run(xd, deep.weight, deep.bias))
+    assert not ops().linear_fits(8, torch.zeros(64, 8192, device=DEV, dtype=torch.bfloat16))
     lin32 = DecodeLinear(1024, 1024).to(DEV)
     x32 = torch.randn(8, 1024, device=DEV)
     assert torch.equal(lin32(x32), F.linear(x32, lin32.weight, lin32.bias))

@@ -10,8 +10,11 @@
 // memory round trips, not arithmetic: a GEMM that walks K in a loop pays one round
 // trip per K step.  Here a workgroup owns a 32-feature x 32-token output tile and
 // splits K over its 8 waves.  Each wave loads the operands of up to 4 K steps of 32 in
-// one batch, so K <= 1024 costs one round trip.  The waves' partial tiles are summed
-// through LDS in a 3-level tree, and wave 0 adds the bias and stores.
+// one batch, so K <= 1024 costs one round trip; a longer K range is walked in batches
+// of 2 steps with the next batch in flight while one is multiplied.  The waves' partial
+// tiles are summed through LDS in the order of a 3-level tree (waves w and w + 4 first,
+// then (s0 + s2) + (s1 + s3)) with three barriers, and four waves then add the bias and
+// store one 16 x 16 quarter each.
 //
 // Operand order.  The product per 32-wide K step is mfma_f32_16x16x32 with A = 16
 // weight rows (features) and B = 16 token rows, giving D[feature][token]; a lane's four
@@ -37,6 +40,7 @@ namespace vfl {
 constexpr int LIN_WAVES = 8;   // waves splitting K
 constexpr int LIN_TILE = 32;   // features and tokens per workgroup
 constexpr int LIN_BATCH = 4;   // K steps whose operands are loaded together
+constexpr int LIN_PIPE_BATCH = 2;  // the same when two batches are in flight
 constexpr int LIN_K_MULTIPLE = 32 * LIN_WAVES;
 constexpr int LIN_BLOCK = 16 * 32;  // elements of one packed 16-row x 32-k weight block
 
@@ -76,22 +80,24 @@ template <int DT> __device__ __forceinline__ float gelu_of_stored(float v) {
 }
 
 // XP: x is packed (no ds_bpermute); GELU: exact GELU after the bias; YP: y is written
-// packed (rows padded to 32; padding rows are left unwritten).
-template <int DT, bool XP, bool GELU, bool YP>
+// packed (rows padded to 32; padding rows are left unwritten); PIPE: batches of
+// LIN_PIPE_BATCH steps, double-buffered (for more than LIN_BATCH steps per wave).
+template <int DT, bool XP, bool GELU, bool YP, bool PIPE>
 __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
     const uint16_t *__restrict__ x, int64_t ldx, const uint16_t *__restrict__ wp,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, int64_t ldy, int M, int N,
     int K, bool vec_store) {
   constexpr int FT = LIN_TILE / 16, TT = LIN_TILE / 16;
-  constexpr int ROW = LIN_TILE + 4;  // LDS floats per token row of a partial tile
-  __shared__ float s_part[(LIN_WAVES / 2) * LIN_TILE * ROW];
+  constexpr int SUB = FT * TT;  // 16 x 16 quarters of the tile
+  constexpr int B = PIPE ? LIN_PIPE_BATCH : LIN_BATCH;
+  // Partial tiles of four waves, each in the MFMA result order (16 bytes per lane).
+  __shared__ floatx4_t s_part[(LIN_WAVES / 2) * SUB * 64];
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int n0 = blockIdx.x * LIN_TILE, m0 = blockIdx.y * LIN_TILE;
   const int ks = K / 32;
   const int kq = K / LIN_WAVES;  // this wave's K range: [wv * kq, (wv + 1) * kq)
   const int kb = wv * kq;
-  const int col = lane & 15;
   // byte address of the lane whose 64-byte run holds this lane's operand chunk
   const int src = 4 * (4 * (lane & 15) + (lane >> 4));
 
@@ -116,10 +122,9 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
     for (int t = 0; t < TT; ++t) acc[f][t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
   const int steps = kq / 32;
-  for (int s0 = 0; s0 < steps; s0 += LIN_BATCH) {
-    uint4 a[LIN_BATCH][FT], b[LIN_BATCH][TT];
+  auto load = [&](uint4 (&a)[B][FT], uint4 (&b)[B][TT], int s0) {
 #pragma unroll
-    for (int g = 0; g < LIN_BATCH; ++g) {
+    for (int g = 0; g < B; ++g) {
       if (s0 + g < steps) {
 #pragma unroll
         for (int f = 0; f < FT; ++f)
@@ -129,8 +134,10 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
           b[g][t] = *reinterpret_cast<const uint4 *>(xrow[t] + XSTEP * (s0 + g));
       }
     }
+  };
+  auto multiply = [&](uint4 (&a)[B][FT], uint4 (&b)[B][TT], int s0) {
 #pragma unroll
-    for (int g = 0; g < LIN_BATCH; ++g) {
+    for (int g = 0; g < B; ++g) {
       if (s0 + g < steps) {
 #pragma unroll
         for (int t = 0; t < TT && !XP; ++t) {
@@ -145,66 +152,80 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
           for (int t = 0; t < TT; ++t) acc[f][t] = Mfma<DT>::qk(a[g][f], b[g][t], acc[f][t]);
       }
     }
+  };
+  if constexpr (PIPE) {
+    uint4 a0[B][FT], b0[B][TT], a1[B][FT], b1[B][TT];
+    load(a0, b0, 0);
+    for (int s0 = 0; s0 < steps; s0 += 2 * B) {
+      if (s0 + B < steps) load(a1, b1, s0 + B);
+      multiply(a0, b0, s0);
+      if (s0 + 2 * B < steps) load(a0, b0, s0 + 2 * B);
+      if (s0 + B < steps) multiply(a1, b1, s0 + B);
+    }
+  } else {
+    for (int s0 = 0; s0 < steps; s0 += B) {
+      uint4 a[B][FT], b[B][TT];
+      load(a, b, s0);
+      multiply(a, b, s0);
+    }
   }
 
-  // Sum the waves' partial tiles: at each level the upper half writes, the lower half adds.
+  // Sum the waves' partial tiles: waves 4..7 hand theirs to waves 0..3, which add and
+  // publish the four sums.
+  if (wv >= LIN_WAVES / 2) {
 #pragma unroll
-  for (int half = LIN_WAVES / 2; half >= 1; half /= 2) {
-    if (wv >= half && wv < 2 * half) {
-      float *slot = s_part + (wv - half) * LIN_TILE * ROW;
+    for (int f = 0; f < FT; ++f)
 #pragma unroll
-      for (int f = 0; f < FT; ++f)
-#pragma unroll
-        for (int t = 0; t < TT; ++t)
-          *reinterpret_cast<floatx4_t *>(slot + (16 * t + col) * ROW + 16 * f +
-                                         4 * (lane >> 4)) = acc[f][t];
-    }
-    __syncthreads();
-    if (wv < half) {
-      const float *slot = s_part + wv * LIN_TILE * ROW;
-#pragma unroll
-      for (int f = 0; f < FT; ++f)
-#pragma unroll
-        for (int t = 0; t < TT; ++t)
-          acc[f][t] += *reinterpret_cast<const floatx4_t *>(slot + (16 * t + col) * ROW +
-                                                             16 * f + 4 * (lane >> 4));
-    }
-    __syncthreads();
+      for (int t = 0; t < TT; ++t)
+        s_part[((wv - LIN_WAVES / 2) * SUB + f * TT + t) * 64 + lane] = acc[f][t];
   }
-  if (wv != 0) return;
-
+  __syncthreads();
+  if (wv < LIN_WAVES / 2) {
 #pragma unroll
-  for (int f = 0; f < FT; ++f) {
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) acc[f][t] += s_part[(wv * SUB + f * TT + t) * 64 + lane];
+  }
+  __syncthreads();
+  if (wv < LIN_WAVES / 2) {
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) s_part[(wv * SUB + f * TT + t) * 64 + lane] = acc[f][t];
+  }
+  __syncthreads();
+
+  // Wave s finishes quarter s: features 16 f + 4 (lane / 16) .. +3 of token 16 t + lane % 16.
+  for (int s = wv; s < SUB; s += LIN_WAVES) {
+    const int f = s / TT, t = s % TT;
+    const floatx4_t v = (s_part[s * 64 + lane] + s_part[(2 * SUB + s) * 64 + lane]) +
+                        (s_part[(SUB + s) * 64 + lane] + s_part[(3 * SUB + s) * 64 + lane]);
     const int n = n0 + 16 * f + 4 * (lane >> 4);
-    if (n >= N) continue;
+    const int m = m0 + 16 * t + (lane & 15);
+    if (n >= N || m >= M) continue;
     float bv[4] = {0.f, 0.f, 0.f, 0.f};
     if (bias) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) bv[j] = n + j < N ? Mfma<DT>::widen(bias[n + j]) : 0.f;
     }
+    uint32_t h[4];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      const int m = m0 + 16 * t + col;
-      if (m >= M) continue;
-      uint32_t h[4];
+    for (int j = 0; j < 4; ++j) {
+      const float o = v[j] + bv[j];
+      h[j] = Mfma<DT>::narrow(GELU ? gelu_of_stored<DT>(o) : o);
+    }
+    if constexpr (YP) {  // 4 consecutive columns of one row: 8 bytes of one lane's chunk
+      *reinterpret_cast<uint2 *>(y + packed_offset(m, n, N)) =
+          make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+      continue;
+    }
+    uint16_t *dst = y + (int64_t)m * ldy + n;
+    if (vec_store && n + 3 < N) {
+      *reinterpret_cast<uint2 *>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float v = acc[f][t][j] + bv[j];
-        h[j] = Mfma<DT>::narrow(GELU ? gelu_of_stored<DT>(v) : v);
-      }
-      if constexpr (YP) {  // 4 consecutive columns of one row: 8 bytes of one lane's chunk
-        *reinterpret_cast<uint2 *>(y + packed_offset(m, n, N)) =
-            make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-        continue;
-      }
-      uint16_t *dst = y + (int64_t)m * ldy + n;
-      if (vec_store && n + 3 < N) {
-        *reinterpret_cast<uint2 *>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (n + j < N) dst[j] = (uint16_t)h[j];
-      }
+      for (int j = 0; j < 4; ++j)
+        if (n + j < N) dst[j] = (uint16_t)h[j];
     }
   }
 }
@@ -263,19 +284,33 @@ extern "C" int vfl_pack_linear_weight(const void *weight, int64_t weight_stride,
   return launch_status("pack_linear_weight");
 }
 
+template <bool XP, bool GELU, bool YP, bool PIPE>
+static void launch_linear_dt(const dim3 &grid, hipStream_t s, int dtype, const void *x,
+                             int64_t x_stride, const void *wp, const void *bias, void *y,
+                             int64_t y_stride, int64_t rows, int out_features, int in_features,
+                             bool vec_store) {
+  if (dtype == VFL_BFLOAT16)
+    decode_linear_kernel<VFL_BFLOAT16, XP, GELU, YP, PIPE><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
+        (const uint16_t *)x, x_stride, (const uint16_t *)wp, (const uint16_t *)bias,
+        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+  else
+    decode_linear_kernel<VFL_FLOAT16, XP, GELU, YP, PIPE><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
+        (const uint16_t *)x, x_stride, (const uint16_t *)wp, (const uint16_t *)bias,
+        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+}
+
+// More K steps per wave than one batch holds: double-buffered batches.
 template <bool XP, bool GELU, bool YP>
 static void launch_linear(const dim3 &grid, hipStream_t s, int dtype, const void *x,
                           int64_t x_stride, const void *wp, const void *bias, void *y,
                           int64_t y_stride, int64_t rows, int out_features, int in_features,
                           bool vec_store) {
-  if (dtype == VFL_BFLOAT16)
-    decode_linear_kernel<VFL_BFLOAT16, XP, GELU, YP><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
-        (const uint16_t *)x, x_stride, (const uint16_t *)wp, (const uint16_t *)bias,
-        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+  if (in_features / LIN_WAVES / 32 > LIN_BATCH)
+    launch_linear_dt<XP, GELU, YP, true>(grid, s, dtype, x, x_stride, wp, bias, y, y_stride,
+                                         rows, out_features, in_features, vec_store);
   else
-    decode_linear_kernel<VFL_FLOAT16, XP, GELU, YP><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
-        (const uint16_t *)x, x_stride, (const uint16_t *)wp, (const uint16_t *)bias,
-        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+    launch_linear_dt<XP, GELU, YP, false>(grid, s, dtype, x, x_stride, wp, bias, y, y_stride,
+                                          rows, out_features, in_features, vec_store);
 }
 
 extern "C" int vfl_linear(const void *x, int64_t x_stride, const void *packed_weight,

@@ -23,12 +23,14 @@ from .hip_attn import _dtype_code, _require_gpu, _stream
 MAX_K = 16
 
 # Where vfl_linear is used: measured on MI355X at 256 rows with the weight streamed
-# from HBM, 6.8 us against hipBLASLt's 11.0 us for 1024 x 1024 and 10.8 against 12.4 us
-# for the 3072 x 1024 q|k|v.  A lone 4096-wide or 4096-deep projection runs no faster
-# than hipBLASLt; the feed-forward pair goes through it as one unit (fc1 with the GELU
-# fused and a packed output that fc2 reads without re-ordering).
+# from HBM (HIP-graph replays over more weight copies than the last-level cache holds),
+# against hipBLASLt timed the same way: 5.6 against 10.7 us for 1024 x 1024, 9.6 against
+# 11.9 us for the 3072 x 1024 q|k|v, 9.8 against 12.3 us for a 1024-wide, 4096-deep
+# projection.  A lone 4096-wide projection runs level with hipBLASLt; the feed-forward
+# pair goes through the kernel as one unit (fc1 with the GELU fused and a packed output
+# that fc2 reads without re-ordering).
 LINEAR_K_MULTIPLE = 256
-LINEAR_MAX_IN = 1024
+LINEAR_MAX_IN = 4096
 LINEAR_MAX_OUT = 3072
 LINEAR_MAX_ROWS = 256
 
