@@ -115,6 +115,18 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
                        8 * (lane & 3);
   constexpr int XSTEP = XP ? LIN_BLOCK : 32;
 
+  // Wave q < SUB finishes quarter q of the tile: features 16 (q / TT) + 4 (lane / 16) .. +3
+  // of token 16 (q % TT) + lane % 16.  Its bias is requested now, with the operands, so
+  // that no load is left for after the reduction.
+  static_assert(SUB <= LIN_WAVES, "one quarter per finishing wave");
+  const int qf = wv / TT, qt = wv % TT;
+  const int qn = n0 + 16 * qf + 4 * (lane >> 4);
+  float bv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (bias && wv < SUB) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bv[j] = qn + j < N ? Mfma<DT>::widen(bias[qn + j]) : 0.f;
+  }
+
   floatx4_t acc[FT][TT];
 #pragma unroll
   for (int f = 0; f < FT; ++f)
@@ -195,38 +207,29 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
   }
   __syncthreads();
 
-  // Wave s finishes quarter s: features 16 f + 4 (lane / 16) .. +3 of token 16 t + lane % 16.
-  for (int s = wv; s < SUB; s += LIN_WAVES) {
-    const int f = s / TT, t = s % TT;
-    const floatx4_t v = (s_part[s * 64 + lane] + s_part[(2 * SUB + s) * 64 + lane]) +
-                        (s_part[(SUB + s) * 64 + lane] + s_part[(3 * SUB + s) * 64 + lane]);
-    const int n = n0 + 16 * f + 4 * (lane >> 4);
-    const int m = m0 + 16 * t + (lane & 15);
-    if (n >= N || m >= M) continue;
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (bias) {
+  if (wv >= SUB) return;
+  const int m = m0 + 16 * qt + (lane & 15);
+  if (qn >= N || m >= M) return;
+  const floatx4_t v = (s_part[wv * 64 + lane] + s_part[(2 * SUB + wv) * 64 + lane]) +
+                      (s_part[(SUB + wv) * 64 + lane] + s_part[(3 * SUB + wv) * 64 + lane]);
+  uint32_t h[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = n + j < N ? Mfma<DT>::widen(bias[n + j]) : 0.f;
-    }
-    uint32_t h[4];
+  for (int j = 0; j < 4; ++j) {
+    const float o = v[j] + bv[j];
+    h[j] = Mfma<DT>::narrow(GELU ? gelu_of_stored<DT>(o) : o);
+  }
+  if constexpr (YP) {  // 4 consecutive columns of one row: 8 bytes of one lane's chunk
+    *reinterpret_cast<uint2 *>(y + packed_offset(m, qn, N)) =
+        make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    return;
+  }
+  uint16_t *dst = y + (int64_t)m * ldy + qn;
+  if (vec_store && qn + 3 < N) {
+    *reinterpret_cast<uint2 *>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+  } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float o = v[j] + bv[j];
-      h[j] = Mfma<DT>::narrow(GELU ? gelu_of_stored<DT>(o) : o);
-    }
-    if constexpr (YP) {  // 4 consecutive columns of one row: 8 bytes of one lane's chunk
-      *reinterpret_cast<uint2 *>(y + packed_offset(m, n, N)) =
-          make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-      continue;
-    }
-    uint16_t *dst = y + (int64_t)m * ldy + n;
-    if (vec_store && n + 3 < N) {
-      *reinterpret_cast<uint2 *>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (n + j < N) dst[j] = (uint16_t)h[j];
-    }
+    for (int j = 0; j < 4; ++j)
+      if (qn + j < N) dst[j] = (uint16_t)h[j];
   }
 }
 
