@@ -40,10 +40,9 @@ def _residual_norm(h: torch.Tensor, y: torch.Tensor, norm: nn.LayerNorm) -> torc
 class DecodeLinear(nn.Linear):
     """nn.Linear whose decode-step calls -- at most 256 rows on the GPU times a 16-bit
     weight of up to 3072 outputs and 4096 inputs -- run on the split-K kernel
-    (vflorence_amd::linear)
-    with a copy of the weight re-laid out for it, made on the first such call and again
-    whenever the weight changes; other shapes, fp32 and host tensors go through F.linear
-    (hipBLASLt on the GPU)."""
+    (vflorence_amd::linear) with a copy of the weight re-laid out for it, made on the
+    first such call and again whenever the weight changes; other shapes, fp32 and host
+    tensors go through F.linear (hipBLASLt on the GPU)."""
 
     def __init__(self, *args, **kwargs):
         super().__init__(*args, **kwargs)
