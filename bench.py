@@ -16,7 +16,8 @@ by the decoder GEMMs.
 Printed (one JSON line): whole-step algorithmic HBM GB/s (``value``), the roofline of
 the dominant kernel (cross-attention, timed live with HIP events on its stream), the
 op-level figure for 256 ragged self-attention sequences (ctx U[1, 1024], 20k-block
-pool), and the CPU restatement (oracle/) timed on the host cores.
+pool), the decoder's projections on vfl_linear against hipBLASLt (cold weights), the
+whole engine's decode step, and the CPU restatement (oracle/) timed on the host cores.
 """
 
 from __future__ import annotations
@@ -486,6 +487,71 @@ def engine_decode(torch, seed: int):
     }
 
 
+def decoder_linear_timing(torch, rows: int = REQUESTS * BEAMS, rotation_mb: int = 400):
+    """The decode-step projections of BART-large (vfl_linear) against hipBLASLt
+    (F.linear), one launch per weight copy over more copies than the 256 MB MALL holds
+    (cold weights, as in a decode step), replayed from a HIP graph; us per launch."""
+    import torch.nn.functional as F
+    from vflorence_amd import decoder_ops as dops
+    from vflorence_amd._lib import check, lib
+    from vflorence_amd.hip_attn import _dtype_code
+
+    dev = "cuda"
+    bf16 = _dtype_code(torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(1)
+    shapes = (("1024x1024 (attention out, cross q)", 1024, 1024, 0),
+              ("3072x1024 (fused qkv)", 3072, 1024, 0),
+              ("4096x1024 (fc1 + GELU, packed out)", 4096, 1024,
+               dops.LINEAR_GELU | dops.LINEAR_Y_PACKED),
+              ("1024x4096 (fc2, packed in)", 1024, 4096, dops.LINEAR_X_PACKED))
+
+    def graph_time(launch, copies):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(copies):
+                launch(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        best = float("inf")
+        for _ in range(5):
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / copies)
+        return best
+
+    out = {}
+    for name, n, k, flags in shapes:
+        copies = max(3, (rotation_mb << 20) // (n * k * 2))
+        ws = [(torch.randn(n, k, device=dev, generator=g) / k**0.5).to(torch.bfloat16)
+              for _ in range(copies)]
+        packed = [dops.pack_linear_weight(w) for w in ws]
+        bias = torch.randn(n, device=dev, generator=g).to(torch.bfloat16)
+        x = torch.randn(rows, k, device=dev, generator=g).to(torch.bfloat16)
+        xin = dops.pack_linear_weight(x) if flags & dops.LINEAR_X_PACKED else x
+        ldx = 0 if flags & dops.LINEAR_X_PACKED else k
+        yp = bool(flags & dops.LINEAR_Y_PACKED)
+        y = torch.empty(dops.packed_elems(rows, n) if yp else rows * n, device=dev,
+                        dtype=torch.bfloat16)
+
+        def vfl(i):
+            check(lib.vfl_linear(xin.data_ptr(), ldx, packed[i].data_ptr(), bias.data_ptr(),
+                                 y.data_ptr(), 0 if yp else n, rows, n, k, flags, bf16,
+                                 torch.cuda.current_stream().cuda_stream))
+
+        F.linear(x, ws[0], bias)  # hipBLASLt initialises outside the capture
+        torch.cuda.synchronize()
+        out[name] = {"vfl_linear_us": round(graph_time(vfl, copies), 2),
+                     "hipblaslt_us": round(graph_time(lambda i: F.linear(x, ws[i], bias),
+                                                      copies), 2),
+                     "weight_copies": copies}
+        del ws, packed
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(torch, wl, budget_s: float, grouped: bool = True):
     """The C restatement (oracle/, OpenMP, fp32 accumulation) on one decoder layer of the
     same workload: per sampled step, the CoW copy of that layer's two caches, the KV slot
@@ -610,6 +676,8 @@ def main():
     print("[bench] op-level self-attention, 256 ragged sequences", flush=True)
     k_avg, k_bytes, o_avg, o_bytes, _ = self_op_timing(torch, args.kernel_reps, args.seed)
     torch.cuda.empty_cache()
+    print("[bench] decoder projections: vfl_linear against hipBLASLt, cold weights", flush=True)
+    linear = decoder_linear_timing(torch)
     decoder = None
     if not args.no_engine:
         print("[bench] engine decode: BART-large bf16, 64 requests x 4 beams", flush=True)
@@ -675,6 +743,7 @@ def main():
                 "kernel_gbps": round(c_gbps, 1),
                 "kernel_bytes": int(c_bytes),
             },
+            "decoder_linear_256_rows_cold_weights": linear,
         },
         "decoder_tokens": decoder,
         "cpu_baseline": cpu,

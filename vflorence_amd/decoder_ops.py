@@ -24,9 +24,9 @@ MAX_K = 16
 
 # Where vfl_linear is used: measured on MI355X at 256 rows with the weight streamed
 # from HBM (HIP-graph replays over more weight copies than the last-level cache holds),
-# against hipBLASLt timed the same way: 5.6 against 10.7 us for 1024 x 1024, 9.6 against
-# 11.9 us for the 3072 x 1024 q|k|v, 9.8 against 12.3 us for a 1024-wide, 4096-deep
-# projection.  A lone 4096-wide projection runs level with hipBLASLt; the feed-forward
+# against hipBLASLt timed the same way: 5.3-5.6 against 10.5-10.7 us for 1024 x 1024,
+# 9.4-10.0 against 11.8-11.9 us for the 3072 x 1024 q|k|v, 9.5-9.8 against 12.3 us for a
+# 1024-wide, 4096-deep projection.  A lone 4096-wide projection runs level with hipBLASLt; the feed-forward
 # pair goes through the kernel as one unit (fc1 with the GELU fused and a packed output
 # that fc2 reads without re-ordering).
 LINEAR_K_MULTIPLE = 256
