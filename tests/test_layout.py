@@ -33,3 +33,21 @@ def test_whole_block_fill_is_layout_independent():
     for b in range(4):
         v[b] = b
     assert [hip_attn.v_cache_logical(v)[b].unique().item() for b in range(4)] == [0, 1, 2, 3]
+
+
+def test_balanced_order_pairs_long_and_short_groups_per_cu():
+    """balanced_order is longest_first with alternate runs reversed: a permutation whose
+    per-CU position sets (p, p + run, p + 2 run, ...) carry near-equal total length."""
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(256, 1025, (64,), generator=g).tolist()
+    lf = hip_attn.longest_first(lens)
+    for run in (1, 5, 16, 64, 100):
+        order = hip_attn.balanced_order(lens, run)
+        assert sorted(order) == list(range(64))
+        assert order[:run] == lf[:run]  # the first run is still longest first
+    order = hip_attn.balanced_order(lens, 16)
+    assert order[16:32] == lf[16:32][::-1] and order[32:48] == lf[32:48]
+    spread = lambda o: (lambda t: max(t) - min(t))(
+        [sum(lens[o[p + 16 * k]] for k in range(4)) for p in range(16)])
+    assert spread(order) < spread(lf)
+    assert hip_attn.balanced_order(lens, 1) == lf

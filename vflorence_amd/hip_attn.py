@@ -221,6 +221,38 @@ def longest_first(lengths) -> list[int]:
     return sorted(range(len(lengths)), key=lambda i: -int(lengths[i]))
 
 
+def balanced_order(lengths, run: int) -> list[int]:
+    """``longest_first`` with every other run of ``run`` groups reversed.
+
+    For a launch whose workgroups are all resident at once (cross-attention: one per
+    group and head).  Workgroups go to the 8 XCDs in turn and, inside an XCD, to its CUs
+    in turn.  So with H heads a CU receives the groups at order positions p, p + run,
+    p + 2 run, ... where run = CUs // H.  Sorted longest first, the CU taking p = 0
+    would then hold the longest group of every run.  Reversing alternate runs pairs
+    long with short on each CU.  Measured with 64 groups x 16 heads on MI355X's 256 CUs
+    (run 16): 32.75 us against 33.2 us.
+    """
+    order = longest_first(lengths)
+    run = max(1, int(run))
+    out = []
+    for i in range(0, len(order), run):
+        chunk = order[i:i + run]
+        out += chunk[::-1] if (i // run) % 2 else chunk
+    return out
+
+
+_cu_count: dict[int, int] = {}
+
+
+def resident_run(device, num_heads: int) -> int:
+    """The ``balanced_order`` run for a launch of one workgroup per (group, head) on
+    ``device``: its compute units divided by the heads."""
+    idx = torch.device(device).index or 0
+    if idx not in _cu_count:
+        _cu_count[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return max(1, _cu_count[idx] // max(1, num_heads))
+
+
 def get_scheduler_metadata(
     *,
     num_reqs: int,

@@ -68,7 +68,7 @@ class CrossStagingBuffers:
                 .view(self.max_rows, self.max_pages)[:n])
 
 
-def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts):
+def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts, run):
     n = len(pages)
     if n > buffers.max_rows or max(len(p) for p in pages) > buffers.max_pages:
         raise ValueError(f"{n} rows / {max(len(p) for p in pages)} pages exceed the staging "
@@ -79,7 +79,7 @@ def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts):
     h[o[0]: o[0] + n] = enc_lens
     h[o[1]: o[1] + ng + 1] = starts
     h[o[1] + ng + 1: o[1] + n + 1] = n  # empty groups past the last
-    order = hip_attn.longest_first([enc_lens[a] for a in starts[:-1]])
+    order = hip_attn.balanced_order([enc_lens[a] for a in starts[:-1]], run)
     h[o[2]: o[2] + ng] = order
     h[o[2] + ng: o[2] + n] = -1  # their workgroups exit at once
     table = h[o[3]: o[3] + buffers.max_rows * buffers.max_pages].reshape(
@@ -106,16 +106,19 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=N
     starts = beam_groups(pages, enc_lens)
     max_group = max(b - a for a, b in zip(starts, starts[1:]))
     n, ng = len(pages), len(starts) - 1
+    # every (group, head) workgroup is resident at once: balance long and short groups
+    # over the CUs (hip_attn.balanced_order)
+    run = hip_attn.resident_run(device, attn.num_heads) if device.type == "cuda" else 1
     if buffers is not None:
         seq_lens, group_start, group_order, block_table = _stage_into(buffers, pages, enc_lens,
-                                                                      starts)
+                                                                      starts, run)
         max_group = hip_attn.MAX_GROUP_SIZE  # one launch shape for every batch of n rows
     else:
         block_table = torch.nn.utils.rnn.pad_sequence(
             [p.to(torch.int32).cpu() for p in pages], batch_first=True
         )
         width = block_table.shape[1]
-        order = hip_attn.longest_first([enc_lens[a] for a in starts[:-1]])
+        order = hip_attn.balanced_order([enc_lens[a] for a in starts[:-1]], run)
         # One host->device copy:
         # [seq_lens (n) | group starts (ng + 1) | group order (ng) | block table (n * width)].
         host = torch.cat(
