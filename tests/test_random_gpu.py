@@ -1,0 +1,73 @@
+"""Seeded random sweep of the attention entry point against the oracle.
+
+Each case draws its dtype, head size, head count, row count, ragged context lengths
+(zeros included), workgroup waves, row groups sharing one table (cross-attention
+beams) and dispatch order (none, longest first, balanced), so combinations that the
+targeted tests do not enumerate are still compared with the float64 oracle under the
+same bars (1e-5 relative in fp32, 2e-2 absolute in bf16 / fp16).
+"""
+
+import random
+
+import pytest
+import torch
+
+from test_kernels_gpu import DEV, check, grouped_case, hip, make_case
+
+pytestmark = pytest.mark.gpu
+
+CASES = 100
+
+
+def draw(seed: int):
+    r = random.Random(seed)
+    dtype = r.choice([torch.bfloat16, torch.float16, torch.float32])
+    head_dim = r.choice([64, 64, 128])
+    H = r.randint(1, 16)
+    waves = r.choice([0, 1, 2, 4, 8])
+    grouped = r.random() < 0.5
+    order = r.choice(["none", "longest", "balanced"])
+    return r, dtype, head_dim, H, waves, grouped, order
+
+
+def run(q, kc, vc, lens, table, scale, waves, starts, gmax, order):
+    hip_attn = hip()
+    firsts = lens.tolist() if starts is None else [lens[i].item() for i in starts[:-1]]
+    perm = {"none": None, "longest": hip_attn.longest_first(firsts),
+            "balanced": hip_attn.balanced_order(firsts, hip_attn.resident_run(DEV, q.shape[1]))}
+    meta = hip_attn.get_scheduler_metadata(
+        num_reqs=q.shape[0], num_heads=q.shape[1], num_kv_heads=q.shape[1],
+        head_dim=q.shape[2], dtype=q.dtype, block_size=kc.shape[2],
+        waves_per_workgroup=waves,
+        group_start=None if starts is None else starts.to(DEV), max_group_size=gmax,
+        group_order=None if perm[order] is None else torch.tensor(
+            perm[order], dtype=torch.int32, device=DEV))
+    out = torch.empty(q.shape, dtype=q.dtype, device=DEV)
+    hip_attn.attention_with_kv_cache(
+        q.contiguous().to(DEV), kc.to(DEV), hip_attn.v_cache_from_logical(vc).to(DEV), out,
+        torch.arange(q.shape[0] + 1, dtype=torch.int32, device=DEV), lens.to(DEV),
+        scale=scale, causal=False, block_table=table.to(DEV), scheduler_metadata=meta)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_random_attention_matches_oracle(seed):
+    r, dtype, head_dim, H, waves, grouped, order = draw(seed)
+    scale = head_dim ** -0.5
+    if grouped:
+        sizes = [r.randint(1, 8) for _ in range(r.randint(1, 6))]
+        enc = [r.choice([0, r.randint(1, 40), r.randint(200, 700)]) for _ in sizes]
+        enc[0] = max(enc[0], 1)  # a table of at least one column
+        q, kc, vc, L, table, starts = grouped_case(sizes, enc, H=H, D=head_dim, dtype=dtype,
+                                                   seed=seed)
+        gmax = max(sizes)
+    else:
+        lens = [r.choice([0, r.randint(1, 17), r.randint(18, 400)])
+                for _ in range(r.randint(1, 40))]
+        q, kc, vc, L, table = make_case(lens, H=H, D=head_dim, dtype=dtype, seed=seed)
+        starts, gmax = None, 1
+    print(f"[random] seed {seed}: {dtype} D {head_dim} H {H} rows {q.shape[0]} waves {waves} "
+          f"groups {'yes' if grouped else 'no'} order {order}", flush=True)
+    out = run(q, kc, vc, L, table, scale, waves, starts, gmax, order)
+    check(out, q, kc, vc, L, table, scale)
