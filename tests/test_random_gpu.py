@@ -103,3 +103,51 @@ def test_random_beam_groups_fused_write_matches_two_steps_and_oracle(seed):
         # the plain one (the library's), so the merge of wave states rounds differently
         oracle_check(two, fused, k2, v2, L, table, H=H, D=head_dim)
     oracle_check(one, fused, k1, v1, L, table, H=H, D=head_dim)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_decode_linear_chains_match_float64(seed):
+    """vfl_linear over random shapes: x (row-major, or packed by an earlier call with
+    LINEAR_Y_PACKED) times a packed weight, with and without bias and GELU.  The packed
+    output holds exactly the row-major call's rows; a call on it equals the call on the
+    row-major rows bit for bit; results are within one rounding of float64 (GELU: of
+    GELU on the rounded pre-activation)."""
+    import torch.nn.functional as F
+    from test_linear_gpu import assert_one_rounding, ops, reference, unpack
+
+    r = random.Random(2000 + seed)
+    dtype = r.choice([torch.bfloat16, torch.float16])
+    rows = r.choice([1, r.randint(2, 31), r.randint(32, 256)])
+    k1 = 256 * r.randint(1, 16)
+    # a packed output needs a multiple of 32; the chained call a multiple of 256
+    n1 = 32 * r.randint(1, 40) if r.random() < 0.5 else 256 * r.randint(1, 16)
+    n2 = r.randint(1, 1100)
+    gelu = r.random() < 0.5
+    with_bias = r.random() < 0.7
+    print(f"[random linear] seed {seed}: {dtype} rows {rows} {k1} -> {n1} -> {n2} gelu {gelu} "
+          f"bias {with_bias}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn(rows, k1, device=DEV, generator=g).to(dtype)
+    w1 = (torch.randn(n1, k1, device=DEV, generator=g) / k1**0.5).to(dtype)
+    b1 = torch.randn(n1, device=DEV, generator=g).to(dtype) if with_bias else None
+    o = ops()
+    flags = o.LINEAR_GELU if gelu else 0
+    p1 = o.pack_linear_weight(w1)
+    mid = o.linear(x, p1, b1, n1, flags=flags)
+    mid_packed = o.linear(x, p1, b1, n1, flags=flags | o.LINEAR_Y_PACKED)
+    assert torch.equal(unpack(mid_packed, rows, n1), mid)
+    pre = reference(x, w1, b1)
+    if gelu:
+        want = F.gelu(pre.to(dtype).double())
+        ulp = 2**-8 if dtype == torch.bfloat16 else 2**-11
+        err = (mid.double() - want).abs()
+        assert (err <= 2.5 * ulp * pre.abs() + ulp * want.abs() + 1e-4).all()
+    else:
+        assert_one_rounding(mid, pre, dtype)
+    if n1 % 256:
+        return  # the second call needs in_features a multiple of 256
+    w2 = (torch.randn(n2, n1, device=DEV, generator=g) / n1**0.5).to(dtype)
+    p2 = o.pack_linear_weight(w2)
+    out = o.linear(mid_packed, p2, None, n2, rows=rows, flags=o.LINEAR_X_PACKED)
+    assert torch.equal(out, o.linear(mid, p2, None, n2))
+    assert_one_rounding(out, reference(mid, w2, None), dtype)
