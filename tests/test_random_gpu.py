@@ -151,3 +151,48 @@ def test_random_decode_linear_chains_match_float64(seed):
     out = o.linear(mid_packed, p2, None, n2, rows=rows, flags=o.LINEAR_X_PACKED)
     assert torch.equal(out, o.linear(mid, p2, None, n2))
     assert_one_rounding(out, reference(mid, w2, None), dtype)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_logprob_topk_matches_processor_and_topk(seed):
+    """log-softmax + generation rules + top-k over random vocab sizes, k, row counts,
+    lengths and rule sets, against LogitsProcessor + torch.topk."""
+    from test_decoder_ops_gpu import canon, ops as dops, reference
+    from transformers import GenerationConfig
+
+    from vflorence_amd.sampling_params import SamplingParams
+
+    r = random.Random(3000 + seed)
+    vocab = r.choice([r.randint(2, 64), r.randint(65, 5000), r.randint(5000, 60000)])
+    k = r.randint(1, min(16, vocab))
+    rows = r.randint(1, 300)
+    tok = lambda: r.randrange(vocab)
+    rules = {}
+    if r.random() < 0.4:
+        rules["min_length"] = r.randint(1, 8)
+    if r.random() < 0.3:
+        rules["forced_bos_token_id"] = tok()
+    if r.random() < 0.3:
+        rules["forced_eos_token_id"] = sorted({tok() for _ in range(r.randint(1, 3))})
+    if r.random() < 0.4:
+        rules["suppress_tokens"] = sorted({tok() for _ in range(r.randint(1, 6))})
+    if r.random() < 0.3:
+        rules["begin_suppress_tokens"] = sorted({tok() for _ in range(r.randint(1, 4))})
+    log_softmax = r.random() < 0.7
+    eos = sorted({tok() for _ in range(r.randint(1, 2))})
+    print(f"[random topk] seed {seed}: vocab {vocab} k {k} rows {rows} rules {rules} "
+          f"eos {eos} log_softmax {log_softmax}", flush=True)
+    params = SamplingParams(eos_token_id=eos, **rules).with_defaults(
+        SamplingParams.from_generation_config(GenerationConfig()))
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    logits = torch.randn(rows, vocab, device=DEV, generator=g) * 4
+    max_length, begin_index = 10, 2
+    lengths = torch.tensor([r.randint(1, max_length) for _ in range(rows)], dtype=torch.int64,
+                           device=DEV)
+    (want_v, want_i), proc, ref = reference(logits, k, log_softmax, params, lengths, vocab,
+                                            max_length, begin_index)
+    got_v, got_i = dops().logprob_topk(logits, k, log_softmax=log_softmax, lengths=lengths,
+                                       rules=proc.topk_rules())
+    torch.testing.assert_close(got_v, want_v, rtol=1e-6, atol=1e-5)
+    assert canon(ref.gather(1, got_i), got_i) == canon(want_v, want_i)
+    assert ((got_i >= 0) & (got_i < vocab)).all()
