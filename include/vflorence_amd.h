@@ -150,7 +150,11 @@ int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_hea
  * such groups row by row).  With group_start NULL every row is its own group
  * (num_groups == num_rows).
  * group_order (optional, int32 [num_groups]): a permutation of the groups giving
- * the dispatch order (longest first balances the tail); NULL = natural order.
+ * the dispatch order; NULL = natural order.  Longest first balances the tail of a
+ * launch that runs in several rounds.  When every (group, head) workgroup is resident
+ * at once, a CU receives the groups at order positions p, p + CUs / heads, ...; then
+ * reversing every other run of CUs / heads groups of the longest-first order pairs long
+ * with short groups on each CU.
  *
  * query: [num_rows][num_heads][head_dim], token / head strides in elements.
  * out:   [num_rows][num_heads][head_dim], contiguous.
