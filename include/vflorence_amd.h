@@ -87,7 +87,9 @@ const char *vfl_get_isa(int dtype, int block_size, int head_dim);
  * key / value are [num_tokens][num_heads][head_dim] with arbitrary token and head
  * strides (in elements) and a contiguous last dimension -- the strided views a
  * fused qkv projection produces.  Negative slots are skipped (padding tokens), as
- * are slots past the end of the pool.  Bit-exact copy.
+ * are slots past the end of the pool.  Bit-exact copy.  block_size must be 16, the
+ * block size the attention kernels read (VFL_E_UNSUPPORTED otherwise, nothing
+ * launched).
  */
 int vfl_reshape_and_cache(const void *key, const void *value,
                           int64_t key_stride_token, int64_t key_stride_head,

@@ -155,6 +155,12 @@ def test_reshape_and_copy_validate_before_launch():
                                      1, None) == -2
     assert lib.vfl_reshape_and_cache(None, None, 0, 0, 0, 0, None, None, None, 0, 16, 64, 16, 10,
                                      1, None) == 0
+    # block sizes without an attention kernel are refused before anything launches
+    # (the 16-bit V layout would land outside the block-head slice)
+    for bs in (8, 32, 18):
+        assert lib.vfl_reshape_and_cache(None, None, 0, 0, 0, 0, None, None, None, 4, 16, 64,
+                                         bs, 10, 1, None) == -2
+        assert b"block_size" in lib.vfl_last_error()
     assert lib.vfl_copy_blocks(None, 24, None, None, 5, 1000, 10, None, None) == -1  # not /16
     assert lib.vfl_copy_blocks(None, 24, None, None, 0, 1024, 10, None, None) == 0
     assert lib.vfl_copy_blocks(None, 24, None, None, 5, 1024, 10, None, None) == -1  # nulls
@@ -201,3 +207,7 @@ def test_cpu_tensors_are_rejected():
     x = torch.zeros(3, 2, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="no CPU path"):
         hip_attn.reshape_and_cache(x, x, k, k, torch.zeros(3, dtype=torch.int64))
+    # a pool of another block size is refused on the host, whatever the device
+    k32 = torch.zeros(4, 2, 32, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="block_size=32"):
+        hip_attn.reshape_and_cache(x, x, k32, k32, torch.zeros(3, dtype=torch.int64))

@@ -36,6 +36,10 @@ template <> struct Elem<VFL_FLOAT16> {
 
 inline int elem_bytes(int dtype) { return dtype == VFL_FLOAT32 ? 4 : 2; }
 
+// Tokens per KV block: the only block size with attention kernels (the 16-bit V layout
+// interleaves tokens by four inside it).
+constexpr int KV_BLOCK_SIZE = 16;
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 

@@ -125,12 +125,15 @@ def reshape_and_cache(
     head strides and a contiguous last dim; caches are contiguous [NB, H, bs, D]; slots
     are int64 [T].  Negative slots are skipped.  ``isa`` is accepted and ignored.
     """
-    dev = _require_gpu(key, value, k_cache, v_cache, slot_mapping)
-    if key.dim() != 3 or value.shape != key.shape:
-        raise ValueError(f"key/value must be [T, H, D] of one shape, got {key.shape}, {value.shape}")
     if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
         raise ValueError("k_cache/v_cache must be [num_blocks, H, block_size, D] of one shape")
     num_blocks, num_heads, block_size, head_dim = k_cache.shape
+    if block_size not in SUPPORTED_BLOCK_SIZES:
+        raise ValueError(f"block_size={block_size} has no attention kernel; supported: "
+                         f"{sorted(SUPPORTED_BLOCK_SIZES)}")
+    dev = _require_gpu(key, value, k_cache, v_cache, slot_mapping)
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError(f"key/value must be [T, H, D] of one shape, got {key.shape}, {value.shape}")
     if key.shape[1:] != (num_heads, head_dim):
         raise ValueError(f"key is {tuple(key.shape)} but caches hold H={num_heads}, D={head_dim}")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
