@@ -126,6 +126,49 @@ def test_decoder_projections_use_the_kernel_where_it_fits():
     assert torch.equal(lin32(x32), F.linear(x32, lin32.weight, lin32.bias))
 
 
+def test_packed_weight_follows_in_place_updates_and_repack():
+    """The packed copy is rewritten in place (captured graphs keep its address): an
+    ordinary weight updated in place is re-laid out on the next eager call; an
+    inference-mode weight, which has no version counter, after ``repack()``; a HIP graph
+    captured before the update reads the new weight once ``repack()`` ran."""
+    from vflorence_amd.layers.bart import DecodeLinear
+
+    torch.manual_seed(1)
+    lin = DecodeLinear(1024, 1024).to(DEV, torch.bfloat16)
+    lin.repack()
+    addr = lin.packed_weight().data_ptr()
+    x = torch.randn(64, 1024, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.mul_(-1)
+    assert torch.equal(lin(x), run(x, lin.weight, lin.bias))
+    assert lin.packed_weight().data_ptr() == addr
+    with torch.inference_mode():
+        inf = DecodeLinear(1024, 1024).to(DEV, torch.bfloat16)
+        assert inf.weight.is_inference()
+        before = inf(x)
+        inf.weight.mul_(0.5)
+        inf.repack()
+        after = inf(x)
+    assert not torch.equal(before, after)
+    assert torch.equal(after, run(x, inf.weight, inf.bias))
+    # a graph captured over the packed copy sees a later update after repack()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        lin(x)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = lin(x)
+    with torch.no_grad():
+        lin.weight.add_(0.01)
+    lin.repack()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, run(x, lin.weight, lin.bias))
+
+
 def unpack(packed, rows, cols):
     """The documented packed layout back to [rows, cols] (rows padded to 32 dropped)."""
     pr = (rows + 31) // 32 * 32

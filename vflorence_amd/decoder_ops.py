@@ -79,15 +79,22 @@ def linear_fits(rows: int, weight: torch.Tensor, *, max_in: int | None = LINEAR_
             and (max_out is None or out_features <= max_out))
 
 
-def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
+def pack_linear_weight(weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``weight`` ([out, in], 16-bit, on the GPU) re-laid out in the matrix cores' operand
     order for ``linear`` (1 KB blocks of 16 rows x 32 inputs in lane order, rows padded
-    to a multiple of 32): a new 1-D tensor of the same dtype."""
+    to a multiple of 32): a 1-D tensor of the same dtype, new or ``out`` (rewritten in
+    place, so HIP graphs captured over it read the new values)."""
     dev = _require_gpu(weight)
     out_features, in_features = weight.shape
     w = weight.contiguous()
-    packed = torch.empty(max(1, lib.vfl_linear_packed_elems(out_features, in_features)),
-                         dtype=weight.dtype, device=dev)
+    elems = max(1, lib.vfl_linear_packed_elems(out_features, in_features))
+    if out is not None:
+        if out.shape != (elems,) or out.dtype != weight.dtype or out.device != weight.device:
+            raise ValueError(f"out must be a {weight.dtype} tensor of {elems} elements on "
+                             f"{weight.device}")
+        packed = out
+    else:
+        packed = torch.empty(elems, dtype=weight.dtype, device=dev)
     check(lib.vfl_pack_linear_weight(w.data_ptr(), w.stride(0), out_features, in_features,
                                      packed.data_ptr(), _dtype_code(weight.dtype), _stream(dev)))
     return packed

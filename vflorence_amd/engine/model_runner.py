@@ -188,6 +188,14 @@ class ModelRunner:
         self._no_pages = torch.zeros(0, dtype=torch.int32)
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
 
+    def repack_weights(self) -> None:
+        """Make the decoder's packed projection weights follow the current weights, after
+        an in-place weight update (the copies are rewritten in place, so captured decode
+        steps stay valid)."""
+        from ..utils.loader import repack_decode_weights
+
+        repack_decode_weights(self.model)
+
     # -- pools -------------------------------------------------------------------------
 
     def allocate_kv_cache(self) -> None:

@@ -40,27 +40,48 @@ def _residual_norm(h: torch.Tensor, y: torch.Tensor, norm: nn.LayerNorm) -> torc
 class DecodeLinear(nn.Linear):
     """nn.Linear whose decode-step calls -- at most 256 rows on the GPU times a 16-bit
     weight of up to 3072 outputs and 4096 inputs -- run on the split-K kernel
-    (vflorence_amd::linear) with a copy of the weight re-laid out for it, made on the
-    first such call and again whenever the weight changes; other shapes, fp32 and host
-    tensors go through F.linear (hipBLASLt on the GPU)."""
+    (vflorence_amd::linear) with a copy of the weight re-laid out for it; other shapes,
+    fp32 and host tensors go through F.linear (hipBLASLt on the GPU).
+
+    The packed copy is made by ``repack`` (``load_model`` calls it after loading the
+    weights) and rewritten in place, so HIP graphs captured over it stay valid.  An
+    eager call also repacks when the weight's version counter moved (an in-place update
+    of an ordinary tensor).  Inference tensors have no version counter: after updating
+    such a weight in place call ``repack`` (``ModelRunner.repack_weights`` does it for
+    the whole decoder), as also after any update that captured graphs must see."""
 
     def __init__(self, *args, **kwargs):
         super().__init__(*args, **kwargs)
         self._packed = None
         self._packed_key = None
 
-    def packed_weight(self) -> torch.Tensor:
-        """The weight in the kernel's packed layout (remade when the weight changes)."""
+    def _weight_key(self):
+        w = self.weight
+        version = None if w.is_inference() else w._version
+        return (w.data_ptr(), version, w.dtype, tuple(w.shape))
+
+    def repack(self) -> None:
+        """Re-lay out the current weight into the packed copy (in place when one of the
+        right size exists)."""
         from .. import decoder_ops
 
-        try:
-            version = self.weight._version
-        except RuntimeError:  # an inference tensor has no version counter
-            version = 0
-        key = (self.weight.data_ptr(), version, self.weight.dtype)
-        if key != self._packed_key:
-            self._packed = decoder_ops.pack_linear_weight(self.weight)
-            self._packed_key = key
+        w = self.weight
+        if not (w.is_cuda and w.dtype in (torch.bfloat16, torch.float16)
+                and decoder_ops.linear_fits(1, w, max_in=None, max_out=None)):
+            self._packed = self._packed_key = None
+            return
+        out = self._packed
+        if out is not None and (out.dtype != w.dtype or out.device != w.device
+                                or out.numel() != decoder_ops.packed_elems(*w.shape)):
+            out = None
+        with torch.no_grad():
+            self._packed = decoder_ops.pack_linear_weight(w.detach(), out=out)
+        self._packed_key = self._weight_key()
+
+    def packed_weight(self) -> torch.Tensor:
+        """The weight in the kernel's packed layout."""
+        if self._packed is None or self._weight_key() != self._packed_key:
+            self.repack()
         return self._packed
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

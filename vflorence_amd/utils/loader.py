@@ -144,4 +144,15 @@ def load_model(config, state_dict: dict | None = None):
         model = BartForConditionalGeneration(hf).to(config.dtype)
     fuse_projections(model, state_dict)
     model.load_state_dict(state_dict, strict=True)
+    repack_decode_weights(model)
     return model.eval()
+
+
+def repack_decode_weights(model) -> None:
+    """Refresh every decode-step projection's packed weight copy in place (after loading
+    or updating weights; captured HIP graphs read the refreshed copies)."""
+    from ..layers.bart import DecodeLinear
+
+    for module in model.modules():
+        if isinstance(module, DecodeLinear):
+            module.repack()
