@@ -8,14 +8,26 @@ identical on CPU and GPU), so the tests rebuild them instead of storing them; ea
 config records the weights' checksum.
 
 Each request is generated on its own (batch 1, no padding); the engine later runs
-them batched.  Greedy cases also record, per request, the smallest gap between the
-best and second-best processed score over its steps: a fp32 GPU run may only take a
-different token where that gap is within float noise.
+them batched.  Every case also records, per request and per step, the margin that decides the
+step: greedy, the gap between the best and second-best processed score; beam search,
+the gap between the ``num_beams``-th and the next accumulated score (which
+candidates live on), and at the last step also between the best two (which
+hypothesis is returned).  A fp32 GPU run may only take a different token where such a gap is
+within float noise, and a 16-bit run's first differing step can be read against it.
+
+The beam cases at BART-large and Florence-2-base shapes follow the reference's own
+parity settings (tests/verify_parity.py:70-108,177): BART with 4 beams, EOS
+suppressed (``min_length`` past ``max_tokens``), length penalty 2 and no repeated
+3-grams; Florence-2-base with 3 beams and neutral decoding that stops at EOS.  Their
+prompts are drawn from seeded streams; a prompt whose decisive margin at some step
+is below 1e-4 (a tie within fp32 rounding of the accumulated scores) is skipped and
+listed with its margin, and each case stores the prompts it kept.
 """
 
 from __future__ import annotations
 
 import json
+import math
 import os
 import sys
 import time
@@ -71,6 +83,35 @@ def prompts(vocab: int, lengths: list[int], seed: int) -> list[list[int]]:
     return [torch.randint(3, vocab, (n,), generator=g).tolist() for n in lengths]
 
 
+class _CandidateGaps:
+    """Records, at every beam-search step, the margin that decides it: the gap between
+    the ``num_beams``-th and the next accumulated score over all beams (which candidates
+    continue) and, at the last step, also the gap between the best two (which hypothesis
+    is returned).  That is the whole decision when no candidate finishes before the last
+    step (the BART-large and Florence-2-base beam cases); with earlier finishes it is a
+    partial view.  Wraps transformers' ``_get_top_k_continuations``, which receives
+    those scores."""
+
+    def __init__(self, model, num_beams: int, max_tokens: int):
+        self.model, self.gaps = model, []
+        self.num_beams, self.max_tokens = num_beams, max_tokens
+        self._orig = model._get_top_k_continuations
+        model._get_top_k_continuations = self._hook
+
+    def _hook(self, *args, **kwargs):
+        acc = kwargs["accumulated_log_probs"]
+        nb = self.num_beams
+        top = acc.topk(nb + 1, dim=-1).values[0]
+        gap = float(top[nb - 1] - top[nb])
+        if len(self.gaps) == self.max_tokens - 1:
+            gap = min(gap, float(top[0] - top[1]))
+        self.gaps.append(gap if math.isfinite(gap) else None)
+        return self._orig(*args, **kwargs)
+
+    def close(self):
+        self.model._get_top_k_continuations = self._orig
+
+
 def hf_generate(model, ids: list[int], params: dict):
     kw = dict(max_new_tokens=params["max_tokens"], num_beams=params["num_beams"], do_sample=False,
               repetition_penalty=params["repetition_penalty"], eos_token_id=params["eos_token_id"],
@@ -84,15 +125,33 @@ def hf_generate(model, ids: list[int], params: dict):
               decoder_start_token_id=model.config.decoder_start_token_id,
               pad_token_id=model.config.pad_token_id, output_scores=True,
               return_dict_in_generate=True)
-    with torch.no_grad():
-        out = model.generate(torch.tensor([ids]), attention_mask=torch.ones(1, len(ids),
-                                                                          dtype=torch.long), **kw)
+    recorder = (_CandidateGaps(model, params["num_beams"], params["max_tokens"])
+                if params["num_beams"] > 1 else None)
+    try:
+        with torch.no_grad():
+            out = model.generate(torch.tensor([ids]),
+                                 attention_mask=torch.ones(1, len(ids), dtype=torch.long), **kw)
+    finally:
+        if recorder is not None:
+            recorder.close()
     tokens = out.sequences[0].tolist()[1:]
     if params["num_beams"] == 1:
         gaps = [float(s[0].topk(2).values.diff().abs()) for s in out.scores]
-        return tokens, min(gaps) if gaps else None
+        return tokens, gaps
     pad = model.config.pad_token_id
-    return [t for t in tokens if t != pad], None
+    return [t for t in tokens if t != pad], recorder.gaps
+
+
+def min_gap(gaps):
+    finite = [g for g in gaps or () if g is not None]
+    return min(finite) if finite else None
+
+
+def case_record(params, outs):
+    """Tokens per request, each request's per-step gaps and their minimum."""
+    return {"params": params, "tokens": [t for t, _ in outs],
+            "gaps": [[None if g is None else round(g, 7) for g in gp] for _, gp in outs],
+            "min_gap": [min_gap(gp) for _, gp in outs]}
 
 
 def build(config_kwargs: dict):
@@ -105,15 +164,57 @@ def build(config_kwargs: dict):
     return config, model, state_dict_checksum(sd)
 
 
+# The reference's beam parity settings (tests/verify_parity.py:81-87): EOS suppressed
+# so every beam runs max_tokens steps, length penalty 2, no repeated 3-grams.
+BART_BEAM4 = {**BASE, "max_tokens": 24, "num_beams": 4, "min_length": 25,
+              "length_penalty": 2.0, "no_repeat_ngram_size": 3}
+# The same without the history rule: the engine then takes its candidates from the
+# fused log-softmax + rules + top-k kernel instead of the torch path.
+BART_BEAM4_FUSED = {**BASE, "max_tokens": 24, "num_beams": 4, "min_length": 25}
+# Florence-2's neutral decoding with 3 beams (tests/verify_parity.py:135-139): stops
+# at EOS.
+FLORENCE_BEAM3 = {**BASE, "max_tokens": 32, "num_beams": 3}
+
+
+# A beam case keeps a prompt only if every step's decisive margin is at least this: a
+# smaller one is a tie within the rounding of fp32 accumulated scores (one ulp at 128 is
+# 1.5e-5), which no other summation order can be required to break the same way.
+BEAM_MARGIN = 1e-4
+
+
+def beam_case(model, vocab: int, params: dict, count: int, length_fn, seed: int, tag: str):
+    """``count`` prompts drawn in order from a seeded stream (lengths from ``length_fn``),
+    each generated with ``params``; a prompt with a decisive margin below BEAM_MARGIN is
+    skipped and recorded in ``skipped``."""
+    g = torch.Generator().manual_seed(seed)
+    kept, outs, skipped = [], [], []
+    while len(kept) < count:
+        n = length_fn(g)
+        ids = torch.randint(3, vocab, (n,), generator=g).tolist()
+        tokens, gaps = hf_generate(model, ids, params)
+        margin = min_gap(gaps)
+        print(tag, n, len(tokens), margin, flush=True)
+        if margin is None or margin < BEAM_MARGIN:
+            skipped.append({"length": n, "min_gap": margin})
+            continue
+        kept.append(ids)
+        outs.append((tokens, gaps))
+    record = case_record(params, outs)
+    record["prompts"] = kept
+    record["skipped"] = skipped
+    return record
+
+
 def florence2_base() -> dict:
     config, model, checksum = build(FLORENCE_BASE)
     reqs = prompts(config.vocab_size, [587] * 6, seed=4)
     params = {**BASE, "max_tokens": 32}
     outs = [hf_generate(model, ids, params) for ids in reqs]
     print("florence2_base", [len(t) for t, _ in outs], flush=True)
-    return {"config": FLORENCE_BASE, "checksum": checksum, "prompts": reqs,
-            "cases": {"greedy32": {"params": params, "tokens": [t for t, _ in outs],
-                                   "min_gap": [gp for _, gp in outs]}}}
+    cases = {"greedy32": case_record(params, outs)}
+    cases["beam3"] = beam_case(model, config.vocab_size, FLORENCE_BEAM3, 6, lambda g: 587,
+                               seed=5, tag="florence2_base beam3")
+    return {"config": FLORENCE_BASE, "checksum": checksum, "prompts": reqs, "cases": cases}
 
 
 def main():
@@ -130,8 +231,7 @@ def main():
     for name, over in SMALL_CASES.items():
         params = {**BASE, **over}
         outs = [hf_generate(model, ids, params) for ids in reqs]
-        small["cases"][name] = {"params": params, "tokens": [t for t, _ in outs],
-                                "min_gap": [g for _, g in outs]}
+        small["cases"][name] = case_record(params, outs)
         print(name, [len(t) for t, _ in outs], flush=True)
     fixtures["small"] = small
 
@@ -145,10 +245,14 @@ def main():
     for ids in reqs:
         outs.append(hf_generate(model, ids, params))
         print("large", len(ids), len(outs[-1][0]), f"{time.time() - t0:.0f}s", flush=True)
+    cases = {"greedy64": case_record(params, outs)}
+    for name, params, seed in (("beam4", BART_BEAM4, 6), ("beam4_fused", BART_BEAM4_FUSED, 7)):
+        cases[name] = beam_case(
+            model, config.vocab_size, params, 8,
+            lambda g: int(torch.randint(128, 1025, (1,), generator=g)), seed=seed,
+            tag=f"large {name}")
     fixtures["bart_large"] = {"config": LARGE, "checksum": checksum, "prompts": reqs,
-                              "cases": {"greedy64": {"params": params,
-                                                     "tokens": [t for t, _ in outs],
-                                                     "min_gap": [gp for _, gp in outs]}}}
+                              "cases": cases}
     fixtures["florence2_base"] = florence2_base()
     with open(OUT, "w") as f:
         json.dump(fixtures, f)

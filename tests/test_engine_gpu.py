@@ -82,6 +82,70 @@ def test_tokens_match_transformers_bart_large_fp32(graphs):
     assert_clean(llm)
 
 
+BEAM_CASES = {  # fixture, case, engine limits
+    "bart_large_beam4": ("bart_large", "beam4", dict(max_num_seqs=32, max_decoder_len=24,
+                                                      max_encoder_len=1024)),
+    "bart_large_beam4_fused": ("bart_large", "beam4_fused",
+                               dict(max_num_seqs=32, max_decoder_len=24, max_encoder_len=1024)),
+    "florence2_base_beam3": ("florence2_base", "beam3",
+                             dict(max_num_seqs=18, max_decoder_len=32, max_encoder_len=587)),
+}
+
+
+@pytest.mark.parametrize("graphs", [False, True], ids=["eager", "hipgraph"])
+@pytest.mark.parametrize("name", list(BEAM_CASES))
+def test_beam_tokens_match_transformers_fp32(name, graphs):
+    """Beam search at the real model shapes, fp32, batched, against transformers'
+    generate() one request at a time (tests/verify_parity.py:70-108,177 settings):
+    BART-large with 4 beams (length penalty 2, no repeated 3-grams -- the torch rule
+    path -- or without it -- the fused top-k kernel path), EOS suppressed, 24 tokens;
+    Florence-2-base shapes with 3 beams, 587 encoder tokens, 32 tokens.  Token-exact."""
+    from vflorence_amd import Request, SamplingParams
+
+    fixture, case, limits = BEAM_CASES[name]
+    fx = fixtures()[fixture]
+    c = fx["cases"][case]
+    assert all(g >= 1e-4 for g in c["min_gap"])  # no decisive step within fp32 rounding
+    llm = engine(fx["config"], fx["checksum"], dtype=torch.float32, cuda_graphs=graphs,
+                 **limits)
+    outs = llm.generate([Request(p) for p in c["prompts"]], SamplingParams(**c["params"]))
+    assert [o.completion_token_ids for o in outs] == c["tokens"]
+    assert_clean(llm)
+
+
+def first_difference(a, b):
+    n = min(len(a), len(b))
+    return next((i for i in range(n) if a[i] != b[i]), None if len(a) == len(b) else n)
+
+
+@pytest.mark.parametrize("name", list(BEAM_CASES))
+def test_beam_tokens_bf16_against_the_fp32_fixture(name):
+    """The same beam cases in bf16 with HIP graphs, held to the reference's bf16 bar
+    (tests/verify_parity.py:59-67): every request returns as many tokens as
+    transformers' fp32 run.  Token differences are reported with the first differing
+    step and the fp32 run's decisive margin at that step."""
+    from vflorence_amd import Request, SamplingParams
+
+    fixture, case, limits = BEAM_CASES[name]
+    fx = fixtures()[fixture]
+    c = fx["cases"][case]
+    llm = engine(fx["config"], fx["checksum"], dtype=torch.bfloat16, cuda_graphs=True,
+                 **limits)
+    outs = llm.generate([Request(p) for p in c["prompts"]], SamplingParams(**c["params"]))
+    got = [o.completion_token_ids for o in outs]
+    report = []
+    for r, (a, b) in enumerate(zip(got, c["tokens"])):
+        assert len(a) == len(b), f"request {r}: {len(a)} tokens against {len(b)}"
+        first = first_difference(a, b)
+        if first is not None:
+            report.append(f"request {r}: first difference at step {first}, fp32 margin "
+                          f"there {c['gaps'][r][first]:.2e}")
+    same = sum(a == b for a, b in zip(got, c["tokens"]))
+    print(f"[bf16 beam parity] {name}: {same}/{len(got)} requests token-identical to the "
+          f"fp32 fixture; " + ("; ".join(report) if report else "no differences"), flush=True)
+    assert_clean(llm)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_16bit_hip_graph_steps_equal_eager_steps(dtype):
     """bf16 / fp16 beam search: replayed decode steps give the same tokens as eager ones
