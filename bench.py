@@ -77,7 +77,10 @@ class Layer:
             a.num_heads, a.head_dim = NUM_HEADS, HEAD_DIM
 
 
-def build_workload(torch, seed: int):
+def build_workload(torch, seed: int, num_layers: int = NUM_LAYERS):
+    """The benchmarked decode workload: pools per layer, the 128-step beam schedule,
+    staged cross-attention and the synthetic q/k/v.  ``num_layers`` below 12 builds the
+    same workload over fewer layers (the parity test of this workload uses it)."""
     from vflorence_amd import workloads
     from vflorence_amd.layers import attention
 
@@ -91,7 +94,7 @@ def build_workload(torch, seed: int):
     shape = (num_blocks, NUM_HEADS, BLOCK, HEAD_DIM)
     cshape = (num_cross, NUM_HEADS, BLOCK, HEAD_DIM)
     layers = []
-    for _ in range(NUM_LAYERS):
+    for _ in range(num_layers):
         pools = [workloads.fill_normal_(torch.empty(s, dtype=dtype, device=dev), 0.125, g)
                  for s in (shape, shape, cshape, cshape)]
         layers.append(Layer(*pools))
@@ -109,14 +112,14 @@ def build_workload(torch, seed: int):
             enc_rows.append(E)
     staged = attention.stage_cross(layers, pages, enc_rows, BLOCK, "gfx950")
     qkv = [workloads.fill_normal_(torch.empty(rows, 3 * NUM_HEADS * HEAD_DIM, dtype=dtype,
-                                              device=dev), 0.125, g) for _ in range(NUM_LAYERS)]
+                                              device=dev), 0.125, g) for _ in range(num_layers)]
     qc = [workloads.fill_normal_(torch.empty(rows, NUM_HEADS, HEAD_DIM, dtype=dtype, device=dev),
-                                 1.0, g) for _ in range(NUM_LAYERS)]
+                                 1.0, g) for _ in range(num_layers)]
     return dict(plans=plans, layers=layers, staged=staged, qkv=qkv, qc=qc, enc=enc,
                 enc_rows=enc_rows, pages=pages, num_blocks=num_blocks, num_cross=num_cross)
 
 
-def step_bytes(plan, enc, elem=2, grouped=True):
+def step_bytes(plan, enc, elem=2, grouped=True, self_only=False):
     from vflorence_amd import workloads
 
     rows = len(plan.context_lens)
@@ -126,14 +129,18 @@ def step_bytes(plan, enc, elem=2, grouped=True):
     else:
         self_b = workloads.self_attention_bytes(plan.context_lens, NUM_HEADS, HEAD_DIM, elem,
                                                 BLOCK)
+    if self_only:
+        return self_b
     cross_b = workloads.cross_attention_bytes(enc, rows, NUM_HEADS, HEAD_DIM, elem, BLOCK)
     cow_b = len(plan.copies) * 2 * NUM_LAYERS * (NUM_HEADS * BLOCK * HEAD_DIM * elem) * 2
     return NUM_LAYERS * (self_b + cross_b) + cow_b, self_b, cross_b, cow_b
 
 
-def capture_steps(torch, wl, grouped=True):
+def capture_steps(torch, wl, grouped=True, keep_outputs=False):
     """One HIP graph per decode step of the schedule.  ``grouped``: each request's beams
-    form one self-attention row group (own tables, shared blocks read once)."""
+    form one self-attention row group (own tables, shared blocks read once).
+    ``keep_outputs``: also return, per step, the [(self out, cross out)] per layer that
+    its graph writes (every step keeps its own output buffers)."""
     from vflorence_amd import hip_attn
     from vflorence_amd.layers import attention
     from vflorence_amd.utils.context import set_context
@@ -145,7 +152,7 @@ def capture_steps(torch, wl, grouped=True):
     qsl = torch.arange(rows + 1, dtype=torch.int32, device=dev)
     scale = HEAD_DIM**-0.5
     pool = torch.cuda.graph_pool_handle()
-    graphs, keep = [], []
+    graphs, keep, outputs = [], [], []
     side = torch.cuda.Stream()
     for t, plan in enumerate(wl["plans"]):
         width = max(len(r) for r in plan.block_tables)
@@ -181,17 +188,21 @@ def capture_steps(torch, wl, grouped=True):
             set_context(context_lens=lens, block_tables=tables, slot_mapping=slots,
                         query_start_loc=qsl, self_metadata=meta, isa="gfx950",
                         cross_staged=wl["staged"])
+            outs = []
             try:
                 if src is not None:
                     hip_attn.copy_blocks(caches, src, dst, ptrs, staged=staged)
                 for i, L in enumerate(wl["layers"]):
                     q, k, v = (x.reshape(rows, NUM_HEADS, HEAD_DIM)
                                for x in wl["qkv"][i].chunk(3, dim=-1))
-                    attention.decoder_self_attention(q, k, v, L.self_attn.k_cache,
-                                                     L.self_attn.v_cache, scale)
-                    attention.decoder_cross_attention(wl["qc"][i], i, scale)
+                    so = attention.decoder_self_attention(q, k, v, L.self_attn.k_cache,
+                                                          L.self_attn.v_cache, scale)
+                    co = attention.decoder_cross_attention(wl["qc"][i], i, scale)
+                    if keep_outputs:
+                        outs.append((so, co))
             finally:
                 set_context()
+            return outs
 
         if t == 0:  # eager once: loads, plans and registrations happen outside capture
             side.wait_stream(torch.cuda.current_stream())
@@ -201,10 +212,85 @@ def capture_steps(torch, wl, grouped=True):
             torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, pool=pool):
-            run()
+            outputs.append(run())
         graphs.append(g)
     torch.cuda.synchronize()
+    if keep_outputs:
+        return graphs, keep, outputs
     return graphs, keep
+
+
+def schedule_order(n: int, steps: int = DECODE_STEPS) -> list[int]:
+    """The decode steps ``n`` timed replays walk: whole passes over the schedule in order,
+    then, for a remainder shorter than the schedule, that many steps at an even stride
+    across it -- so every timed region covers the whole schedule (short and long
+    contexts alike) whatever ``n`` is."""
+    order = [t for _ in range(n // steps) for t in range(steps)]
+    rem = n % steps
+    order += [j * steps // rem for j in range(rem)]
+    return order
+
+
+KERNEL_NAMES = {  # kernel name prefixes of the decode step's launches
+    "cross": "void vfl::paged_decode_mfma_kernel<1, 64, 4, 2, false>",
+    "self": "void vfl::paged_decode_shared_kernel<1, 64, 2, 2, true>",
+    "self_rows": "void vfl::paged_decode_mfma_kernel<1, 64, 2, 2, true>",
+    "cow": "vfl::copy_blocks_kernel",
+}
+
+
+def in_step_kernel_times(torch, graphs):
+    """Each kernel's duration inside the decode-step graphs: one pass over the whole
+    schedule's graphs replayed under torch.profiler, which records every kernel a graph
+    launches with its device timestamps (the same timestamps rocprofv3's kernel trace
+    reports).  Returns {kernel: [per-launch seconds in launch order]}."""
+    from torch.profiler import ProfilerActivity, profile
+
+    for g in graphs:  # warm: the pass below starts from the same state as any other
+        g.replay()
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        for g in graphs:
+            g.replay()
+        torch.cuda.synchronize()
+    out = {k: [] for k in KERNEL_NAMES}
+    events = [e for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
+    events.sort(key=lambda e: e.time_range.start)
+    for e in events:
+        for k, prefix in KERNEL_NAMES.items():
+            if e.name.startswith(prefix):
+                out[k].append(e.device_time * 1e-6)
+    return out
+
+
+def workloads_cross_bytes(wl) -> int:
+    from vflorence_amd import workloads
+
+    return workloads.cross_attention_bytes(wl["enc"], REQUESTS * BEAMS, NUM_HEADS, HEAD_DIM, 2,
+                                           BLOCK)
+
+
+def self_in_step_table(durations, plans, grouped):
+    """In-step self-attention launches (``durations`` in launch order, NUM_LAYERS per
+    step) by the step's context length: mean duration and algorithmic GB/s per bucket
+    of decode steps."""
+    if len(durations) != len(plans) * NUM_LAYERS:
+        return None
+    buckets = ((0, 16), (16, 32), (32, 64), (64, 96), (96, 128))
+    out = []
+    for lo, hi in buckets:
+        secs, nbytes, n = 0.0, 0, 0
+        for t in range(lo, min(hi, len(plans))):
+            b = step_bytes(plans[t], None, grouped=grouped, self_only=True)
+            for s_ in durations[t * NUM_LAYERS:(t + 1) * NUM_LAYERS]:
+                secs += s_
+                nbytes += b
+                n += 1
+        if n:
+            out.append({"context_tokens": f"{lo + 1}..{hi}", "launches": n,
+                        "avg_us": round(secs / n * 1e6, 2),
+                        "gbps": round(nbytes / secs / 1e9, 1)})
+    return out
 
 
 def time_kernel(torch, launch, n: int):
@@ -561,7 +647,7 @@ def cpu_baseline(torch, wl, budget_s: float, grouped: bool = True):
 
     from oracle import oracle as orc
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads, host = host_threads()
     L0 = wl["layers"][0]
 
     def host_bits(t):
@@ -612,7 +698,28 @@ def cpu_baseline(torch, wl, budget_s: float, grouped: bool = True):
                    f"cross attention), oracle/paged_attention.c with OpenMP, "
                    f"{spent:.1f} s"),
         "seconds": round(spent, 2),
+        "host": host,
     }
+
+
+def host_threads():
+    """OpenMP threads for the CPU baseline and a description of the host: every core this
+    process may run on, unless the environment sets OMP_NUM_THREADS lower (a host shared
+    between jobs states this job's share that way)."""
+    affinity = len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(affinity, int(env)) if env.isdigit() and int(env) > 0 else affinity
+    return threads, {"cpu_model": model, "cores_in_affinity": affinity,
+                     "omp_num_threads_env": env or None, "threads_used": threads}
 
 
 def main():
@@ -640,17 +747,18 @@ def main():
     plans = wl["plans"]
     per_step = [step_bytes(p, wl["enc"], grouped=grouped) for p in plans]
 
-    for i in range(args.warmup):
-        graphs[i % DECODE_STEPS].replay()
+    for t in schedule_order(args.warmup):
+        graphs[t].replay()
     torch.cuda.synchronize()
-    print(f"[bench] timing {args.steps} decode steps", flush=True)
+    timed_steps = schedule_order(args.steps)
+    print(f"[bench] timing {args.steps} decode steps (steps {timed_steps[0]}..{timed_steps[-1]} "
+          f"of the {DECODE_STEPS}-step schedule)", flush=True)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     e0.record()
     total_bytes = 0
-    for i in range(args.steps):
-        t = (args.warmup + i) % DECODE_STEPS
+    for t in timed_steps:
         graphs[t].replay()
         total_bytes += per_step[t][0]
     e1.record()
@@ -659,17 +767,43 @@ def main():
     elapsed = e0.elapsed_time(e1) * 1e-3
     gbps = total_bytes / elapsed / 1e9
     ms_per_step = elapsed * 1e3 / args.steps
-
-    print("[bench] timing the cross-attention kernel", flush=True)
-    c_avg, c_bytes = cross_kernel_timing(torch, wl, args.kernel_reps)
-    c_gbps = c_bytes / c_avg / 1e9
+    c_bytes = workloads_cross_bytes(wl)
+    print("[bench] in-step kernel durations: the schedule's graphs replayed under "
+          "torch.profiler", flush=True)
+    try:
+        in_step = in_step_kernel_times(torch, graphs)
+        if len(in_step["cross"]) != DECODE_STEPS * NUM_LAYERS:
+            raise RuntimeError(f"the profiled pass saw {len(in_step['cross'])} cross-attention "
+                               f"launches, expected {DECODE_STEPS * NUM_LAYERS}")
+    except RuntimeError as exc:
+        print(f"[bench] in-step kernel durations unavailable: {exc}", file=sys.stderr,
+              flush=True)
+        in_step = None
     del graphs, keep
     torch.cuda.empty_cache()
+
+    print("[bench] timing the cross-attention kernel back to back", flush=True)
+    c_avg, _ = cross_kernel_timing(torch, wl, args.kernel_reps)
+    c_gbps = c_bytes / c_avg / 1e9
+    if in_step is not None:
+        cross_in_step = in_step["cross"]
+        c_step_avg = sum(cross_in_step) / len(cross_in_step)
+        self_key = "self" if grouped else "self_rows"
+        self_by_ctx = self_in_step_table(in_step[self_key], wl["plans"], grouped)
+        cow = in_step["cow"]
+        measured_over = (f"{len(cross_in_step)} launches inside the decode-step graphs, one "
+                         f"pass over the whole {DECODE_STEPS}-step schedule (torch.profiler "
+                         f"device timestamps)")
+    else:
+        c_step_avg, self_by_ctx, cow = c_avg, None, []
+        measured_over = "back-to-back launches (the in-step pass was unavailable)"
+    c_step_gbps = c_bytes / c_step_avg / 1e9
 
     cpu = None
     if args.cpu_seconds > 0:
         print("[bench] CPU baseline (oracle restatement)", flush=True)
         cpu = cpu_baseline(torch, wl, args.cpu_seconds, grouped)
+    wl_plans, wl_enc = wl["plans"], wl["enc"]
     del wl
     torch.cuda.empty_cache()
 
@@ -720,12 +854,15 @@ def main():
             "bound": "hbm",
             "kernel": ("paged_decode_mfma_kernel<bf16, D=64, 4 waves, 2 blocks/stage> "
                        "(cross-attention, 4 beams per group)"),
-            "achieved": round(c_gbps, 1),
+            "achieved": round(c_step_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(c_gbps / HBM_PEAK_GBPS, 4),
+            "frac": round(c_step_gbps / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic(c_bytes),
-            "avg_launch_us": round(c_avg * 1e6, 2),
+            "avg_launch_us": round(c_step_avg * 1e6, 2),
+            "avg_launch_us_measured_over": measured_over,
+            "back_to_back_avg_launch_us": round(c_avg * 1e6, 2),
+            "back_to_back_frac": round(c_gbps / HBM_PEAK_GBPS, 4),
             "algorithmic_bytes_per_launch": int(c_bytes),
         },
         "ops": {
@@ -739,9 +876,19 @@ def main():
                 "op_bytes": int(o_bytes),
             },
             "cross_attention_64x4": {
-                "kernel_us": round(c_avg * 1e6, 2),
-                "kernel_gbps": round(c_gbps, 1),
+                "in_step_us": round(c_step_avg * 1e6, 2),
+                "in_step_gbps": round(c_step_gbps, 1),
+                "back_to_back_us": round(c_avg * 1e6, 2),
+                "back_to_back_gbps": round(c_gbps, 1),
                 "kernel_bytes": int(c_bytes),
+            },
+            "self_attention_in_step_by_context": self_by_ctx,
+            "copy_on_write_in_step": {
+                "launches": len(cow),
+                "avg_us": round(sum(cow) / len(cow) * 1e6, 2) if cow else None,
+                "gbps": (round(sum(step_bytes(p, wl_enc, grouped=grouped)[3]
+                                   for p in wl_plans if p.copies) / sum(cow) / 1e9, 1)
+                         if cow else None),
             },
             "decoder_linear_256_rows_cold_weights": linear,
         },
