@@ -6,7 +6,8 @@
  * Every entry point takes plain device pointers, element strides and sizes, and a
  * hipStream_t passed as `void *` (NULL = the legacy default stream).  No entry point
  * allocates device memory; the one that needs scratch space (vfl_copy_blocks with
- * overlapping pairs) takes it from the caller.  All work is enqueued asynchronously
+ * overlapping pairs) takes it from the caller, or from a buffer the library holds in
+ * each GPU's memory (vfl_copy_blocks_noalloc).  All work is enqueued asynchronously
  * on `stream`, in call order, so a caller that issues copy_blocks ->
  * reshape_and_cache -> attention_with_kv_cache on one stream gets the reference's
  * ordering.
@@ -53,6 +54,9 @@ enum vfl_dtype { VFL_FLOAT32 = 0, VFL_BFLOAT16 = 1, VFL_FLOAT16 = 2 };
  *                           partition of the rows gives the same results.
  */
 enum vfl_group_tables { VFL_GROUP_SHARED_TABLE = 0, VFL_GROUP_OWN_TABLES = 1 };
+
+/* bytes of the per-GPU staging buffer behind vfl_copy_blocks_noalloc (64 MiB) */
+#define VFL_NOALLOC_STAGING_BYTES (64u << 20)
 
 /* status codes */
 enum vfl_status {
@@ -226,6 +230,22 @@ int vfl_self_attention_with_kv_write(const void *query, int64_t query_stride_tok
 int vfl_copy_blocks(void *const *caches, int num_caches, const int64_t *src,
                     const int64_t *dst, int64_t num_pairs, int64_t block_bytes,
                     int64_t num_blocks, void *staging, void *stream);
+
+/*
+ * No counterpart in the reference: vfl_copy_blocks for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same copy and semantics; with `staged` non-zero the
+ * gather-then-scatter goes through a staging buffer the library holds in each GPU's
+ * device memory from the first call on that GPU until the process ends, of
+ * VFL_NOALLOC_STAGING_BYTES bytes: num_caches * num_pairs * block_bytes beyond that is
+ * refused with VFL_E_INVALID before anything is launched.  No device memory is
+ * allocated.  Calls that overlap on one GPU (other streams, other threads) share that
+ * buffer and race; serialise them.  The buffer keeps the last call's contents and
+ * needs no clearing (every staged byte is written before it is read).
+ */
+int vfl_copy_blocks_noalloc(void *const *caches, int num_caches, const int64_t *src,
+                            const int64_t *dst, int64_t num_pairs, int64_t block_bytes,
+                            int64_t num_blocks, int staged, void *stream);
 
 /*
  * The decoder layer's residual + LayerNorm (vflorence/models/bart.py:192-201:

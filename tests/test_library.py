@@ -164,6 +164,17 @@ def test_reshape_and_copy_validate_before_launch():
     assert lib.vfl_copy_blocks(None, 24, None, None, 5, 1000, 10, None, None) == -1  # not /16
     assert lib.vfl_copy_blocks(None, 24, None, None, 0, 1024, 10, None, None) == 0
     assert lib.vfl_copy_blocks(None, 24, None, None, 5, 1024, 10, None, None) == -1  # nulls
+    # the no-allocation variant: the same checks, and staging beyond the library's
+    # buffer refused on the host before anything launches
+    from vflorence_amd._lib import NOALLOC_STAGING_BYTES
+
+    assert lib.vfl_copy_blocks_noalloc(None, 24, None, None, 5, 1000, 10, 1, None) == -1
+    assert lib.vfl_copy_blocks_noalloc(None, 24, None, None, 0, 1024, 10, 1, None) == 0
+    assert lib.vfl_copy_blocks_noalloc(None, 24, None, None, 5, 1024, 10, 0, None) == -1
+    fake = 1 << 20
+    pairs = NOALLOC_STAGING_BYTES // (24 * 32768) + 1
+    assert lib.vfl_copy_blocks_noalloc(fake, 24, fake, fake, pairs, 32768, 10, 1, None) == -1
+    assert b"exceeds" in lib.vfl_last_error()
 
 
 def test_linear_validates_before_launch():

@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "vfl_attention_with_kv_cache",
     "vfl_self_attention_with_kv_write",
     "vfl_copy_blocks",
+    "vfl_copy_blocks_noalloc",
     "vfl_add_layer_norm",
     "vfl_logprob_topk",
     "vfl_linear_packed_elems",
@@ -81,6 +82,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp],
     ),
+    "vfl_copy_blocks_noalloc": (
+        ctypes.c_int,
+        [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
+    ),
     "vfl_add_layer_norm": (
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _f32, _i32, _vp],
@@ -97,6 +102,10 @@ _SIGNATURES = {
         [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp],
     ),
 }
+
+
+# bytes of the library's per-GPU staging buffer (VFL_NOALLOC_STAGING_BYTES)
+NOALLOC_STAGING_BYTES = 64 << 20
 
 
 class LibraryMissing(ImportError):

@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace vfl {
@@ -151,6 +153,40 @@ __global__ __launch_bounds__(COPY_THREADS) void copy_blocks_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Library-held staging for vfl_copy_blocks_noalloc: one array per GPU, in the code
+// object's device memory, so the entry point never allocates.  Host code must not pass
+// the array's name to a kernel (it is a host-side stand-in there); the device address
+// of each GPU's copy is looked up once per device with hipGetSymbolAddress.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[VFL_NOALLOC_STAGING_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mutex;
+static void *g_scratch_ptr[MAX_DEVICES];
+
+// Device address of the current device's scratch array (looked up on the first call on
+// that device); nullptr with the error set on failure.
+static void *device_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+    set_error("copy_blocks_noalloc: no current HIP device (device %d)", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      set_error("copy_blocks_noalloc: hipGetSymbolAddress on device %d failed: %s", dev,
+                hipGetErrorString(err));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace vfl
 
 using namespace vfl;
@@ -229,30 +265,33 @@ extern "C" int vfl_reshape_and_cache(const void *key, const void *value,
   return launch_status("reshape_and_cache");
 }
 
-extern "C" int vfl_copy_blocks(void *const *caches, int num_caches, const int64_t *src,
-                               const int64_t *dst, int64_t num_pairs, int64_t block_bytes,
-                               int64_t num_blocks, void *staging, void *stream) {
-  clear_error();
+// Host checks shared by both copy entry points; VFL_OK when there is work to launch, 1
+// when there is nothing to do.
+static int check_copy_args(const char *who, void *const *caches, int num_caches,
+                           const int64_t *src, const int64_t *dst, int64_t num_pairs,
+                           int64_t block_bytes) {
   if (num_caches < 0 || num_pairs < 0 || block_bytes <= 0 || block_bytes % 16 != 0) {
-    set_error("copy_blocks: bad sizes (caches %d pairs %lld block_bytes %lld)", num_caches,
+    set_error("%s: bad sizes (caches %d pairs %lld block_bytes %lld)", who, num_caches,
               (long long)num_pairs, (long long)block_bytes);
     return VFL_E_INVALID;
   }
-  if (num_caches == 0 || num_pairs == 0) return VFL_OK;
+  if (num_caches == 0 || num_pairs == 0) return 1;
   if (!caches || !src || !dst) {
-    set_error("copy_blocks: null pointer argument");
+    set_error("%s: null pointer argument", who);
     return VFL_E_INVALID;
   }
   if (num_pairs > 65535 || num_caches > 65535) {
-    set_error("copy_blocks: at most 65535 pairs and 65535 caches per call (got %lld, %d)",
+    set_error("%s: at most 65535 pairs and 65535 caches per call (got %lld, %d)", who,
               (long long)num_pairs, num_caches);
     return VFL_E_INVALID;
   }
-  if (staging && ((uintptr_t)staging % 16) != 0) {
-    set_error("copy_blocks: staging buffer must be 16-byte aligned");
-    return VFL_E_INVALID;
-  }
-  hipStream_t s = (hipStream_t)stream;
+  return VFL_OK;
+}
+
+// The copy itself: one direct pass, or gather into `staging` then scatter from it.
+static int launch_copy(void *const *caches, int num_caches, const int64_t *src,
+                       const int64_t *dst, int64_t num_pairs, int64_t block_bytes,
+                       int64_t num_blocks, uint8_t *staging, hipStream_t s, const char *who) {
   const unsigned gx = (unsigned)((block_bytes + COPY_BYTES_PER_WG - 1) / COPY_BYTES_PER_WG);
   const dim3 grid(gx, (unsigned)num_pairs, (unsigned)num_caches);
   if (!staging) {
@@ -260,11 +299,51 @@ extern "C" int vfl_copy_blocks(void *const *caches, int num_caches, const int64_
                                                      num_blocks, 0, nullptr);
   } else {
     copy_blocks_kernel<<<grid, COPY_THREADS, 0, s>>>(caches, src, dst, num_pairs, block_bytes,
-                                                     num_blocks, 1, (uint8_t *)staging);
-    int st = launch_status("copy_blocks");
+                                                     num_blocks, 1, staging);
+    int st = launch_status(who);
     if (st != VFL_OK) return st;
     copy_blocks_kernel<<<grid, COPY_THREADS, 0, s>>>(caches, src, dst, num_pairs, block_bytes,
-                                                     num_blocks, 2, (uint8_t *)staging);
+                                                     num_blocks, 2, staging);
   }
-  return launch_status("copy_blocks");
+  return launch_status(who);
 }
+
+extern "C" int vfl_copy_blocks_noalloc(void *const *caches, int num_caches, const int64_t *src,
+                                       const int64_t *dst, int64_t num_pairs,
+                                       int64_t block_bytes, int64_t num_blocks, int staged,
+                                       void *stream) {
+  clear_error();
+  int st = check_copy_args("copy_blocks_noalloc", caches, num_caches, src, dst, num_pairs,
+                           block_bytes);
+  if (st != VFL_OK) return st == 1 ? VFL_OK : st;
+  uint8_t *staging = nullptr;
+  if (staged) {
+    const int64_t need = (int64_t)num_caches * num_pairs * block_bytes;
+    if (need > (int64_t)VFL_NOALLOC_STAGING_BYTES) {
+      set_error("copy_blocks_noalloc: staging %lld bytes (%d caches x %lld pairs x %lld) "
+                "exceeds the library's %lld-byte buffer",
+                (long long)need, num_caches, (long long)num_pairs, (long long)block_bytes,
+                (long long)VFL_NOALLOC_STAGING_BYTES);
+      return VFL_E_INVALID;
+    }
+    staging = (uint8_t *)device_scratch();
+    if (!staging) return VFL_E_LAUNCH;
+  }
+  return launch_copy(caches, num_caches, src, dst, num_pairs, block_bytes, num_blocks, staging,
+                     (hipStream_t)stream, "copy_blocks_noalloc");
+}
+
+extern "C" int vfl_copy_blocks(void *const *caches, int num_caches, const int64_t *src,
+                               const int64_t *dst, int64_t num_pairs, int64_t block_bytes,
+                               int64_t num_blocks, void *staging, void *stream) {
+  clear_error();
+  int st = check_copy_args("copy_blocks", caches, num_caches, src, dst, num_pairs, block_bytes);
+  if (st != VFL_OK) return st == 1 ? VFL_OK : st;
+  if (staging && ((uintptr_t)staging % 16) != 0) {
+    set_error("copy_blocks: staging buffer must be 16-byte aligned");
+    return VFL_E_INVALID;
+  }
+  return launch_copy(caches, num_caches, src, dst, num_pairs, block_bytes, num_blocks,
+                     (uint8_t *)staging, (hipStream_t)stream, "copy_blocks");
+}
+
