@@ -552,7 +552,7 @@ def engine_decode(torch, seed: int):
         rows_done = steps = 0
         t0 = time.perf_counter()
         while not llm.is_finished():
-            rows_done += len(llm.scheduler.running)
+            rows_done += llm.scheduler.num_running
             llm.step()
             steps += 1
         torch.cuda.synchronize()

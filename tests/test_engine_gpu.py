@@ -35,7 +35,7 @@ def assert_clean(llm):
     bm = llm.scheduler.block_manager
     assert llm.is_finished()
     assert bm.num_free_blocks == bm.num_blocks and not any(bm.ref_counts)
-    assert not llm.scheduler._finished_beams
+    assert llm.scheduler.num_pending_beams == 0 and not llm.scheduler.waiting
     runner = llm.runner
     assert not runner._cross_pages
     assert sorted(runner._cross_free) == list(range(llm.config.num_cross_blocks))
@@ -171,43 +171,52 @@ def test_16bit_hip_graph_steps_equal_eager_steps(dtype):
 
 def test_prepare_and_encode_follow_the_reference_formulas(small_engine):
     """Slots, context lengths, tables and positions of one step
-    (model_runner.py:294-305) and the paged encoder K/V (:236-259) read back from HBM."""
+    (model_runner.py:294-305) read back from HBM against the formulas applied to the
+    host core's rows, and the paged encoder K/V (:236-259).  Three requests join at
+    different steps, so their rows hold different numbers of cached tokens."""
     from vflorence_amd import SamplingParams, hip_attn
     from vflorence_amd.engine.sequence import Sequence
-    from vflorence_amd.utils.context import get_context
+    from vflorence_amd.utils.context import get_context, set_context
 
     llm = small_engine
-    runner = llm.runner
-    params = SamplingParams(max_tokens=8).with_defaults(llm._sampling_params)
+    runner, sched = llm.runner, llm.scheduler
+    params = SamplingParams(max_tokens=30).with_defaults(llm._sampling_params)
     fx = fixtures()["small"]
-    seqs = [Sequence(i, [2], fx["prompts"][i], params) for i in range(3)]
-    bm = llm.scheduler.block_manager
+    joins = {0: 0, 5: 1, 17: 2}
+    seqs = []
     with torch.inference_mode():
-        runner._encode(seqs)
-        # feed a few tokens by hand: seq i has i + 1 tokens cached before this step
-        for i, seq in enumerate(seqs):
-            seq.token_ids = [2] + [10 + t for t in range(i + 17)]
-            seq.num_cached_tokens = len(seq.token_ids) - 1
-            while len(seq.block_table) * 16 <= seq.num_cached_tokens:
-                seq.block_table.append(bm._allocate_block())
-        ids, pos = runner._prepare(seqs)
+        for step in range(21):
+            if step in joins:
+                i = joins[step]
+                seqs.append(Sequence(i, [2], fx["prompts"][i], params))
+                sched.add(seqs[-1])
+            batch = sched.schedule()
+            if batch.fresh:
+                runner._encode(batch.fresh)
+            # tokens decided on the host: no decoder step needed to advance the rows
+            sched.postprocess(batch, np.full(batch.num_rows, 10 + step, np.int64))
+        batch = sched.schedule()
+        rows = sched.running
+        assert [r.num_cached_tokens for r in rows] == [21, 16, 4]
+        ids, pos = runner._prepare(batch)
         ctx = get_context()
-        # three sequences padded to the 4-row bucket: the padding row feeds token 0 at
+        # three rows padded to the 4-row bucket: the padding row feeds token 0 at
         # position 0, has an empty context and writes no slot
         assert pos.shape[0] == ids.shape[0] == ctx.context_lens.shape[0] == 4
-        want_pos = [s.num_cached_tokens for s in seqs]
+        want_pos = [r.num_cached_tokens for r in rows]
         assert pos.tolist() == want_pos + [0]
-        assert ids.tolist() == [s.token_ids[p] for s, p in zip(seqs, want_pos)] + [0]
+        assert ids.tolist() == [r.token_ids[p] for r, p in zip(rows, want_pos)] + [0]
         assert ctx.context_lens.tolist() == [p + 1 for p in want_pos] + [0]
-        assert ctx.slot_mapping.tolist() == [s.block_table[p // 16] * 16 + p % 16
-                                             for s, p in zip(seqs, want_pos)] + [-1]
+        assert ctx.slot_mapping.tolist() == [r.block_table[p // 16] * 16 + p % 16
+                                             for r, p in zip(rows, want_pos)] + [-1]
         # 0-padded rows at the runner's fixed table width (the kernels read only
         # ceil(len / 16) entries of a row)
         width = ctx.block_tables.shape[1]
-        assert width >= max(len(s.block_table) for s in seqs)
-        assert ctx.block_tables.tolist() == [s.block_table + [0] * (width - len(s.block_table))
-                                             for s in seqs] + [[0] * width]
+        assert width >= max(len(r.block_table) for r in rows)
+        assert ctx.block_tables.tolist() == [r.block_table + [0] * (width - len(r.block_table))
+                                             for r in rows] + [[0] * width]
         assert ctx.query_start_loc.tolist() == list(range(5))
+        set_context()
         # encoder pages: request i's tokens at pages[t // 16] * 16 + t % 16 hold kv_proj
         layer = runner.decoder_layers[1]
         attn = layer.encoder_attn
@@ -222,21 +231,7 @@ def test_prepare_and_encode_follow_the_reference_formulas(small_engine):
             vc = hip_attn.v_cache_logical(attn.v_cache)[blk, :, off, :]
             torch.testing.assert_close(kc, k.view(enc_len, attn.num_heads, -1), rtol=0, atol=0)
             torch.testing.assert_close(vc, v.view(enc_len, attn.num_heads, -1), rtol=0, atol=0)
-    from vflorence_amd.utils.context import set_context
-
-    set_context()
-    # the one-token invariant (model_runner.py:277-282), and a row with no block at its
-    # write position, are refused before anything is staged
-    two_new = Sequence(7, [2, 5, 6], fx["prompts"][0], params)
-    two_new.block_table = [0]
-    with pytest.raises(ValueError, match="1 token per sequence, got 3"):
-        runner._prepare([two_new])
-    no_block = Sequence(8, [2], fx["prompts"][0], params)
-    with pytest.raises(ValueError, match="no block for its write position"):
-        runner._prepare([no_block])
-    for seq in seqs:
-        bm.deallocate(seq)
-        runner.clear_request(seq.request_id)
+    llm.abort()
     assert_clean(llm)
 
 
@@ -311,7 +306,7 @@ def test_continuous_batching_keeps_each_requests_tokens(graphs):
         if not llm.is_finished():
             for rid, out in llm.step():
                 done[rid] = out.completion_token_ids
-            sizes.add(len(llm.scheduler.running))
+            sizes.add(llm.scheduler.num_running)
         step += 1
     assert len(done) == 30 and len(sizes) > 3
     for rid, tokens in done.items():
@@ -366,7 +361,7 @@ def test_continuous_batching_stress_florence2_large_shape():
     50/50 mix of 587 and U[64, 1024] and output lengths geometric (mean 96, cap 256).
     Active requests share one SamplingParams (the reference requires it,
     vflorence/engine/llm_engine.py:147), so each request is retired at its drawn length
-    the way a finished one is (scheduler removal + encoder pages released).  The batch
+    by cancelling it (``abort_request``: blocks and encoder pages released).  The batch
     changes size from step to step, the graphs stay within the row buckets, every row
     gets one token per step, and every block and page returns."""
     from transformers import BartConfig
@@ -393,16 +388,16 @@ def test_continuous_batching_stress_florence2_large_shape():
             ids = rng.integers(3, cfg.vocab_size, size=enc[i]).tolist()
             target[llm.add_request(Request(ids), sp)] = out_len[i]
         if not llm.is_finished():
-            before = {s.request_id: s.num_generated for s in llm.scheduler.running}
+            before = {r.request_id: len(r.token_ids) - 1 for r in llm.scheduler.running}
             sizes.add(len(before))
             for rid, out in llm.step():  # reached the 256-token cap: finished by the engine
                 done[rid] = len(out.completion_token_ids)
-            for seq in list(llm.scheduler.running):
-                assert seq.num_generated == before.get(seq.request_id, 0) + 1
-                if seq.num_generated >= target[seq.request_id]:
-                    llm.scheduler.remove(seq)
-                    llm.runner.clear_request(seq.request_id)
-                    done[seq.request_id] = seq.num_generated
+            for row in llm.scheduler.running:
+                generated = len(row.token_ids) - 1
+                assert generated == before.get(row.request_id, 0) + 1
+                if generated >= target[row.request_id]:
+                    assert llm.abort_request(row.request_id)
+                    done[row.request_id] = generated
         step += 1
     assert done == target
     assert max(sizes) <= 512 and len(sizes) > 50

@@ -1,7 +1,9 @@
-"""Host-side engine logic on the CPU: logits rules against transformers' processors,
-beam-candidate selection, the scheduler's beam gate (the reference's known answers),
-block-manager invariants, the synthetic checkpoint, and the BART encoder against
-transformers' (dense part only: the decoder's paged attention needs the GPU)."""
+"""Host-side engine logic on the CPU: logits rules against transformers' processors;
+the native host core (block pool, admission, step metadata, greedy and beam updates)
+against the reference's known answers and, step by step on random workloads, against
+the oracle's restatement of the reference's bookkeeping (oracle/engine_host.py); the
+synthetic checkpoint; and the BART encoder against transformers' (dense part only:
+the decoder's paged attention needs the GPU)."""
 
 import json
 import os
@@ -11,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle.engine_host import HostOracle
 from vflorence_amd.engine.block_manager import BlockManager
 from vflorence_amd.engine.scheduler import Scheduler
 from vflorence_amd.engine.sequence import Sequence
@@ -100,70 +103,208 @@ def test_out_of_vocab_rule_tokens_are_dropped():
     assert torch.isfinite(scores[:, 4]).all()
 
 
-def beam_search(seqs, scores, params):
-    from vflorence_amd.engine.model_runner import ModelRunner
+# --------------------------------------------------------------------------------------
+# the native host core
+# --------------------------------------------------------------------------------------
+def host_views(rows: int, width: int) -> dict:
+    """Numpy buffers of one packed step (the pinned staging layout's fields)."""
+    i64 = {k: np.zeros(rows, np.int64) for k in ("input_ids", "positions", "slots", "lengths",
+                                                 "copy_src", "copy_dst", "row_requests")}
+    i32 = dict(context_lens=np.zeros(rows, np.int32), order=np.zeros(rows, np.int32),
+               group_start=np.zeros(rows + 1, np.int32), tables=np.zeros((rows, width), np.int32))
+    return {**i64, **i32}
 
-    return ModelRunner._beam_search(None, seqs, scores, params)
+
+def config(max_num_seqs, num_blocks, block_size=16):
+    return SimpleNamespace(max_num_seqs=max_num_seqs, num_blocks=num_blocks,
+                           block_size=block_size)
 
 
-def test_beam_candidates_match_flattened_topk():
-    """Per-row top-k, then a per-request merge == top-k over the request's flattened
-    (rows x vocab) scores (the reference's test_engine.py:250-277 check)."""
-    torch.manual_seed(0)
-    for eos, vocab in (([2], 32), ([2, 3, 4], 32), ([2], 5)):
-        params = SamplingParams(num_beams=4, eos_token_id=eos).with_defaults(defaults())
-        keep = max(2, 1 + len(eos)) * 4
-        seqs = [Sequence(r, [1], [3], params) for r in (0, 0, 0, 0, 1, 2, 2)]
-        for seq in seqs:
-            seq.cum_logprob = -torch.rand(()).item()
-        scores = torch.log_softmax(torch.randn(len(seqs), vocab), dim=-1)
-        scores[-1, :2] = float("-inf")
-        got = beam_search(seqs, scores.clone(), params)
-        total = scores + torch.tensor([s.cum_logprob for s in seqs]).unsqueeze(-1)
-        for rid in (0, 1, 2):
-            rows = [i for i, s in enumerate(seqs) if s.request_id == rid]
-            values, idx = torch.topk(total[rows].flatten(), min(keep, len(rows) * vocab))
-            want = [(rows[i // vocab], i % vocab, v) for i, v in zip(idx.tolist(), values.tolist())]
-            row_of = {id(s): i for i, s in enumerate(seqs)}
-            assert [(row_of[id(p)], t, c) for p, t, c in got[rid]] == want
+def run_greedy(sched, tokens_for_step):
+    """Drive ``sched`` to completion with host-made greedy tokens; returns outputs."""
+    outs = {}
+    step = 0
+    while not sched.is_finished():
+        batch = sched.schedule()
+        toks = np.array([tokens_for_step(step, r) for r in range(batch.num_rows)], np.int64)
+        outs.update(sched.postprocess(batch, toks))
+        step += 1
+    return outs
+
+
+def test_exact_block_budget_fits():
+    """A request whose tokens fill its one block exactly runs with a one-block pool
+    (the reference's tests/test_engine.py:182-189)."""
+    params = SamplingParams(max_tokens=16, min_length=17, eos_token_id=[2]).with_defaults(
+        defaults())
+    sched = Scheduler(config(max_num_seqs=1, num_blocks=1))
+    sched.add(Sequence(0, [1], [3, 4, 5], params))
+    outs = run_greedy(sched, lambda step, r: 5)
+    assert len(outs[0].completion_token_ids) == 16
+    bm = sched.block_manager
+    assert bm.num_free_blocks == 1 and not any(bm.ref_counts)
+
+
+def test_shared_beams_fit_two_blocks():
+    """Two beams share their prompt block; with a two-block pool the copy-on-write of
+    the shared partial block still fits (tests/test_engine.py:361-366)."""
+    params = SamplingParams(max_tokens=3, num_beams=2, min_length=4, eos_token_id=[2]
+                            ).with_defaults(defaults())
+    sched = Scheduler(config(max_num_seqs=2, num_blocks=2))
+    sched.add(Sequence(0, [1], [3, 4, 5], params))
+    outs = {}
+    while not sched.is_finished():
+        batch = sched.schedule()
+        rows = batch.num_rows
+        scores = np.tile(np.array([[-0.1, -0.2, -0.3, -0.4]], np.float32), (rows, 1))
+        ids = np.tile(np.array([[10, 11, 12, 13]], np.int64), (rows, 1))
+        outs.update(sched.postprocess(batch, (scores, ids)))
+    assert len(outs[0].completion_token_ids) == 3
+    assert sched.block_manager.num_free_blocks == 2
+
+
+def test_copy_budget_counts_a_shared_block_once_its_owner_left():
+    """Two children of one parent share its block: both must copy while the parent
+    holds it (2 new blocks); once the parent lets go, the last writer keeps it in place
+    (1 new block) -- the reference's tests/test_engine.py:368-380."""
+    params = SamplingParams().with_defaults(defaults())
+    bm = BlockManager(8, 16)
+    parent = Sequence(0, [1], [3], params)
+    assert bm.ensure_capacity(parent) is None
+    parent.num_cached_tokens = 1
+    children = [parent.fork(4, 0.0), parent.fork(5, 0.0)]
+    for child in children:
+        bm.fork(parent, child)
+    assert bm.required_new_blocks(children) == 2
+    bm.deallocate(parent)
+    assert bm.required_new_blocks(children) == 1
+
+
+def test_copy_on_write_pair_and_counts():
+    """A fork writing into its parent's shared block moves to a fresh block; the pair
+    names both and each block keeps one holder (tests/test_engine.py:382-393)."""
+    params = SamplingParams().with_defaults(defaults())
+    bm = BlockManager(8, 16)
+    parent = Sequence(0, [1], [3], params)
+    assert bm.ensure_capacity(parent) is None
+    parent.num_cached_tokens = 1
+    child = parent.fork(4, 0.0)
+    bm.fork(parent, child)
+    src = parent.block_table[0]
+    pair = bm.ensure_capacity(child)
+    assert pair == (src, child.block_table[0]) and child.block_table == [pair[1]]
+    assert (bm.ref_counts[src], bm.ref_counts[pair[1]]) == (1, 1)
+    # free list: FIFO, freed blocks at the back, a table freed last block first
+    bm.deallocate(parent)
+    assert bm.free_block_ids[-1] == src
+    with pytest.raises(RuntimeError, match="KV cache is full"):
+        full = BlockManager(1, 16)
+        a = Sequence(0, [1], [3], params)
+        full.ensure_capacity(a)
+        full.ensure_capacity(Sequence(1, [1], [3], params))
 
 
 def test_beam_gate_reference_cases():
-    """The reference's known answers for the EOS/rank gate (tests/test_beam.py:22-32)."""
+    """The reference's known answers for the EOS/rank gate (tests/test_beam.py:22-57):
+    candidates taken in the listed rank order -- stopped ones (EOS) scored below the
+    live ones so no early stop intervenes -- keep a stopped candidate only within the
+    first num_beams ranks, and live ones fill num_beams running beams.  Pins the
+    oracle's walk; the host core is held to the oracle on merged candidates below."""
     cases = json.load(open(os.path.join(GOLDEN, "reference_kats.json")))["beam_gate"]["cases"]
     for stopped, num_beams, want_finished, want_live in cases:
         eos = [100 + r for r in range(len(stopped))]
+        orc = HostOracle(8, 16, 8)
+        orc.add(0, [1], num_beams, 10, eos, 1.0, False)
+        orc.schedule()
+        parent = orc.running[0]
+        cands = {0: [(parent, (100 + r) if s else r, (-10.0 - r) if s else -float(r))
+                     for r, s in enumerate(stopped)]}
+        outputs = orc.walk(cands)
+        if outputs:
+            best = outputs[0][1][-1] - 100
+            finished, live = list(range(best, num_beams)), []
+        else:
+            finished = [h.tokens[-1] - 100 for h in orc.finished_beams[0]]
+            live = [h.tokens[-1] for h in orc.running]
+        assert (finished, live) == (want_finished, want_live), stopped
+
+
+def test_beam_gate_on_the_host_core():
+    """The gate's cases where the listed ranks are also the score order (every stopped
+    candidate below the live ones, or none live): the host core keeps the same
+    finished and live ranks."""
+    for stopped, num_beams, want_finished, want_live in (
+            ([False, False, True, True], 2, [], [0, 1]),
+            ([True, True, True], 2, [0, 1], [])):
+        eos = [100 + r for r in range(len(stopped))]
         params = SamplingParams(num_beams=num_beams, max_tokens=10, eos_token_id=eos,
                                 early_stopping=False).with_defaults(defaults())
-        sched = Scheduler(SimpleNamespace(max_num_seqs=8, num_blocks=8, block_size=16))
-        parent = Sequence(0, [1], [3], params)
-        sched.add(parent)
-        seqs, _ = sched.schedule()
-        cands = [(parent, (100 + r) if s else r, (-10.0 - r) if s else -float(r))
-                 for r, s in enumerate(stopped)]
-        outputs = sched.postprocess(seqs, {0: cands})
+        ids = np.array([[(100 + r) if s else r for r, s in enumerate(stopped)]], np.int64)
+        scores = -np.arange(len(stopped), dtype=np.float32)[None, :]
+        sched = Scheduler(config(max_num_seqs=8, num_blocks=8))
+        sched.add(Sequence(0, [1], [3], params))
+        outputs = sched.postprocess(sched.schedule(), (scores, ids))
         if outputs:
             best = outputs[0][1].completion_token_ids[-1] - 100
             finished, live = list(range(best, num_beams)), []
         else:
-            finished = [s.completion_token_ids[-1] - 100 for s in sched._finished_beams[0]]
-            live = [s.completion_token_ids[-1] for s in sched.running]
+            finished = [] if not sched.num_pending_beams else None
+            live = [r.token_ids[-1] for r in sched.running]
         assert (finished, live) == (want_finished, want_live), stopped
+
+
+def test_oracle_merge_equals_flattened_topk():
+    """The oracle's per-request merge (each row's top-k plus its cumulative log-prob,
+    best first) equals top-k over the request's flattened rows x vocab scores (the
+    reference's tests/test_engine.py:250-277 check)."""
+    torch.manual_seed(0)
+    for eos, vocab in (([2], 32), ([2, 3, 4], 32), ([2], 5)):
+        nb = 4
+        keep = max(2, 1 + len(eos)) * nb
+        rids = [0, 0, 0, 0, 1, 2, 2]
+        cums = [-float(torch.rand(())) for _ in rids]
+        scores = torch.log_softmax(torch.randn(len(rids), vocab), dim=-1)
+        top, ids = torch.topk(scores, min(keep, vocab), dim=-1)
+        orc = HostOracle(64, 16, 64)
+        for rid in (0, 1, 2):
+            orc.add(rid, [1], nb, 50, eos, 1.0, False)
+        orc.schedule()
+        # shape the running rows as the rids above, with the given cumulative scores
+        proto = {h.rid: h for h in orc.running}
+        orc.running = [proto[r].child(9, c) for r, c in zip(rids, cums)]
+        for h in orc.running:
+            h.tokens = h.tokens[:-1]
+        merged = {}
+        for r, h in enumerate(orc.running):
+            vals = top[r].numpy().astype(np.float32) + np.float32(h.cum)
+            merged.setdefault(h.rid, []).extend(
+                (r, int(t), float(v)) for t, v in zip(ids[r].tolist(), vals))
+        total = (scores + torch.tensor(cums).unsqueeze(-1)).float()
+        for rid in (0, 1, 2):
+            rows = [i for i, r in enumerate(rids) if r == rid]
+            vals, idx = torch.topk(total[rows].flatten(), min(keep, len(rows) * vocab))
+            want = [(rows[i // vocab], i % vocab) for i in idx.tolist()]
+            got = sorted(merged[rid], key=lambda c: c[2], reverse=True)[:keep]
+            assert [(r, t) for r, t, _ in got] == want
 
 
 def test_scheduler_admission_counts_beams_and_keeps_beams_adjacent():
     params = SamplingParams(num_beams=3, max_tokens=8, eos_token_id=[]).with_defaults(defaults())
-    sched = Scheduler(SimpleNamespace(max_num_seqs=7, num_blocks=64, block_size=16))
+    sched = Scheduler(config(max_num_seqs=7, num_blocks=64))
     for r in range(3):
         sched.add(Sequence(r, [1], [3], params))
-    seqs, copies = sched.schedule()
-    assert [s.request_id for s in seqs] == [0, 1] and not copies  # 3 + 3 <= 7 < 9
-    cands = {r: [(seqs[r], 10 + k, -0.1 * k) for k in range(6)] for r in (0, 1)}
-    assert sched.postprocess(seqs, cands) == []
-    seqs, copies = sched.schedule()
-    assert [s.request_id for s in seqs] == [0, 0, 0, 1, 1, 1]
+    batch = sched.schedule()
+    assert [s.request_id for s in batch.fresh] == [0, 1] and batch.num_pairs == 0  # 3+3 <= 7 < 9
+    scores = np.tile(-0.1 * np.arange(6, dtype=np.float32), (2, 1))
+    ids = np.tile(10 + np.arange(6, dtype=np.int64), (2, 1))
+    assert sched.postprocess(batch, (scores, ids)) == []
+    batch = sched.schedule()
+    assert [r.request_id for r in sched.running] == [0, 0, 0, 1, 1, 1]
     # three children share their parent's one block; all but the last writer copy it
-    assert len(copies) == 4 and len({d for _, d in copies}) == 4
+    views = host_views(8, 4)
+    sched.core.pack(8, 4, 8, views)
+    pairs = list(zip(views["copy_src"][:batch.num_pairs], views["copy_dst"][:batch.num_pairs]))
+    assert batch.num_pairs == 4 and len({d for _, d in pairs}) == 4
 
 
 def test_block_manager_invariants_under_random_forks():
@@ -196,80 +337,116 @@ def test_block_manager_invariants_under_random_forks():
     assert bm.num_free_blocks == 64 and not any(bm.ref_counts)
 
 
-class _ForkAllScheduler(Scheduler):
-    """The reference's beam bookkeeping verbatim in effect: fork every live child from
-    its parent, then deallocate every parent (vflorence/engine/scheduler.py:120-126)."""
+def random_candidates(rng, rows, k, vocab, eos_rate):
+    """Each row's best-first (scores, ids): distinct ids, scores on a 1/8 grid so exact
+    ties occur inside and across rows; EOS (token 2) now and then."""
+    ids = np.stack([rng.choice(np.arange(3, vocab), size=k, replace=False) for _ in range(rows)])
+    eos = rng.random((rows, k)) < eos_rate
+    ids[eos] = 2
+    for r in range(rows):  # keep ids distinct after placing EOS
+        seen = set()
+        for c in range(k):
+            while ids[r, c] in seen:
+                ids[r, c] = rng.integers(3, vocab)
+            seen.add(ids[r, c])
+    scores = -np.sort(np.round(rng.exponential(1.5, (rows, k)) * 8) / 8, axis=1)
+    return scores.astype(np.float32), ids.astype(np.int64)
 
-    def _postprocess_beam(self, seqs, candidates_by_request):
-        outputs = []
-        for request_id, candidates in candidates_by_request.items():
-            sp = candidates[0][0].sampling_params
-            finished = self._finished_beams[request_id]
-            live = []
-            for rank, (parent, token, cum) in enumerate(candidates):
-                if rank >= sp.num_beams and len(live) >= sp.num_beams:
-                    break
-                child = parent.fork(token, cum)
-                if token in sp.eos_ids() or child.num_generated >= sp.max_tokens:
-                    if rank < sp.num_beams:
-                        finished.append(child)
-                elif len(live) < sp.num_beams:
-                    live.append((parent, child))
-            finished.sort(key=lambda q: q.score, reverse=True)
-            del finished[sp.num_beams:]
-            best = max((c.score for _, c in live), default=float("-inf"))
-            if not live or (len(finished) >= sp.num_beams and (
-                    sp.early_stopping or finished[-1].score >= best)):
-                self._finished_beams.pop(request_id, None)
-                outputs.append((request_id, finished[0].to_output()))
+
+@pytest.mark.parametrize("beams,early,lp,seed", [
+    (1, False, 1.0, 0), (1, False, 1.0, 1), (4, False, 1.0, 2), (4, True, 1.0, 3),
+    (3, False, 2.0, 4), (4, False, -0.5, 5), (2, False, 1.0, 6), (8, False, 1.0, 7)])
+def test_host_core_equals_the_oracle_step_by_step(beams, early, lp, seed):
+    """Continuous batching with seeded arrivals, greedy or beam search with random
+    candidates: every step the core admits the same requests, packs the reference's
+    metadata formulas, makes the same copy-on-write pairs, leaves the same holder
+    counts and free list (order included), the same running rows (tokens, tables,
+    cumulative scores) and finishes the same requests with the same tokens as the
+    oracle's literal restatement."""
+    rng = np.random.default_rng(seed)
+    bs, max_seqs, num_blocks = 16, 24, 200
+    max_tokens = 40
+    params = SamplingParams(num_beams=beams, max_tokens=max_tokens, eos_token_id=[2],
+                            early_stopping=early, length_penalty=lp).with_defaults(defaults())
+    sched = Scheduler(config(max_num_seqs=max_seqs, num_blocks=num_blocks))
+    orc = HostOracle(num_blocks, bs, max_seqs)
+    arrivals = sorted(rng.integers(0, 30, size=14).tolist())
+    rid, step, seen_pairs, seen_groups = 0, 0, 0, 0
+    keep = max(2, 1 + 1) * beams
+    while arrivals or not sched.is_finished():
+        while arrivals and arrivals[0] <= step:
+            arrivals.pop(0)
+            prompt = [1] if rng.random() < 0.7 else [1, 4]
+            sched.add(Sequence(rid, prompt, [3], params))
+            orc.add(rid, prompt, beams, max_tokens, [2], lp, early)
+            rid += 1
+        batch = sched.schedule()
+        assert [s.request_id for s in batch.fresh] == orc.schedule()
+        n = batch.num_rows
+        assert n == len(orc.running)
+        if n:
+            padded = n + int(rng.integers(0, 3))
+            views = host_views(padded, 8)
+            grouped = sched.core.pack(padded, 8, 8, views)
+            want = orc.metadata()
+            for name in ("input_ids", "positions", "slots", "lengths", "context_lens",
+                         "row_requests"):
+                assert views[name][:n].tolist() == want[name], name
+            for r, t in enumerate(want["tables"]):
+                assert views["tables"][r].tolist() == t + [0] * (8 - len(t))
+            assert not views["tables"][n:].any() and (views["slots"][n:] == -1).all()
+            pairs = list(zip(views["copy_src"][:batch.num_pairs].tolist(),
+                             views["copy_dst"][:batch.num_pairs].tolist()))
+            assert pairs == orc.pairs
+            seen_pairs += len(pairs)
+            rids = want["row_requests"]
+            if grouped:
+                seen_groups += 1
+                starts = views["group_start"]
+                assert starts[0] == 0 and starts[-1] == padded
+                for g in range(len(starts) - 1):  # each group: rows of one request
+                    assert len({rids[r] for r in range(starts[g], min(starts[g + 1], n))}) <= 1
             else:
-                for parent, child in live:
-                    self.block_manager.fork(parent, child)
-                    self.running.append(child)
-        for seq in seqs:
-            self.running.remove(seq)
-            self.block_manager.deallocate(seq)
-        return outputs
+                order = views["order"][:padded].tolist()
+                ctx = views["context_lens"][:padded].tolist()
+                assert order == sorted(range(padded), key=lambda r: -ctx[r])
+        bm = sched.block_manager
+        assert bm.ref_counts == orc.pool.refs
+        assert bm.free_block_ids == list(orc.pool.free)
+        if n == 0:
+            step += 1
+            continue
+        if beams == 1:
+            toks = rng.integers(3, 60, n)
+            toks[rng.random(n) < 0.05] = 2
+            got, want = sched.postprocess(batch, toks), orc.greedy(toks)
+        else:
+            scores, ids = random_candidates(rng, n, keep, 60, 0.04)
+            got, want = sched.postprocess(batch, (scores, ids)), orc.beam(scores, ids)
+        assert [(r, o.completion_token_ids) for r, o in got] == want
+        rows = sched.running
+        assert [(r.request_id, r.token_ids, r.block_table, r.num_cached_tokens)
+                for r in rows] == [(h.rid, h.tokens, h.table, h.cached) for h in orc.running]
+        assert [r.cum_logprob for r in rows] == [h.cum for h in orc.running]
+        step += 1
+    assert sched.block_manager.num_free_blocks == num_blocks
+    assert rid == 14 and step > 10
+    if beams > 1:
+        assert seen_pairs > 0 and seen_groups > 0
 
 
-@pytest.mark.parametrize("early_stopping,length_penalty", [(False, 1.0), (True, 1.0),
-                                                             (False, 2.0), (False, -0.5)])
-def test_beam_table_handover_keeps_the_reference_block_state(early_stopping, length_penalty):
-    """Handing a parent's table to its first live child instead of fork + deallocate,
-    and forking only the candidates that are kept, leave every step's block tables,
-    copy-on-write pairs, reference counts, free list (order included) and outputs
-    identical to forking every child."""
-    import random
-
-    def run(cls, seed):
-        rng = random.Random(seed)
-        params = SamplingParams(num_beams=4, max_tokens=60, eos_token_id=[2],
-                                early_stopping=early_stopping,
-                                length_penalty=length_penalty).with_defaults(defaults())
-        sched = cls(SimpleNamespace(max_num_seqs=24, num_blocks=160, block_size=16))
-        for r in range(6):
-            sched.add(Sequence(r, [1], [3], params))
-        trace = []
-        while not sched.is_finished():
-            seqs, copies = sched.schedule()
-            bm = sched.block_manager
-            trace.append(([list(s.block_table) for s in seqs], list(copies),
-                          list(bm.ref_counts), list(bm.free_block_ids)))
-            cands = {}
-            for s in seqs:
-                row = []
-                for _ in range(3):  # a few children per parent, EOS now and then
-                    tok = 2 if rng.random() < 0.03 else rng.randrange(3, 50)
-                    row.append((s, tok, s.cum_logprob - rng.random()))
-                cands.setdefault(s.request_id, []).extend(row)
-            for rid in cands:
-                cands[rid].sort(key=lambda c: -c[2])
-            outs = sched.postprocess(seqs, cands)
-            trace.append(sorted((rid, o.completion_token_ids) for rid, o in outs))
-        return trace
-
-    for seed in range(4):
-        assert run(Scheduler, seed) == run(_ForkAllScheduler, seed)
+def test_pool_full_raises_and_abort_frees_everything():
+    """A step the pool cannot cover raises "KV cache is full" before any block moves;
+    reset() returns every block (the engine's abort)."""
+    params = SamplingParams(max_tokens=40, eos_token_id=[]).with_defaults(defaults())
+    sched = Scheduler(config(max_num_seqs=4, num_blocks=3))
+    for r in range(4):
+        sched.add(Sequence(r, [1], [3], params))
+    with pytest.raises(RuntimeError, match="KV cache is full"):
+        sched.schedule()
+    assert sched.block_manager.num_free_blocks == 3
+    sched.reset()
+    assert sched.is_finished() and sched.block_manager.free_block_ids == [0, 1, 2]
 
 
 def test_synthetic_checkpoint_is_deterministic_and_loads_into_transformers():
@@ -312,38 +489,3 @@ def test_encoder_matches_transformers():
         want = hf.model.encoder(input_ids=ids).last_hidden_state
         got = mine.encode(ids)
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
-
-
-def test_vectorised_beam_merge_equals_the_general_merge():
-    """Equal-size adjacent beam groups take the vectorised merge; it must list the same
-    candidates in the same order as the row-by-row stable sort, ties included."""
-    from vflorence_amd.engine import model_runner as mr
-
-    params = SamplingParams(num_beams=3, eos_token_id=[2]).with_defaults(defaults())
-    g = torch.Generator().manual_seed(3)
-    for rows_per_req, vocab in ((3, 40), (1, 40), (3, 4)):
-        seqs = [Sequence(r, [1], [3], params) for r in range(5) for _ in range(rows_per_req)]
-        for s in seqs:
-            s.cum_logprob = -float(torch.rand((), generator=g))
-        scores = torch.log_softmax(torch.randn(len(seqs), vocab, generator=g), dim=-1)
-        scores[:, 5:9] = -1.0  # exact ties inside and across rows
-        scores[1, :] = float("-inf")
-        keep = max(2, 1 + len(params.eos_ids())) * params.num_beams
-        top, ids = torch.topk(scores, min(keep, vocab), dim=-1)
-        top = top + torch.tensor([s.cum_logprob for s in seqs]).unsqueeze(-1)
-        fast = mr._merge_equal_beam_groups(seqs, top.numpy(), ids.numpy(), keep)
-        assert fast is not None
-        general = {}
-        for s, row_s, row_i in zip(seqs, top.tolist(), ids.tolist()):
-            general.setdefault(s.request_id, []).extend(zip([s] * len(row_i), row_i, row_s))
-        for c in general.values():
-            c.sort(key=lambda x: x[2], reverse=True)
-            del c[keep:]
-        assert fast == general
-    # unequal or interleaved groups are left to the general merge
-    seqs = [Sequence(r, [1], [3], params) for r in (0, 0, 1)]
-    assert mr._merge_equal_beam_groups(seqs, np.zeros((3, 2), np.float32),
-                                       np.zeros((3, 2), np.int64), 4) is None
-    seqs = [Sequence(r, [1], [3], params) for r in (0, 1, 0, 1)]
-    assert mr._merge_equal_beam_groups(seqs, np.zeros((4, 2), np.float32),
-                                       np.zeros((4, 2), np.int64), 4) is None

@@ -1,5 +1,7 @@
-"""The C-ABI library loads, exports what include/vflorence_amd.h declares, and its
-host-side planning and argument checks behave (no GPU work is launched here)."""
+"""The C-ABI libraries load and export what their headers declare
+(include/vflorence_amd.h: the GPU library; include/vfl_engine.h: the engine's host
+core), and the GPU library's host-side planning and argument checks behave (no GPU
+work is launched here)."""
 
 import ctypes
 import os
@@ -11,10 +13,23 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "vflorence_amd.h")
 
 
-def declared_functions():
-    text = open(HEADER).read()
+HOST_HEADER = os.path.join(ROOT, "include", "vfl_engine.h")
+
+
+def declared_functions(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(vfl_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_host_core_exports_every_declared_symbol():
+    from vflorence_amd.engine import core
+
+    declared = declared_functions(HOST_HEADER)
+    assert declared and sorted(core.EXPORTED_SYMBOLS) == declared
+    raw = ctypes.CDLL(core.LIB_PATH)
+    for name in declared:
+        assert hasattr(raw, name), name
 
 
 def test_library_exports_every_declared_symbol():

@@ -1,8 +1,9 @@
-"""In-tree build of libvflorence_amd.so for gfx950 (hipcc, no cmake).
+"""In-tree builds (no cmake): libvflorence_amd.so for gfx950 (hipcc) and the engine's
+native host core libvfl_host.so (g++, CPU only).
 
     python -m vflorence_amd._build          # or __graft_entry__.build()
 
-The library is written next to this file so it travels with the source tree.
+The libraries are written next to this file so they travel with the source tree.
 """
 
 from __future__ import annotations
@@ -39,6 +40,27 @@ def hipcc() -> str:
     return path
 
 
+HOST_SOURCES = ("host/engine_core.cpp",)
+HOST_OUTPUT = os.path.join(HERE, "libvfl_host.so")
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Werror"]
+
+
+def build_host_library(verbose: bool = False) -> str:
+    """Compile the engine's host core into HOST_OUTPUT; always recompiles."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if not cxx:
+        raise RuntimeError("g++ not found; the engine's host core cannot be built")
+    tmp = HOST_OUTPUT + ".tmp"
+    cmd = [cxx, *HOST_FLAGS, *[os.path.join(CSRC, s) for s in HOST_SOURCES], "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError("g++ failed:\n" + proc.stdout + proc.stderr)
+    os.replace(tmp, HOST_OUTPUT)
+    return HOST_OUTPUT
+
+
 def build_library(verbose: bool = False) -> str:
     """Compile every HIP source into OUTPUT; always recompiles."""
     tmp = OUTPUT + ".tmp"
@@ -59,3 +81,4 @@ def build_library(verbose: bool = False) -> str:
 
 if __name__ == "__main__":
     print(build_library(verbose="-v" in sys.argv))
+    print(build_host_library(verbose="-v" in sys.argv))

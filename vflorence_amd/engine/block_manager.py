@@ -1,91 +1,86 @@
-"""Paged KV-block allocator with reference counts and copy-on-write.
+"""The reference's block-manager API (vflorence/engine/block_manager.py:4-73) over the
+native block pool (``vfl_pool``, include/vfl_engine.h).
 
-Same allocation semantics as vflorence/engine/block_manager.py:4-73, so a run
-reproduces the reference's block tables and copy pairs exactly: blocks leave a FIFO
-free list from the front and return to its back (deallocation walks a table from
-its last block), a forked sequence shares every block of its parent, and the
-sequence about to write into a shared block gets a private copy -- except the last
-holder, which writes in place.  The tables it produces feed the GPU kernels; the
-allocator itself stays on the host.
+The pool keeps every block's holder count and the free list; this class applies its
+decisions to ``Sequence.block_table`` lists.  Same observable behaviour as the
+reference: blocks leave the free list from the front and return to its back, a
+released table returns its blocks last block first, a fork shares its parent's
+blocks, and a sequence about to write into a block others still hold moves to a
+fresh copy (the pair is returned for the caller to copy) unless it is the last
+holder.  The engine uses the pool directly from its host core; this class serves
+code that drives sequences itself (the synthetic beam schedule of the benchmark,
+tests) and, over the engine's own pool (``BlockManager.view``), inspection.
 """
 
 from __future__ import annotations
 
-from collections import deque
+import numpy as np
+
+from .core import BlockPool
+
+_APPEND, _COPY = 1, 2
 
 
 class BlockManager:
-    def __init__(self, num_blocks: int, block_size: int):
-        self.num_blocks = num_blocks
+    def __init__(self, num_blocks: int, block_size: int, *, pool: BlockPool | None = None):
+        self.pool = pool if pool is not None else BlockPool(num_blocks, block_size)
         self.block_size = block_size
-        self.reset()
 
-    def reset(self) -> None:
-        """Return every block to the free list (after an aborted batch)."""
-        self.ref_counts = [0] * self.num_blocks
-        self.free_block_ids = deque(range(self.num_blocks))
+    @classmethod
+    def view(cls, pool: BlockPool) -> "BlockManager":
+        """Read access to a pool another owner drives (its counts and free list)."""
+        return cls(0, pool.block_size, pool=pool)
+
+    @property
+    def num_blocks(self) -> int:
+        return self.pool.num_blocks
 
     @property
     def num_free_blocks(self) -> int:
-        return len(self.free_block_ids)
+        return self.pool.num_free
 
-    def _allocate_block(self) -> int:
-        if not self.free_block_ids:
-            raise RuntimeError("KV cache is full; increase num_blocks")
-        block = self.free_block_ids.popleft()
-        self.ref_counts[block] = 1
-        return block
+    @property
+    def ref_counts(self) -> list[int]:
+        return self.pool.refcounts().tolist()
 
-    def _write_block_index(self, seq) -> int:
-        return seq.num_cached_tokens // self.block_size
+    @property
+    def free_block_ids(self) -> list[int]:
+        """The free list, next block out first."""
+        return self.pool.free_list().tolist()
+
+    def reset(self) -> None:
+        """Every block free again (after an aborted batch)."""
+        self.pool.reset()
 
     def required_new_blocks(self, seqs) -> int:
-        """Blocks this step needs: one per sequence entering a new block, plus one per
-        sequence writing into a block still shared with a sequence that writes later
-        (the last writer of a shared block keeps it)."""
-        needed = 0
-        holders_left: dict[int, int] = {}
-        for seq in seqs:
-            idx = self._write_block_index(seq)
-            if idx >= len(seq.block_table):
-                needed += 1
-                continue
-            block = seq.block_table[idx]
-            refs = holders_left.get(block, self.ref_counts[block])
-            if refs > 1:
-                needed += 1
-                holders_left[block] = refs - 1
-        return needed
+        """Blocks that giving every sequence a writable slot would take: one per sequence
+        starting a new block, and one per writer of a shared block except its last
+        holder."""
+        bs = self.block_size
+        writes = np.full(len(seqs), -1, dtype=np.int32)
+        for i, seq in enumerate(seqs):
+            idx = seq.num_cached_tokens // bs
+            if idx < len(seq.block_table):
+                writes[i] = seq.block_table[idx]
+        return self.pool.blocks_needed(writes)
 
     def ensure_capacity(self, seq) -> tuple[int, int] | None:
-        """Give ``seq`` a writable slot for its next token.
-
-        Appends a fresh block when the token starts one; when the block it writes into
-        is shared, moves ``seq`` to a private copy and returns ``(src, dst)`` for the
-        caller to copy before the write.  Otherwise returns None.
-        """
-        idx = self._write_block_index(seq)
-        if idx >= len(seq.block_table):
-            seq.block_table.append(self._allocate_block())
-            return None
-        block = seq.block_table[idx]
-        if self.ref_counts[block] == 1:
-            return None
-        private = self._allocate_block()
-        self.ref_counts[block] -= 1
-        seq.block_table[idx] = private
-        return block, private
+        """Make the position ``seq.num_cached_tokens`` writable; returns the (src, dst)
+        pair to copy when ``seq`` moved off a shared block, else None."""
+        action, block, src = self.pool.prepare_write(seq.block_table, seq.num_cached_tokens)
+        if action == _APPEND:
+            seq.block_table.append(block)
+        elif action == _COPY:
+            seq.block_table[seq.num_cached_tokens // self.block_size] = block
+            return src, block
+        return None
 
     def fork(self, parent, child) -> None:
-        """``child`` shares all of ``parent``'s blocks."""
+        """``child`` shares every block of ``parent``."""
         child.block_table = list(parent.block_table)
-        for block in child.block_table:
-            self.ref_counts[block] += 1
+        self.pool.share(child.block_table)
 
     def deallocate(self, seq) -> None:
-        """Drop ``seq``'s references (last block first); unreferenced blocks are freed."""
-        for block in reversed(seq.block_table):
-            self.ref_counts[block] -= 1
-            if self.ref_counts[block] == 0:
-                self.free_block_ids.append(block)
+        """``seq`` lets go of its blocks (last first); blocks nobody holds become free."""
+        self.pool.release(seq.block_table)
         seq.block_table.clear()

@@ -10,16 +10,17 @@ the GPU:
   (model_runner.py:62-77); a device table of the self-attention pools' addresses is
   made once for the batched copy-on-write launch;
 * a step's metadata (token ids, positions, slots, copy pairs, lengths, dispatch
-  order, block tables) is packed on the host into one pinned buffer at fixed offsets
-  and sent with one asynchronous host->device copy; the Context holds views of the
-  device copy (model_runner.py:273-341);
+  order, block tables) is written by the engine's native host core straight into one
+  pinned buffer at fixed offsets and sent with one asynchronous host->device copy; the
+  Context holds views of the device copy (model_runner.py:273-341);
 * the self-attention op receives a scheduler metadata that enables the fused KV write:
   the block manager's copy-on-write rule guarantees each row writes its last context
   position in a block no other row reads;
 * encoder K/V are projected on the device and scattered into pages with one
   ``reshape_and_cache`` per layer (model_runner.py:208-259);
 * logits rules and top-k run on the device; only the chosen ids (greedy) or each
-  row's top-k (beam search) come back to the host.
+  row's top-k (beam search) come back to the host, where the host core merges a
+  request's candidates.
 """
 
 from __future__ import annotations
@@ -46,16 +47,17 @@ class _StepBuffers:
     """Pinned host staging and its device twin for one step's metadata.
 
     int32 word layout for ``rows`` sequences and tables ``width`` blocks wide:
-    six int64 vectors of ``rows`` (token ids, positions, slots, copy sources, copy
-    destinations, lengths), then int32 context lengths, dispatch order, the row groups'
-    starts (``rows + 1``) and the ``[rows, width]`` block tables.
+    seven int64 vectors of ``rows`` (token ids, positions, slots, copy sources, copy
+    destinations, lengths, row request ids), then int32 context lengths, dispatch
+    order, the row groups' starts (``rows + 1``) and the ``[rows, width]`` block tables.
     """
 
-    I64 = ("input_ids", "positions", "slots", "copy_src", "copy_dst", "lengths")
+    I64 = ("input_ids", "positions", "slots", "copy_src", "copy_dst", "lengths",
+           "row_requests")
 
     def __init__(self, rows: int, width: int, device):
         self.rows, self.width = rows, width
-        words = 12 * rows + 3 * rows + 1 + rows * width
+        words = 2 * len(self.I64) * rows + 3 * rows + 1 + rows * width
         self.host = torch.zeros(words, dtype=torch.int32, pin_memory=True)
         self.dev = torch.zeros(words, dtype=torch.int32, device=device)
         self.copied = torch.cuda.Event()
@@ -68,10 +70,11 @@ class _StepBuffers:
         r, w = self.rows, self.width
         out = {name: buf[2 * r * i: 2 * r * (i + 1)].view(torch.int64)
                for i, name in enumerate(self.I64)}
-        out["context_lens"] = buf[12 * r: 13 * r]
-        out["order"] = buf[13 * r: 14 * r]
-        out["group_start"] = buf[14 * r: 15 * r + 1]
-        out["tables"] = buf[15 * r + 1: 15 * r + 1 + r * w].view(r, w)
+        base = 2 * len(self.I64) * r
+        out["context_lens"] = buf[base: base + r]
+        out["order"] = buf[base + r: base + 2 * r]
+        out["group_start"] = buf[base + 2 * r: base + 3 * r + 1]
+        out["tables"] = buf[base + 3 * r + 1: base + 3 * r + 1 + r * w].view(r, w)
         return out
 
     def upload(self) -> None:
@@ -108,48 +111,6 @@ def row_buckets(max_rows: int) -> list[int]:
         sizes.append(s)
         s += 8 if s < 64 else 16 if s < 128 else 32
     return [b for b in sizes if b < max_rows] + [max_rows]
-
-
-def _row_groups(seqs, max_group: int) -> list[int]:
-    """Starts of the runs of rows that belong to one request (its beams, adjacent in the
-    running list, vflorence/engine/scheduler.py:121-126), cut every ``max_group`` rows,
-    followed by the row count."""
-    starts = [0]
-    for i in range(1, len(seqs)):
-        if seqs[i].request_id != seqs[i - 1].request_id or i - starts[-1] >= max_group:
-            starts.append(i)
-    starts.append(len(seqs))
-    return starts
-
-
-def _merge_equal_beam_groups(seqs, scores, ids, keep: int):
-    """The per-request candidate merge, vectorised for the usual beam-search batch: each
-    request's rows adjacent and every request with the same number of rows.  Returns
-    None for any other batch (the general merge handles it).
-
-    Equals sorting each request's candidates -- listed row by row, each row best first
-    -- by score, stably, best first: a stable ascending sort of the negated scores.
-    """
-    n, k = scores.shape
-    rids = [s.request_id for s in seqs]
-    nb = 1
-    while nb < n and rids[nb] == rids[0]:
-        nb += 1
-    if n % nb:
-        return None
-    heads = rids[::nb]
-    groups = n // nb
-    if len(set(heads)) != groups or not (
-            np.array(rids).reshape(groups, nb) == np.array(heads)[:, None]).all():
-        return None
-    flat = scores.reshape(groups, nb * k)
-    order = np.argsort(-flat, axis=1, kind="stable")[:, :keep]
-    rows = order // k + (np.arange(groups) * nb)[:, None]
-    toks = ids[rows, order % k].tolist()
-    vals = np.take_along_axis(flat, order, axis=1).tolist()
-    rows = rows.tolist()
-    return {rid: [(seqs[r], t, v) for r, t, v in zip(rows[j], toks[j], vals[j])]
-            for j, rid in enumerate(heads)}
 
 
 class ModelRunner:
@@ -219,15 +180,13 @@ class ModelRunner:
                     2 * len(self.decoder_layers) * math.prod(cross) * self.model.lm_head.weight
                     .element_size() / mb, cfg.num_cross_blocks)
 
-    def _copy_blocks(self, copies, src: torch.Tensor | None = None,
-                     dst: torch.Tensor | None = None) -> None:
+    def _copy_blocks(self, copies) -> None:
         """Copy-on-write of ``(src, dst)`` block pairs in every self-attention pool, one
         launch (model_runner.py:162-167)."""
         if not copies:
             return
-        if src is None:
-            src = torch.tensor([s for s, _ in copies], dtype=torch.int64, device=self.device)
-            dst = torch.tensor([d for _, d in copies], dtype=torch.int64, device=self.device)
+        src = torch.tensor([s for s, _ in copies], dtype=torch.int64, device=self.device)
+        dst = torch.tensor([d for _, d in copies], dtype=torch.int64, device=self.device)
         hip_attn.copy_blocks(self._self_caches, src, dst, self._cache_ptrs,
                              staged=hip_attn.copy_pairs_need_staging(copies))
 
@@ -284,99 +243,65 @@ class ModelRunner:
 
     # -- step metadata -----------------------------------------------------------------
 
-    def _prepare(self, seqs, copies=()):
+    def _prepare(self, batch):
         """Stage the step's metadata in HBM, run the copy-on-write, publish the Context.
 
-        Returns the device ``(input_ids, positions)`` of the one token fed per sequence,
-        padded to the step's row bucket (``row_buckets``): padding rows feed token 0 at
-        position 0 with a zero-length context and write no KV slot, so the rows of the
-        real sequences come out as without padding and their logits are the first rows.
+        The host core writes the metadata of its scheduled rows into the pinned staging
+        (model_runner.py:288-305 formulas: the fed token is each row's last, at position
+        ``num_cached_tokens``; slot = table[pos // bs] * bs + pos % bs; context pos + 1).
+        Returns the device ``(input_ids, positions)`` padded to the step's row bucket
+        (``row_buckets``): padding rows feed token 0 at position 0 with a zero-length
+        context and write no KV slot, so the real rows come out as without padding and
+        their logits are the first rows.
         """
-        bs = self.block_size
-        n = len(seqs)
-        positions = np.fromiter((seq.num_cached_tokens for seq in seqs), np.int64, n)
-        lengths = np.fromiter((len(seq.token_ids) for seq in seqs), np.int64, n)
-        table_lens = np.fromiter((len(seq.block_table) for seq in seqs), np.int64, n)
-        bad = np.flatnonzero(lengths - positions != 1)
-        if bad.size:
-            raise ValueError("each step must feed 1 token per sequence, got "
-                             f"{lengths[bad[0]] - positions[bad[0]]}")
-        if (positions // bs >= table_lens).any():
-            raise ValueError("a sequence has no block for its write position "
-                             "(BlockManager.ensure_capacity was not called)")
-        # rows n .. padded-1 are padding: no token written, zero-length contexts
+        core, n, num_pairs = batch.core, batch.num_rows, batch.num_pairs
         padded = next((b for b in self._buckets if b >= n), n)
         buf = self._buffers
-        width = int(table_lens.max())
-        if padded > buf.rows or width > buf.width or len(copies) > buf.rows:
-            buf = self._buffers = _StepBuffers(max(padded, len(copies), buf.rows),
+        width = core.max_table_len()
+        if padded > buf.rows or width > buf.width or num_pairs > buf.rows:
+            buf = self._buffers = _StepBuffers(max(padded, num_pairs, buf.rows),
                                                max(width, buf.width), self.device)
             self._graphs.clear()  # they read the old buffers
             self._self_metadata.clear()
         buf.copied.synchronize()  # the previous step's upload has left the staging
         h = buf.np
-        w = buf.width
-        tables = h["tables"]
-        tables[:n] = [seq.block_table + [0] * (w - len(seq.block_table)) for seq in seqs]
-        # the one token fed is the last of each sequence's token ids (at its position)
-        h["input_ids"][:n] = [seq.token_ids[-1] for seq in seqs]
-        h["positions"][:n] = positions
-        h["lengths"][:n] = lengths
-        # slot = block_table[pos // bs] * bs + pos % bs (model_runner.py:296-299)
-        h["slots"][:n] = (tables[np.arange(n), positions // bs].astype(np.int64) * bs
-                          + positions % bs)
-        lens = positions + 1
-        h["context_lens"][:n] = lens
-        if padded > n:
-            for name, value in (("input_ids", 0), ("positions", 0), ("slots", -1),
-                                ("context_lens", 0), ("lengths", 1)):
-                h[name][n:padded] = value
-            h["tables"][n:padded] = 0
         # Beams of a request share their prefix blocks (copy-on-write forks): their
-        # self-attention runs as one row group that reads each shared block once.  The
-        # group list is padded with empty groups to n entries so that one launch shape
-        # serves every batch of n rows.
-        starts = _row_groups(seqs, hip_attn.MAX_GROUP_SIZE)
-        grouped = len(starts) - 1 < n
-        if grouped:  # padding rows are groups of one (zero output)
-            starts += range(n + 1, padded + 1)
-            num_groups = len(starts) - 1
-            h["group_start"][: num_groups + 1] = starts
-            h["group_start"][num_groups + 1: padded + 1] = padded
-        else:  # one row per workgroup: longest context first
-            h["order"][:padded] = hip_attn.longest_first(lens.tolist() + [0] * (padded - n))
-        if copies:
-            h["copy_src"][: len(copies)] = [s for s, _ in copies]
-            h["copy_dst"][: len(copies)] = [d for _, d in copies]
+        # self-attention runs as row groups that read each shared block once; the group
+        # list is padded with empty groups so one launch shape serves every n-row batch.
+        grouped = core.pack(padded, buf.width, hip_attn.MAX_GROUP_SIZE, h)
         buf.upload()
         d = buf.d
-        # copy-on-write first: this step writes into the now-private blocks
-        self._copy_blocks(copies, d["copy_src"][: len(copies)], d["copy_dst"][: len(copies)])
+        if num_pairs:  # copy-on-write first: this step writes into the now-private blocks
+            src, dst = h["copy_src"][:num_pairs], h["copy_dst"][:num_pairs]
+            staged = bool(np.intersect1d(src, dst).size)
+            hip_attn.copy_blocks(self._self_caches, d["copy_src"][:num_pairs],
+                                 d["copy_dst"][:num_pairs], self._cache_ptrs, staged=staged)
         # the plan points at fixed views of the step buffers: one per (rows, grouped)
+        bs = self.block_size
         self_metadata = self._self_metadata.get((padded, grouped))
         if self_metadata is None:
+            common = dict(num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
+                          head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
+                          fuse_kv_write=True)
             if grouped:
                 self_metadata = hip_attn.get_scheduler_metadata(
-                    num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
-                    head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
                     group_start=d["group_start"][: padded + 1],
-                    max_group_size=hip_attn.MAX_GROUP_SIZE, own_tables=True,
-                    fuse_kv_write=True)
-            else:
+                    max_group_size=hip_attn.MAX_GROUP_SIZE, own_tables=True, **common)
+            else:  # one row per workgroup, longest context first
                 self_metadata = hip_attn.get_scheduler_metadata(
-                    num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
-                    head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
-                    group_order=d["order"][:padded], fuse_kv_write=True)
+                    group_order=d["order"][:padded], **common)
             self._self_metadata[(padded, grouped)] = self_metadata
         self._step_grouped = grouped
-        request_ids = tuple(seq.request_id for seq in seqs) + (None,) * (padded - n)
-        if request_ids != self._cross_key:
-            pages, enc_lens = zip(*(self._cross_pages[rid] for rid in request_ids[:n]))
+        rows = h["row_requests"][:n]
+        key = (padded, rows.tobytes())
+        if key != self._cross_key:
+            request_ids = rows.tolist()
+            pages, enc_lens = zip(*(self._cross_pages[rid] for rid in request_ids))
             pages = pages + (self._no_pages,) * (padded - n)
             enc_lens = enc_lens + (0,) * (padded - n)
             self._cross_staged = attention.stage_cross(self.decoder_layers, pages, enc_lens, bs,
                                                        self.isa, buffers=self._cross_buffers)
-            self._cross_key = request_ids
+            self._cross_key = key
         set_context(
             context_lens=d["context_lens"][:padded],
             block_tables=d["tables"][:padded],
@@ -401,20 +326,17 @@ class ModelRunner:
             self._sampling_params = sampling_params
         return self._logits_processor
 
-    def _sample(self, seqs, logits, lengths: torch.Tensor | None = None):
-        """Greedy: one token id per sequence.  Beam search: ``{request_id: candidates}``
-        (model_runner.py:355-381)."""
-        sp = seqs[0].sampling_params
+    def _sample(self, batch, logits, lengths: torch.Tensor):
+        """Greedy: each row's token id.  Beam search: each row's best
+        ``max(2, 1 + n_eos) * num_beams`` processed log-probs and token ids, best first
+        (model_runner.py:355-398); the host core merges a request's rows.  Host numpy
+        arrays either way."""
+        sp = batch.sampling_params
         processor = self._get_logits_processor(sp)
-        device = logits.device
-        if lengths is None:
-            lengths = torch.tensor([len(s.token_ids) for s in seqs], dtype=torch.long,
-                                   device=device)
         history = None
         if processor.needs_history:
-            width = max(len(s.token_ids) for s in seqs)
-            history = torch.tensor([[-1] * (width - len(s.token_ids)) + s.token_ids
-                                    for s in seqs], dtype=torch.long).to(device)
+            history = torch.from_numpy(batch.core.history()).to(logits.device,
+                                                                 non_blocking=True)
         rules = processor.topk_rules() if logits.is_cuda else None
         keep = max(2, 1 + len(sp.eos_ids())) * sp.num_beams
         if rules is not None and (sp.num_beams == 1 or keep <= decoder_ops.MAX_K):
@@ -422,67 +344,45 @@ class ModelRunner:
             if sp.num_beams == 1:
                 _, ids = decoder_ops.logprob_topk(logits, 1, log_softmax=False, lengths=lengths,
                                                   rules=rules)
-                return ids[:, 0].tolist()
+                return _to_host(ids[:, 0])[0].numpy()
             top, ids = decoder_ops.logprob_topk(logits, min(keep, logits.shape[-1]),
                                                 log_softmax=True, lengths=lengths, rules=rules)
-            return self._merge_candidates(seqs, top, ids, keep)
+            top, ids = _to_host(top.float(), ids)
+            return top.numpy(), ids.numpy()
         scores = logits.float()
         if sp.num_beams > 1:
             scores = torch.log_softmax(scores, dim=-1)
         scores = processor(history, scores, lengths)
         if sp.num_beams == 1:
-            return scores.argmax(dim=-1).tolist()
-        return self._beam_search(seqs, scores, sp)
+            return _to_host(scores.argmax(dim=-1))[0].numpy()
+        return self._beam_search(scores, sp)
 
-    def _beam_search(self, seqs, scores, sampling_params) -> dict[int, list]:
-        """Each request's best ``max(2, 1 + n_eos) * num_beams`` continuations as
-        ``(parent, token_id, cum_logprob)``, best first (model_runner.py:383-410).
-
-        Per-row top-k runs on the device; only ``[rows, k]`` values and ids come back,
-        and the per-request merge keeps the reference's ordering (a stable sort of the
-        candidates listed row by row).
-        """
+    def _beam_search(self, scores, sampling_params):
+        """Each row's best ``max(2, 1 + n_eos) * num_beams`` continuations
+        (model_runner.py:383-393) on the device: ([rows, k] scores, [rows, k] ids) on
+        the host."""
         keep = max(2, 1 + len(sampling_params.eos_ids())) * sampling_params.num_beams
-        top_scores, top_ids = torch.topk(scores, min(keep, scores.shape[-1]), dim=-1)
-        return ModelRunner._merge_candidates(seqs, top_scores, top_ids, keep)
-
-    @staticmethod
-    def _merge_candidates(seqs, top_scores, top_ids, keep: int) -> dict[int, list]:
-        """Add each row's cumulative log-prob to its top-k and keep every request's best
-        ``keep`` candidates over its rows, best first."""
-        top_scores, top_ids = _to_host(top_scores.float(), top_ids)
-        scores, ids = top_scores.numpy(), top_ids.numpy()
-        # each row's cumulative log-prob cast to float32 and added in float32
-        # (model_runner.py:394-396)
-        scores += np.array([s.cum_logprob for s in seqs], dtype=np.float32)[:, None]
-        fast = _merge_equal_beam_groups(seqs, scores, ids, keep)
-        if fast is not None:
-            return fast
-        candidates = defaultdict(list)
-        for seq, row_scores, row_ids in zip(seqs, scores.tolist(), ids.tolist()):
-            candidates[seq.request_id].extend(zip([seq] * len(row_ids), row_ids, row_scores))
-        for cands in candidates.values():
-            cands.sort(key=lambda c: c[2], reverse=True)
-            del cands[keep:]
-        return dict(candidates)
+        top, ids = torch.topk(scores, min(keep, scores.shape[-1]), dim=-1)
+        top, ids = _to_host(top, ids)
+        return top.numpy(), ids.numpy()
 
     # -- step ----------------------------------------------------------------------------
 
     @torch.inference_mode()
-    def run(self, seqs, copies=()):
-        """Encode fresh sequences, run one decoder step, return ``_sample``'s result."""
-        if not seqs:
-            return []
-        fresh = [seq for seq in seqs if seq.num_cached_tokens == 0]
-        if fresh:
-            self._encode(fresh)
+    def run(self, batch):
+        """Encode the step's newly admitted requests, run one decoder step over the
+        scheduled rows, return ``_sample``'s result (None for an empty step)."""
+        if batch.num_rows == 0:
+            return None
+        if batch.fresh:
+            self._encode(batch.fresh)
         try:
-            input_ids, positions = self._prepare(seqs, copies)
+            input_ids, positions = self._prepare(batch)
             logits = self._forward(input_ids, positions)
         finally:
             set_context()
-        n = len(seqs)  # the rows past n are padding
-        return self._sample(seqs, logits[:n], self._buffers.d["lengths"][:n])
+        n = batch.num_rows  # the rows past n are padding
+        return self._sample(batch, logits[:n], self._buffers.d["lengths"][:n])
 
     def _forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         """The decoder step, eager or replayed from a HIP graph of this batch size.

@@ -1,147 +1,120 @@
-"""Continuous batching and beam bookkeeping on the host.
+"""Continuous batching on the native host core (vflorence/engine/scheduler.py:8-127).
 
-Same policy as vflorence/engine/scheduler.py:8-127, because block tables, copy pairs
-and beam selection must come out exactly as the reference's for token parity:
+The running hypotheses, their block tables and the beam bookkeeping live in the
+engine core (``engine/core.py``, include/vfl_engine.h); this class submits requests
+to it, starts steps, feeds each step's sampled tokens or beam candidates back and
+turns finished requests into ``RequestOut``.  The policy is the reference's:
 
-* admission is FIFO while the running requests' beam counts fit ``max_num_seqs``;
-* before a step every running sequence gets a writable slot
-  (``BlockManager.ensure_capacity``), and the step fails if the pool cannot cover it;
-* greedy steps append each sampled token and retire finished sequences;
-* beam steps walk each request's candidates best first: a stopped candidate becomes a
-  finished hypothesis only if it ranks within the top ``num_beams``, live ones fill up
-  to ``num_beams`` running children, finished hypotheses are kept by length-penalised
-  score, and the request ends when no live beam remains or the early-stopping test
-  passes.  Children share their parent's blocks (``fork``) and every parent is retired,
-  so a request's beams stay adjacent in ``running``, which the cross-attention beam
-  groups rely on.
+* admission is FIFO while the running requests' beams plus the next request's fit
+  ``max_num_seqs``;
+* a step first makes every running row's next position writable (a fresh block, or
+  a private copy of a block other rows still hold), and fails with "KV cache is full"
+  if the pool cannot cover that;
+* greedy steps append each row's token and retire finished rows;
+* beam steps keep each request's best live continuations, collect finished
+  hypotheses by length-penalised score and end the request when no continuation lives
+  or the early-stopping test passes; a request's beams stay adjacent.
 """
 
 from __future__ import annotations
 
-from collections import defaultdict, deque
-from operator import attrgetter
+from collections import deque
 
 from .block_manager import BlockManager
+from .core import EngineCore, RowView
 from .sequence import RequestOut, Sequence
 
-_score = attrgetter("score")
+
+class StepBatch:
+    """A scheduled step: how many rows run and how many copy-on-write pairs precede
+    them, the requests admitted this step (their encoders run first), the shared
+    sampling parameters, and the core that holds the rows."""
+
+    __slots__ = ("core", "num_rows", "num_pairs", "fresh", "sampling_params")
+
+    def __init__(self, core, num_rows, num_pairs, fresh, sampling_params):
+        self.core = core
+        self.num_rows = num_rows
+        self.num_pairs = num_pairs
+        self.fresh = fresh
+        self.sampling_params = sampling_params
 
 
 class Scheduler:
     def __init__(self, config):
         self.max_num_seqs = config.max_num_seqs
-        self.block_manager = BlockManager(config.num_blocks, config.block_size)
+        self.core = EngineCore(config.num_blocks, config.block_size, config.max_num_seqs)
+        self.block_manager = BlockManager.view(self.core.pool)
         self.waiting: deque[Sequence] = deque()
-        self.running: list[Sequence] = []
-        self._finished_beams: dict[int, list[Sequence]] = defaultdict(list)
+        self._requests: dict[int, Sequence] = {}  # submitted, not yet finished
 
     def is_finished(self) -> bool:
-        return not self.waiting and not self.running
+        return not self.waiting and self.core.num_running == 0
 
     def reset(self) -> None:
+        """Drop every request and free every block (after an aborted step)."""
+        self.core.reset()
         self.waiting.clear()
-        self.running.clear()
-        self._finished_beams.clear()
-        self.block_manager.reset()
+        self._requests.clear()
 
     def add(self, seq: Sequence) -> None:
+        p = seq.sampling_params
+        self.core.add_request(seq.request_id, seq.token_ids, p.num_beams, p.max_tokens,
+                              sorted(p.eos_ids()), p.length_penalty, p.early_stopping)
         self.waiting.append(seq)
+        self._requests[seq.request_id] = seq
 
-    def remove(self, seq: Sequence) -> None:
-        self.running.remove(seq)
-        self.block_manager.deallocate(seq)
+    def active_params(self):
+        """The sampling parameters the submitted requests share (None when idle)."""
+        for seq in self._requests.values():
+            return seq.sampling_params
+        return None
 
-    def schedule(self) -> tuple[list[Sequence], list[tuple[int, int]]]:
-        """Admit waiting requests, give every running sequence a slot; return the step's
-        sequences and its copy-on-write pairs."""
-        if self.waiting:  # admission needs the running requests' beam counts
-            beams = {seq.request_id: seq.sampling_params.num_beams for seq in self.running}
-            used = sum(beams.values())
-            while (self.waiting
-                   and used + self.waiting[0].sampling_params.num_beams <= self.max_num_seqs):
-                seq = self.waiting.popleft()
-                self.running.append(seq)
-                used += seq.sampling_params.num_beams
-        seqs = list(self.running)
-        bm = self.block_manager
-        if bm.required_new_blocks(seqs) > bm.num_free_blocks:
-            raise RuntimeError("KV cache is full; increase num_blocks")
-        copies = []
-        for seq in seqs:
-            pair = bm.ensure_capacity(seq)
-            if pair is not None:
-                copies.append(pair)
-        return seqs, copies
+    @property
+    def num_running(self) -> int:
+        """Running rows (hypotheses)."""
+        return self.core.num_running
 
-    def postprocess(self, seqs: list[Sequence], sample_out) -> list[tuple[int, RequestOut]]:
-        for seq in seqs:
-            seq.num_cached_tokens += 1
-        if seqs and seqs[0].sampling_params.num_beams > 1:
-            return self._postprocess_beam(seqs, sample_out)
-        return self._postprocess_greedy(seqs, sample_out)
+    @property
+    def running(self) -> list[RowView]:
+        """Snapshots of the running rows, in row order."""
+        return self.core.rows()
 
-    def _postprocess_greedy(self, seqs, token_ids) -> list[tuple[int, RequestOut]]:
+    @property
+    def num_pending_beams(self) -> int:
+        """Requests holding finished beam hypotheses while other beams still run."""
+        return self.core.num_pending_beams
+
+    def abort_request(self, request_id: int) -> bool:
+        """Drop a waiting or running request between steps (its blocks are freed, it is
+        not reported as finished); False if it is not known."""
+        known = self.core.abort_request(request_id)
+        self.waiting = deque(s for s in self.waiting if s.request_id != request_id)
+        return self._requests.pop(request_id, None) is not None or known
+
+    def schedule(self) -> StepBatch:
+        admitted = self.core.schedule()
+        fresh = []
+        for rid in admitted:
+            seq = self.waiting.popleft()
+            if seq.request_id != rid:
+                raise RuntimeError(f"admission order diverged: {seq.request_id} != {rid}")
+            fresh.append(seq)
+        return StepBatch(self.core, self.core.num_rows, self.core.num_pairs, fresh,
+                         self.active_params())
+
+    def postprocess(self, batch: StepBatch, sample_out) -> list[tuple[int, RequestOut]]:
+        """Feed the step's result back: greedy, one token per row; beam search, each
+        row's best ``k`` (scores, token ids) as two [rows, k] arrays."""
+        if batch.num_rows == 0:
+            return []
+        if batch.sampling_params.num_beams > 1:
+            scores, ids = sample_out
+            self.core.beam_update(scores, ids)
+        else:
+            self.core.greedy_update(sample_out)
         outputs = []
-        for seq, token in zip(seqs, token_ids):
-            seq.append_token(token)
-            if seq.is_finished:
-                self.remove(seq)
-                outputs.append((seq.request_id, seq.to_output()))
-        return outputs
-
-    def _postprocess_beam(self, seqs, candidates_by_request) -> list[tuple[int, RequestOut]]:
-        outputs = []
-        eos_of: dict[int, set[int]] = {}
-        for request_id, candidates in candidates_by_request.items():
-            sp = candidates[0][0].sampling_params
-            num_beams = sp.num_beams
-            eos = eos_of.get(id(sp))
-            if eos is None:
-                eos = eos_of[id(sp)] = sp.eos_ids()
-            max_tokens = sp.max_tokens
-            finished = self._finished_beams[request_id]
-            live: list[tuple[Sequence, Sequence]] = []
-            for rank, (parent, token, cum_logprob) in enumerate(candidates):
-                if rank >= num_beams and len(live) >= num_beams:
-                    break
-                # Sequence.is_finished of the child (the parent's tokens plus ``token``),
-                # decided before the child exists: only kept candidates are forked
-                generated = len(parent.token_ids) + 1 - len(parent.decoder_token_ids)
-                if token in eos or generated >= max_tokens:
-                    if rank < num_beams:
-                        finished.append(parent.fork(token, cum_logprob))
-                elif len(live) < num_beams:
-                    live.append((parent, parent.fork(token, cum_logprob)))
-            if finished:
-                finished.sort(key=_score, reverse=True)
-                del finished[num_beams:]
-            # the early-stopping test compares with the best live beam only when the
-            # finished list is full (the live scores are not needed otherwise)
-            done = not live or (len(finished) >= num_beams and (
-                sp.early_stopping
-                or finished[-1].score >= max(child.score for _, child in live)))
-            if done:
-                self._finished_beams.pop(request_id, None)
-                outputs.append((request_id, finished[0].to_output()))
-            else:
-                # A parent's first live child takes over its block table; further
-                # children fork from that child.  The reference forks every child and
-                # then deallocates every parent (scheduler.py:120-126): per block that
-                # is +1 per child and -1 per parent, so the reference counts, the blocks
-                # freed below and their order come out the same.
-                holder: dict[int, Sequence] = {}
-                for parent, child in live:
-                    owner = holder.get(id(parent))
-                    if owner is None:
-                        child.block_table = parent.block_table
-                        parent.block_table = []
-                        holder[id(parent)] = child
-                    else:
-                        self.block_manager.fork(owner, child)
-                    self.running.append(child)
-        # retire every parent: blocks freed in step order, one pass over ``running``
-        for seq in seqs:
-            self.block_manager.deallocate(seq)
-        retired = set(map(id, seqs))
-        self.running = [s for s in self.running if id(s) not in retired]
+        for rid, completion in self.core.finished():
+            seq = self._requests.pop(rid)
+            outputs.append((rid, RequestOut(seq.encoder_token_ids, completion, seq.pixel_values)))
         return outputs
