@@ -33,6 +33,10 @@ class Config:
     device: str = "cuda"
     # decode steps replayed from HIP graphs, one per batch size (eager when False)
     cuda_graphs: bool = False
+    # the decoder step under torch.compile(dynamic=True), as the reference compiles it
+    # (vflorence/engine/model_runner.py:102-124); the attention, KV-write, LayerNorm and
+    # projection custom ops stay opaque.  An alternative to cuda_graphs, not combined.
+    compile: bool = False
     block_size: int = field(init=False)
     num_cross_blocks: int = field(init=False)
     hf_config: object = field(init=False)
@@ -45,6 +49,8 @@ class Config:
         self.block_size = BLOCK_SIZE
         if self.max_num_seqs <= 0:
             raise ValueError("max_num_seqs must be positive")
+        if self.compile and self.cuda_graphs:
+            raise ValueError("compile and cuda_graphs are alternatives; choose one")
         if self.dtype not in (torch.float32, torch.bfloat16, torch.float16):
             raise ValueError("dtype must be torch.float32, torch.bfloat16 or torch.float16")
         if isinstance(self.model, PretrainedConfig):

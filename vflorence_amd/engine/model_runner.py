@@ -148,6 +148,10 @@ class ModelRunner:
         self._self_metadata: dict[tuple[int, bool], hip_attn.SchedulerMetadata] = {}
         self._no_pages = torch.zeros(0, dtype=torch.int32)
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
+        # the decoder step; compiled as the reference compiles it when asked
+        # (vflorence/engine/model_runner.py:121-123)
+        self.decode_fn = (torch.compile(self.model, dynamic=True) if config.compile
+                          else self.model)
 
     def repack_weights(self) -> None:
         """Make the decoder's packed projection weights follow the current weights, after
@@ -395,7 +399,7 @@ class ModelRunner:
         repeats in the replay with the same values.
         """
         if not self.config.cuda_graphs:
-            return self.model(input_ids, positions)
+            return self.decode_fn(input_ids, positions)
         n = input_ids.shape[0]
         key = (n, self._step_grouped)  # grouped steps launch another kernel
         entry = self._graphs.get(key)

@@ -24,6 +24,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from ..decoder_ops import LINEAR_MAX_IN, LINEAR_MAX_OUT, LINEAR_MAX_ROWS
 from .attention import decoder_cross_attention, decoder_self_attention
 
 
@@ -68,7 +69,8 @@ class DecodeLinear(nn.Linear):
         w = self.weight
         if not (w.is_cuda and w.dtype in (torch.bfloat16, torch.float16)
                 and decoder_ops.linear_fits(1, w, max_in=None, max_out=None)):
-            self._packed = self._packed_key = None
+            self._packed = None
+            self._packed_key = self._weight_key()
             return
         out = self._packed
         if out is not None and (out.dtype != w.dtype or out.device != w.device
@@ -78,18 +80,34 @@ class DecodeLinear(nn.Linear):
             self._packed = decoder_ops.pack_linear_weight(w.detach(), out=out)
         self._packed_key = self._weight_key()
 
-    def packed_weight(self) -> torch.Tensor:
-        """The weight in the kernel's packed layout."""
-        if self._packed is None or self._weight_key() != self._packed_key:
+    def packed_weight(self) -> torch.Tensor | None:
+        """The weight in the kernel's packed layout (None when the kernel cannot take
+        this weight).  Under torch.compile the copy made at load time is used as is
+        (version counters are not traced; ``repack`` after an update)."""
+        if torch.compiler.is_compiling():
+            return self._packed
+        if self._packed_key is None or self._weight_key() != self._packed_key:
             self.repack()
         return self._packed
 
+    def kernel_weight(self, rows: int, max_in: int | None = LINEAR_MAX_IN,
+                      max_out: int | None = LINEAR_MAX_OUT) -> torch.Tensor | None:
+        """The packed weight when the split-K kernel serves ``rows`` rows of this
+        projection (in / out features within ``max_in`` / ``max_out``), else None."""
+        packed = self.packed_weight()
+        if (packed is None or not 0 < rows <= LINEAR_MAX_ROWS
+                or (max_in is not None and self.in_features > max_in)
+                or (max_out is not None and self.out_features > max_out)):
+            return None
+        return packed
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.is_cuda and x.dtype == self.weight.dtype:
-            from .. import decoder_ops
+            packed = self.kernel_weight(x.numel() // x.shape[-1])
+            if packed is not None:
+                from .. import decoder_ops
 
-            if decoder_ops.linear_fits(x.numel() // x.shape[-1], self.weight):
-                return decoder_ops.linear(x, self.packed_weight(), self.bias, self.out_features)
+                return decoder_ops.linear(x, packed, self.bias, self.out_features)
         return F.linear(x, self.weight, self.bias)
 
 
@@ -227,14 +245,13 @@ class BartDecoderLayer(nn.Module):
             from .. import decoder_ops as ops
 
             rows = h.numel() // h.shape[-1]
-            w1, w2 = self.fc1.weight, self.fc2.weight
-            if (0 < rows <= ops.LINEAR_MAX_ROWS and ops.linear_fits(rows, w1, max_out=None)
-                    and ops.linear_fits(rows, w2, max_in=None)):
-                mid = ops.linear(h, self.fc1.packed_weight(), self.fc1.bias,
-                                 self.fc1.out_features,
+            w1 = self.fc1.kernel_weight(rows, max_out=None)
+            w2 = self.fc2.kernel_weight(rows, max_in=None)
+            if w1 is not None and w2 is not None:
+                mid = ops.linear(h, w1, self.fc1.bias, self.fc1.out_features,
                                  flags=ops.LINEAR_GELU | ops.LINEAR_Y_PACKED)
-                out = ops.linear(mid, self.fc2.packed_weight(), self.fc2.bias,
-                                 self.fc2.out_features, rows=rows, flags=ops.LINEAR_X_PACKED)
+                out = ops.linear(mid, w2, self.fc2.bias, self.fc2.out_features, rows=rows,
+                                 flags=ops.LINEAR_X_PACKED)
                 return out.view(*h.shape[:-1], self.fc2.out_features)
         return self.fc2(self.activation_fn(self.fc1(h)))
 
