@@ -85,6 +85,37 @@ def test_reshape_and_cache_unaligned_source():
         assert torch.equal(vl[s // bs, :, s % bs], value[t])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_reshape_and_cache_v_groups(dtype, head_dim, offset):
+    """V of 16-bit pools is written a whole 4-token group at a time when four tokens
+    take four consecutive slots starting at a multiple of 4, else token by token: runs
+    that start on and off a group, a padding slot inside a run, a ragged tail, repeated
+    blocks in another order; 16-byte aligned and unaligned source rows (``offset``)."""
+    g = torch.Generator().manual_seed(14 + head_dim + offset)
+    H, bs, NB = 16, 16, 40
+    slots = (list(range(32, 48)) + list(range(66, 74)) + [100, 101, -1, 103]
+             + list(range(200, 207)) + [5, 4, 7, 6] + list(range(400, 404)))
+    T = len(slots)
+    fused = torch.randn(T, 2 * H * head_dim + offset, generator=g).to(dtype)
+    key = fused[:, offset: offset + H * head_dim].reshape(T, H, head_dim)
+    value = fused[:, offset + H * head_dim:].reshape(T, H, head_dim)
+    kc = torch.randn(NB, H, bs, head_dim, generator=g).to(dtype)
+    vc = torch.randn(NB, H, bs, head_dim, generator=g).to(dtype)
+    kd, vd = kc.to(DEV), hip().v_cache_from_logical(vc).to(DEV)
+    fd = fused.to(DEV)
+    keyd = fd[:, offset: offset + H * head_dim].reshape(T, H, head_dim)
+    vald = fd[:, offset + H * head_dim:].reshape(T, H, head_dim)
+    st = torch.tensor(slots, dtype=torch.int64)
+    hip().reshape_and_cache(keyd, vald, kd, vd, st.to(DEV))
+    torch.cuda.synchronize()
+    ko, vo = raw_bits(kc), raw_bits(vc)
+    orc.reshape_and_cache(raw_bits(key), raw_bits(value), ko, vo, st.numpy())
+    assert np.array_equal(raw_bits(kd), ko)
+    assert np.array_equal(raw_bits(hip().v_cache_logical(vd)), vo)
+
+
 def test_reshape_and_cache_large_encoder_write():
     """The encoder path writes G * enc_len rows at once (model_runner.py:248-259)."""
     g = torch.Generator().manual_seed(13)

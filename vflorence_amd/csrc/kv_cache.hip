@@ -32,17 +32,33 @@ int launch_status(const char *what) {
   return VFL_OK;
 }
 
+// Whether tokens t .. t+3 (all < T) take slots s .. s+3 in order, s = slots[t] a
+// multiple of 4: one whole 4-token group of a block.
+__device__ __forceinline__ bool fills_group(const int64_t *slots, int64_t t, int64_t T,
+                                            int64_t num_slots) {
+  if (t < 0 || t + 3 >= T) return false;
+  const int64_t s = slots[t];
+  return s >= 0 && s % 4 == 0 && s + 3 < num_slots && slots[t + 1] == s + 1 &&
+         slots[t + 2] == s + 2 && slots[t + 3] == s + 3;
+}
+
 // ---------------------------------------------------------------------------
 // reshape_and_cache: one thread per 16-byte chunk of a (token, head) row.
 // ---------------------------------------------------------------------------
 // VT: the V pool stores each [block][head] slice with tokens interleaved in groups of
-// four (16-bit pools, vtile_index); the token's head_dim values land 4 elements apart.
+// four (16-bit pools, vtile_index: [token/4][dim][token%4]).  Tokens whose slots fill
+// a 4-token group in order (every group of a prompt's encoder tokens but a ragged last
+// one) are written by the thread of the group's first token: its 8 dims of the 4 tokens
+// are 64 contiguous bytes, so a group's threads write its whole run for the head in
+// full 128-byte lines, and the group's other threads skip V.  Any other token
+// (scattered slots, a ragged group) writes its own V element by element.
+// whole_words: the V pool is 16-byte aligned (the group's stores are then aligned).
 template <int DT, bool ALIGNED, bool VT>
 __global__ __launch_bounds__(256) void reshape_and_cache_kernel(
     const typename Elem<DT>::T *__restrict__ key, const typename Elem<DT>::T *__restrict__ value,
     int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh, typename Elem<DT>::T *__restrict__ kc,
     typename Elem<DT>::T *__restrict__ vc, const int64_t *__restrict__ slots, int64_t num_tokens,
-    int num_heads, int chunks_per_row, int block_size, int64_t num_slots) {
+    int num_heads, int chunks_per_row, int block_size, int64_t num_slots, bool whole_words) {
   using T = typename Elem<DT>::T;
   constexpr int VEC = Elem<DT>::VEC;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -60,27 +76,43 @@ __global__ __launch_bounds__(256) void reshape_and_cache_kernel(
   const int64_t dst = ((blk * num_heads + h) * block_size + off) * head_dim + c * VEC;
   const T *ks = key + t * k_st + h * k_sh + c * VEC;
   const T *vs = value + t * v_st + h * v_sh + c * VEC;
-  uint4 kv, vv;
-  if constexpr (ALIGNED) {
-    kv = *reinterpret_cast<const uint4 *>(ks);
-    vv = *reinterpret_cast<const uint4 *>(vs);
-    *reinterpret_cast<uint4 *>(kc + dst) = kv;
+  static_assert(!VT || DT != VFL_FLOAT32, "interleaved V tiles are 16-bit");
+  auto load = [](const T *p) {
+    if constexpr (ALIGNED) return *reinterpret_cast<const uint4 *>(p);
+    else return load16_unaligned<DT>(p);
+  };
+  const uint4 kv = load(ks);
+  if constexpr (ALIGNED) *reinterpret_cast<uint4 *>(kc + dst) = kv;
+  else store16_unaligned<DT>(kc + dst, kv);
+  if constexpr (!VT) {
+    const uint4 vv = load(vs);
+    if constexpr (ALIGNED) *reinterpret_cast<uint4 *>(vc + dst) = vv;
+    else store16_unaligned<DT>(vc + dst, vv);
   } else {
-    kv = load16_unaligned<DT>(ks);
-    vv = load16_unaligned<DT>(vs);
-    store16_unaligned<DT>(kc + dst, kv);
-  }
-  if constexpr (VT) {
-    static_assert(DT != VFL_FLOAT32, "interleaved V tiles are 16-bit");
     T *vt = vc + (blk * num_heads + h) * (int64_t)head_dim * block_size;
+    if (whole_words && off % 4 == 0 && fills_group(slots, t, num_tokens, num_slots)) {
+      // tokens t .. t+3, dims 8c .. 8c+7: word q of token j holds dims 8c+2q, 8c+2q+1
+      uint4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = load(vs + j * v_st);
+      uint4 *run = reinterpret_cast<uint4 *>(vt + vtile_index(off, c * VEC, head_dim));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t a = (&v[0].x)[q], b = (&v[1].x)[q], e = (&v[2].x)[q], f = (&v[3].x)[q];
+        run[q] = make_uint4((a & 0xffffu) | (b << 16), (e & 0xffffu) | (f << 16),
+                            (a >> 16) | (b & 0xffff0000u), (e >> 16) | (f & 0xffff0000u));
+      }
+      return;
+    }
+    const int k = off % 4;
+    if (whole_words && k != 0 && t >= k && slots[t - k] == slot - k &&
+        fills_group(slots, t - k, num_tokens, num_slots))
+      return;  // written by the group's first token
+    const uint4 vv = load(vs);
     const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
     for (int e = 0; e < VEC; ++e)
       vt[vtile_index(off, c * VEC + e, head_dim)] = (T)(w[e / 2] >> (16 * (e & 1)));
-  } else if constexpr (ALIGNED) {
-    *reinterpret_cast<uint4 *>(vc + dst) = vv;
-  } else {
-    store16_unaligned<DT>(vc + dst, vv);
   }
 }
 
@@ -95,14 +127,15 @@ static void launch_reshape(bool aligned, const void *key, const void *value, int
   const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
   constexpr bool VT = DT != VFL_FLOAT32;  // v_tile_interleaved(DT)
+  const bool whole_words = (uintptr_t)vc % 16 == 0;
   if (aligned)
     reshape_and_cache_kernel<DT, true, VT><<<dim3((unsigned)blocks), dim3(threads), 0, stream>>>(
         (const E *)key, (const E *)value, k_st, k_sh, v_st, v_sh, (E *)kc, (E *)vc, slots, T, H,
-        cpr, BS, num_blocks * BS);
+        cpr, BS, num_blocks * BS, whole_words);
   else
     reshape_and_cache_kernel<DT, false, VT><<<dim3((unsigned)blocks), dim3(threads), 0, stream>>>(
         (const E *)key, (const E *)value, k_st, k_sh, v_st, v_sh, (E *)kc, (E *)vc, slots, T, H,
-        cpr, BS, num_blocks * BS);
+        cpr, BS, num_blocks * BS, whole_words);
 }
 
 // ---------------------------------------------------------------------------
