@@ -54,6 +54,9 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-engine", action="store_true",
                    help="skip the whole-engine decoder tokens/s measurement")
+    p.add_argument("--table-walk", action="store_true",
+                   help="grouped self-attention walks the block tables in every launch "
+                        "instead of reading the step's group plan")
     p.add_argument("--ungrouped-self", action="store_true",
                    help="self-attention one row per workgroup (no shared-prefix groups)")
     p.add_argument("--counters", action="store_true",
@@ -139,9 +142,11 @@ def step_bytes(plan, enc, elem=2, grouped=True, self_only=False):
     return NUM_LAYERS * (self_b + cross_b) + cow_b, self_b, cross_b, cow_b
 
 
-def capture_steps(torch, wl, grouped=True, keep_outputs=False):
+def capture_steps(torch, wl, grouped=True, keep_outputs=False, planned=True):
     """One HIP graph per decode step of the schedule.  ``grouped``: each request's beams
     form one self-attention row group (own tables, shared blocks read once).
+    ``planned``: grouped launches read the step's group plan (made on the host from the
+    step's tables, uploaded before capture) instead of walking the block tables.
     ``keep_outputs``: also return, per step, the [(self out, cross out)] per layer that
     its graph writes (every step keeps its own output buffers)."""
     from vflorence_amd import hip_attn
@@ -164,14 +169,21 @@ def capture_steps(torch, wl, grouped=True, keep_outputs=False):
         lens = torch.tensor(plan.context_lens, dtype=torch.int32, device=dev)
         slots = torch.tensor(plan.slot_mapping, dtype=torch.int64, device=dev)
         # slots come from BlockManager tables (private last blocks): fused KV write
+        gplan = None
         if grouped:
             # every group is resident at once: no dispatch order needed
-            starts = torch.arange(0, rows + 1, BEAMS, dtype=torch.int32, device=dev)
+            starts_h = torch.arange(0, rows + 1, BEAMS, dtype=torch.int32)
+            starts = starts_h.to(dev)
             order = None
+            if planned:
+                gplan = hip_attn.build_group_plan(
+                    tables.cpu(), lens.cpu(), starts_h, max_group_size=BEAMS,
+                    block_size=BLOCK, num_blocks=wl["layers"][0].self_attn.k_cache.shape[0],
+                ).to(dev)
             meta = hip_attn.get_scheduler_metadata(
                 num_reqs=rows, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS, head_dim=HEAD_DIM,
                 dtype=torch.bfloat16, block_size=BLOCK, group_start=starts,
-                max_group_size=BEAMS, own_tables=True, fuse_kv_write=True)
+                max_group_size=BEAMS, own_tables=True, fuse_kv_write=True, group_plan=gplan)
         else:
             starts = None
             order = torch.tensor(hip_attn.longest_first(plan.context_lens), dtype=torch.int32,
@@ -185,7 +197,7 @@ def capture_steps(torch, wl, grouped=True, keep_outputs=False):
             src = torch.tensor([s for s, _ in plan.copies], dtype=torch.int64, device=dev)
             dst = torch.tensor([d for _, d in plan.copies], dtype=torch.int64, device=dev)
             staged = hip_attn.copy_pairs_need_staging(plan.copies)
-        keep.append((tables, lens, slots, starts, order, meta, src, dst))
+        keep.append((tables, lens, slots, starts, order, meta, src, dst, gplan))
 
         def run():
             set_context(context_lens=lens, block_tables=tables, slot_mapping=slots,
@@ -236,7 +248,8 @@ def schedule_order(n: int, steps: int = DECODE_STEPS) -> list[int]:
 
 KERNEL_NAMES = {  # kernel name prefixes of the decode step's launches
     "cross": "void vfl::paged_decode_mfma_kernel<1, 64, 4, 2, false>",
-    "self": "void vfl::paged_decode_shared_kernel<1, 64, 2, 2, true>",
+    "self": "void vfl::paged_decode_planned_kernel<1, 64, 2, 4, true>",
+    "self_walk": "void vfl::paged_decode_shared_kernel<1, 64, 2, 2, true>",
     "self_rows": "void vfl::paged_decode_mfma_kernel<1, 64, 2, 2, true>",
     "cow": "vfl::copy_blocks_kernel",
 }
@@ -908,7 +921,8 @@ def main():
         return
     print("[bench] capturing 128 decode-step graphs", flush=True)
     grouped = not args.ungrouped_self
-    graphs, keep = capture_steps(torch, wl, grouped)
+    planned = grouped and not args.table_walk
+    graphs, keep = capture_steps(torch, wl, grouped, planned=planned)
     plans = wl["plans"]
     per_step = [step_bytes(p, wl["enc"], grouped=grouped) for p in plans]
 
@@ -958,7 +972,7 @@ def main():
     if in_step is not None:
         cross_in_step = in_step["cross"]
         c_step_avg = sum(cross_in_step) / len(cross_in_step)
-        self_key = "self" if grouped else "self_rows"
+        self_key = ("self" if planned else "self_walk") if grouped else "self_rows"
         self_by_ctx = self_in_step_table(in_step[self_key], wl["plans"], grouped)
         cow = in_step["cow"]
         measured_over = (f"{len(cross_in_step)} launches inside the decode-step graphs, one "
@@ -1018,7 +1032,9 @@ def main():
         "attn_path_rows_per_s": round(rows * args.steps / elapsed, 1),
         "attn_path_request_tokens_per_s": round(REQUESTS * args.steps / elapsed, 1),
         "bytes_per_step_avg": int(total_bytes / args.steps),
-        "self_attention_groups": "beams (shared prefix blocks read once)" if grouped else "rows",
+        "self_attention_groups": (("beams (shared prefix blocks read once), "
+                                   + ("group plan per step" if planned else "table walk"))
+                                  if grouped else "rows"),
         "wall_s_timed": round(wall, 4),
         "roofline": {
             "bound": "hbm",

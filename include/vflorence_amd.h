@@ -118,6 +118,14 @@ typedef struct vfl_sched_meta {
   int32_t waves_per_workgroup; /* waves splitting one (group, head) context: 1..8   */
   int32_t max_group_size;      /* largest row group (beams)                         */
   int32_t group_tables;        /* enum vfl_group_tables                             */
+  /* Optional group plan (own-table groups, 16-bit caches): set by the caller after
+   * vfl_get_scheduler_metadata, which leaves it NULL.  A device copy of what
+   * vfl_build_group_plan wrote for this call's tables, lengths and groups; the launch
+   * then reads each group's distinct blocks from it instead of walking the tables,
+   * and runs group_plan_slots x num_heads workgroups. */
+  const int32_t *group_plan;
+  int64_t group_plan_stride;   /* words per slot (vfl_group_plan_stride)            */
+  int64_t group_plan_slots;    /* slots the plan holds (>= its groups)              */
 } vfl_sched_meta;
 
 /*
@@ -134,6 +142,32 @@ int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, int num_hea
                                int64_t max_blocks_per_seq, int max_group_size,
                                int dtype, int waves_per_workgroup, int group_tables,
                                vfl_sched_meta *meta);
+
+/*
+ * Group plans: the per-step schedule of own-table row groups (a request's beams)
+ * that the reference's get_scheduler_metadata computes per decode step
+ * (vflorence/engine/model_runner.py:308-319), made once on the host and read by every
+ * layer's self-attention launch.  Words of one slot for groups of up to
+ * max_group_size rows (1..8) over block tables max_blocks_per_seq wide (<= 65536);
+ * 0 for sizes out of range.
+ */
+int64_t vfl_group_plan_stride(int max_group_size, int64_t max_blocks_per_seq);
+
+/*
+ * Host function (all pointers host memory; no device call).  Writes plan, of
+ * 4 + num_slots * stride int32: plan[0] = num_groups, then one slot per dispatch
+ * position s < num_slots: group group_order[s] (s when group_order is NULL) for
+ * s < num_groups, empty after.  A slot holds its group's first row and row count and,
+ * position by position, each distinct block id in [0, num_blocks) that the group's
+ * rows list there, with the rows that list it.  Arguments as for
+ * vfl_attention_with_kv_cache (block_table / seq_lens / group_start / group_order of
+ * the same call).  Fails when a group has more than 8 rows or stride is too small.
+ */
+int vfl_build_group_plan(const int32_t *block_table, int64_t block_table_stride,
+                         int max_blocks_per_seq, const int32_t *seq_lens, int64_t num_rows,
+                         const int32_t *group_start, const int32_t *group_order,
+                         int64_t num_groups, int block_size, int64_t num_blocks,
+                         int32_t *plan, int64_t num_slots, int64_t stride);
 
 /*
  * Replaces vllm_cpu_attn.attention_with_kv_cache(query, k_cache, v_cache, out,

@@ -25,6 +25,8 @@ EXPORTED_SYMBOLS = (
     "vfl_get_isa",
     "vfl_reshape_and_cache",
     "vfl_get_scheduler_metadata",
+    "vfl_group_plan_stride",
+    "vfl_build_group_plan",
     "vfl_attention_with_kv_cache",
     "vfl_self_attention_with_kv_write",
     "vfl_copy_blocks",
@@ -49,6 +51,9 @@ class SchedMeta(ctypes.Structure):
         ("waves_per_workgroup", ctypes.c_int32),
         ("max_group_size", ctypes.c_int32),
         ("group_tables", ctypes.c_int32),
+        ("group_plan", ctypes.c_void_p),
+        ("group_plan_stride", ctypes.c_int64),
+        ("group_plan_slots", ctypes.c_int64),
     ]
 
 
@@ -66,6 +71,11 @@ _SIGNATURES = {
     "vfl_get_scheduler_metadata": (
         ctypes.c_int,
         [_i64, _i64, _i32, _i32, _i32, _i64, _i32, _i32, _i32, _i32, ctypes.POINTER(SchedMeta)],
+    ),
+    "vfl_group_plan_stride": (_i64, [_i32, _i64]),
+    "vfl_build_group_plan": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _vp, _i64, _vp, _vp, _i64, _i32, _i64, _vp, _i64, _i64],
     ),
     "vfl_attention_with_kv_cache": (
         ctypes.c_int,

@@ -207,6 +207,37 @@ template <int N> __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// Maximum over the 16 lanes of each row (every lane gets its row's maximum).
+__device__ __forceinline__ int row_max16(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR1, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR2, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, DPP_ROW_HALF_MIRROR, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, DPP_ROW_MIRROR, 0xF, 0xF, false));
+  return x;
+}
+
+// Across the four 16-lane rows, lane-wise: lanes l, l^16, l^32 and l^48 (the four row
+// groups of one MFMA tile column) all end with the same value.  v_permlane16_swap
+// pairs rows 0-1 and 2-3, v_permlane32_swap rows 0-2 and 1-3; both are VALU moves, no
+// LDS round trip.  The sum is (r0 + r1) + (r2 + r3) on every lane, the order of an
+// xor-16-then-xor-32 butterfly.
+__device__ __forceinline__ float rows_max4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 constexpr float NEG_INF_F = -__builtin_huge_valf();

@@ -45,6 +45,20 @@ struct KvWrite {
   bool vec;  // every K and V row is 16-byte aligned (16-byte loads)
 };
 
+// K/V pages are read once per decode step, so their loads are non-temporal: they stream
+// through without displacing the metadata, queries and tables the step's next launches
+// read from the caches.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 load_stream16(const uint16_t *p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 load_stream8(const uint16_t *p) {
+  const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(p));
+  return make_uint2(v.x, v.y);
+}
+
 template <int DT, int D>
 __device__ __forceinline__ void mfma_load_block(const uint16_t *__restrict__ kc,
                                                 const uint16_t *__restrict__ vc, int id, bool ok,
@@ -54,12 +68,12 @@ __device__ __forceinline__ void mfma_load_block(const uint16_t *__restrict__ kc,
 #pragma unroll
   for (int kk = 0; kk < D / 32; ++kk) {
     blk.k[kk] = make_uint4(0, 0, 0, 0);
-    if (ok) blk.k[kk] = *reinterpret_cast<const uint4 *>(kc + base + k_lane + 32 * kk);
+    if (ok) blk.k[kk] = load_stream16(kc + base + k_lane + 32 * kk);
   }
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
     blk.v[c] = make_uint2(0, 0);
-    if (ok) blk.v[c] = *reinterpret_cast<const uint2 *>(vc + base + v_lane + 64 * c);
+    if (ok) blk.v[c] = load_stream8(vc + base + v_lane + 64 * c);
   }
 }
 
@@ -83,8 +97,7 @@ __device__ __forceinline__ void mfma_consume(const uint4 (&qop)[D / 32], MfmaBlo
     sv[j] = valid[j] ? s[j] * scale_log2 : NEG_INF_F;
   }
   float mb = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-  mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-  mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+  mb = rows_max4(mb);
   // Each column moves its reference only when its own block max needs it, so a
   // column's arithmetic never depends on the other columns of the tile.
   const bool need = mb > m + RESCALE_SLACK_LOG2;
@@ -332,8 +345,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
   }
 
   // Column totals of the running sums (the 4 row groups hold disjoint tokens).
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  l = rows_sum4(l);
 
   if constexpr (NW == 1) {
     if (col >= nrows) return;

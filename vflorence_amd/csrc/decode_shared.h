@@ -66,11 +66,7 @@ __device__ __forceinline__ uint32_t column_mask(bool pred) {
 
 // Maximum of a per-column value over the 16 columns (every lane gets it).
 __device__ __forceinline__ int column_max(int x) {
-  x = max(x, __shfl_xor(x, 1, 64));
-  x = max(x, __shfl_xor(x, 2, 64));
-  x = max(x, __shfl_xor(x, 4, 64));
-  x = max(x, __shfl_xor(x, 8, 64));
-  return x;
+  return row_max16(x);
 }
 
 // Fold one block into the lane's state for the columns that list it (`mine`).
@@ -96,8 +92,7 @@ __device__ __forceinline__ void mfma_consume_cols(const uint4 (&qop)[D / 32], Mf
     sv[j] = (mine && t < Lc) ? s[j] * scale_log2 : NEG_INF_F;
   }
   float mb = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-  mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-  mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+  mb = rows_max4(mb);
   // Each column moves its reference only when its own block max needs it, so a
   // column's arithmetic never depends on the other columns of the tile.
   const bool need = mb > m + RESCALE_SLACK_LOG2;
@@ -395,8 +390,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_shared_kernel(
   }
 
   // Column totals of the running sums (the 4 row groups hold disjoint tokens).
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  l = rows_sum4(l);
 
   if constexpr (NW == 1) {
     if (!has_row) return;

@@ -17,7 +17,7 @@
 //   token rows keeps its own online-softmax state, merged across rows once at the
 //   end (no cross-row traffic in the loop).
 #include "common.h"
-#include "decode_shared.h"
+#include "decode_planned.h"
 
 namespace vfl {
 
@@ -349,6 +349,9 @@ struct AttnArgs {
   hipStream_t stream;
   KvWrite kvw;      // slots == nullptr: no fused KV write
   bool own_tables;  // groups whose rows keep their own tables (paged_decode_shared_kernel)
+  const int32_t *plan;  // group plan (paged_decode_planned_kernel), or nullptr
+  int64_t plan_stride, plan_slots;
+  bool q_vec;  // query rows 16-byte aligned
 };
 
 // fp32 caches: VALU kernel over the logical V layout, G query rows per group.
@@ -391,8 +394,31 @@ constexpr int MFMA_STAGE_BLOCKS = 2;
 // steps: 3 and 4 blocks per stage were no faster and cost occupancy).
 constexpr int SHARED_STAGE_BLOCKS = 2;
 
+// Stage size of the planned group kernel: every wave requests this many blocks per
+// round trip.
+constexpr int PLANNED_STAGE_BLOCKS = 4;
+
+template <int DT, int D, int NW>
+static int launch_planned(const AttnArgs &a) {
+  const dim3 grid((unsigned)(a.plan_slots * a.H));
+  if (a.kvw.slots)
+    paged_decode_planned_kernel<DT, D, NW, PLANNED_STAGE_BLOCKS, true>
+        <<<grid, dim3(NW * 64), 0, a.stream>>>(
+        (const uint16_t *)a.q, a.q_st, a.q_sh, a.q_vec, (const uint16_t *)a.kc,
+        (const uint16_t *)a.vc, (uint16_t *)a.out, a.seq_lens, a.plan, a.plan_stride,
+        a.plan_slots, a.max_blocks, a.num_rows, a.H, a.num_blocks, a.scale_log2, a.kvw);
+  else
+    paged_decode_planned_kernel<DT, D, NW, PLANNED_STAGE_BLOCKS, false>
+        <<<grid, dim3(NW * 64), 0, a.stream>>>(
+        (const uint16_t *)a.q, a.q_st, a.q_sh, a.q_vec, (const uint16_t *)a.kc,
+        (const uint16_t *)a.vc, (uint16_t *)a.out, a.seq_lens, a.plan, a.plan_stride,
+        a.plan_slots, a.max_blocks, a.num_rows, a.H, a.num_blocks, a.scale_log2, a.kvw);
+  return launch_status("attention_with_kv_cache");
+}
+
 template <int DT, int D, int NW>
 static int launch_mfma(const AttnArgs &a) {
+  if (a.plan) return launch_planned<DT, D, NW>(a);
   const dim3 grid((unsigned)(a.num_groups * a.H));
   if (a.own_tables) {
     if (a.kvw.slots)
@@ -529,6 +555,34 @@ extern "C" int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, 
   meta->waves_per_workgroup = nw;
   meta->max_group_size = max_group_size;
   meta->group_tables = group_tables;
+  meta->group_plan = nullptr;
+  meta->group_plan_stride = 0;
+  meta->group_plan_slots = 0;
+  return VFL_OK;
+}
+
+extern "C" int64_t vfl_group_plan_stride(int max_group_size, int64_t max_blocks_per_seq) {
+  return group_plan_stride(max_group_size, max_blocks_per_seq);
+}
+
+extern "C" int vfl_build_group_plan(const int32_t *block_table, int64_t block_table_stride,
+                                    int max_blocks_per_seq, const int32_t *seq_lens,
+                                    int64_t num_rows, const int32_t *group_start,
+                                    const int32_t *group_order, int64_t num_groups,
+                                    int block_size, int64_t num_blocks, int32_t *plan,
+                                    int64_t num_slots, int64_t stride) {
+  clear_error();
+  if (!plan) {
+    set_error("build_group_plan: plan is NULL");
+    return VFL_E_INVALID;
+  }
+  const char *why = nullptr;
+  if (build_group_plan(block_table, block_table_stride, max_blocks_per_seq, seq_lens, num_rows,
+                       group_start, group_order, num_groups, block_size, num_blocks, plan,
+                       num_slots, stride, &why) != 0) {
+    set_error("build_group_plan: %s", why);
+    return VFL_E_INVALID;
+  }
   return VFL_OK;
 }
 
@@ -616,6 +670,25 @@ static int attention_impl(const void *query, int64_t query_stride_token,
   a.stream = (hipStream_t)stream;
   a.kvw = kvw;
   a.own_tables = group_start != nullptr && meta->group_tables == VFL_GROUP_OWN_TABLES;
+  a.plan = nullptr;
+  a.plan_stride = a.plan_slots = 0;
+  a.q_vec = (uintptr_t)query % 16 == 0 && query_stride_token % 8 == 0 &&
+            query_stride_head % 8 == 0;
+  if (meta->group_plan != nullptr && a.own_tables && dtype != VFL_FLOAT32) {
+    if ((uintptr_t)meta->group_plan % 16 != 0 || meta->group_plan_stride < PLAN_HEADER ||
+        meta->group_plan_stride % 4 != 0 || meta->group_plan_slots < num_groups ||
+        meta->group_plan_slots * num_heads > 2147483647LL ||
+        meta->max_group_size > PLAN_MAX_ROWS) {
+      set_error("%s: group plan of %lld slots x %lld words (16-byte aligned, stride a "
+                "multiple of 4, at least num_groups %lld slots, groups of <= %d rows)",
+                who, (long long)meta->group_plan_slots, (long long)meta->group_plan_stride,
+                (long long)num_groups, PLAN_MAX_ROWS);
+      return VFL_E_INVALID;
+    }
+    a.plan = meta->group_plan;
+    a.plan_stride = meta->group_plan_stride;
+    a.plan_slots = meta->group_plan_slots;
+  }
   if (a.own_tables && dtype == VFL_FLOAT32) {
     // The VALU kernel reads one table per group; with rows keeping their own tables
     // every row is its own group instead (same results: grouping is only a sharing

@@ -158,6 +158,74 @@ def reshape_and_cache(
 
 
 @dataclass(eq=False)
+class GroupPlan:
+    """A decode step's schedule of own-table row groups (``build_group_plan``): per
+    dispatch slot, a group's first row and row count and, position by position, the
+    distinct block ids its rows read with the rows that read each.  Made on the host
+    from the step's block tables once; every layer's self-attention launch reads it
+    (from the device copy) instead of walking the tables.
+
+    ``words``: int32 [4 + slots * stride]; ``max_blocks``: the block-table width it was
+    made for.
+    """
+
+    words: torch.Tensor
+    stride: int
+    slots: int
+    max_blocks: int
+
+    def to(self, device, non_blocking: bool = False) -> "GroupPlan":
+        return GroupPlan(self.words.to(device, non_blocking=non_blocking), self.stride,
+                         self.slots, self.max_blocks)
+
+
+def group_plan_stride(max_group_size: int, max_blocks: int) -> int:
+    """int32 words of one slot of a group plan (``vfl_group_plan_stride``)."""
+    stride = int(lib.vfl_group_plan_stride(int(max_group_size), int(max_blocks)))
+    if stride <= 0:
+        raise ValueError(f"no group plan for groups of {max_group_size} rows over tables "
+                         f"{max_blocks} wide (at most {MAX_GROUP_SIZE} rows, 65536 blocks)")
+    return stride
+
+
+def build_group_plan(block_table: torch.Tensor, seq_lens: torch.Tensor,
+                     group_start: torch.Tensor, *, group_order: torch.Tensor | None = None,
+                     num_slots: int | None = None, max_group_size: int = MAX_GROUP_SIZE,
+                     block_size: int = 16, num_blocks: int | None = None,
+                     out: torch.Tensor | None = None) -> GroupPlan:
+    """Group plan of one step from host (CPU int32) tensors: the block table
+    [rows, width], seq_lens [rows], group_start [groups + 1] and the optional dispatch
+    order [groups] of the self-attention call it is for (``vfl_build_group_plan``).
+    ``num_slots`` (default: the group count) sizes it for a launch padded to more
+    groups; ``out`` reuses a CPU int32 buffer (pinned, say) of at least the size."""
+    for name, t in (("block_table", block_table), ("seq_lens", seq_lens),
+                    ("group_start", group_start)):
+        if t.device.type != "cpu" or t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous CPU int32 tensor")
+    if block_table.dim() != 2 or seq_lens.shape != (block_table.shape[0],):
+        raise ValueError("block_table must be [rows, width] and seq_lens [rows]")
+    num_groups = group_start.numel() - 1
+    if group_order is not None and (group_order.device.type != "cpu" or
+                                    group_order.dtype != torch.int32 or
+                                    group_order.shape != (num_groups,)):
+        raise ValueError(f"group_order must be a CPU int32 tensor [{num_groups}]")
+    slots = num_groups if num_slots is None else int(num_slots)
+    width = block_table.shape[1]
+    stride = group_plan_stride(max_group_size, width)
+    words = 4 + slots * stride
+    if out is None:
+        out = torch.empty(words, dtype=torch.int32)
+    elif out.device.type != "cpu" or out.dtype != torch.int32 or out.numel() < words:
+        raise ValueError(f"out must be a CPU int32 tensor of at least {words} words")
+    check(lib.vfl_build_group_plan(
+        block_table.data_ptr(), block_table.stride(0), width, seq_lens.data_ptr(),
+        block_table.shape[0], group_start.data_ptr(),
+        None if group_order is None else group_order.data_ptr(), num_groups, block_size,
+        (1 << 62) if num_blocks is None else int(num_blocks), out.data_ptr(), slots, stride))
+    return GroupPlan(out[:words], stride, slots, width)
+
+
+@dataclass(eq=False)
 class SchedulerMetadata:
     """Launch plan for ``attention_with_kv_cache``: the GPU stand-in for the opaque
     tensor ``vllm_cpu_attn.get_scheduler_metadata`` returns.
@@ -188,6 +256,9 @@ class SchedulerMetadata:
     # context position, in a block no other row reads (the block manager's
     # copy-on-write invariant); lets the self-attention op fuse the KV write.
     fuse_kv_write: bool = False
+    # Device copy of the step's group plan (own-table groups, 16-bit caches): the
+    # launch reads the groups' blocks from it instead of walking the tables.
+    group_plan: GroupPlan | None = None
     _plans: dict = field(default_factory=dict, repr=False)
 
     def plan(self, num_rows: int, max_blocks: int) -> SchedMeta:
@@ -214,6 +285,14 @@ class SchedulerMetadata:
                     ctypes.byref(meta),
                 )
             )
+            gp = self.group_plan
+            if gp is not None:
+                if gp.max_blocks != max_blocks:
+                    raise ValueError(f"the group plan was made for block tables {gp.max_blocks} "
+                                     f"wide, the call's table is {max_blocks} wide")
+                meta.group_plan = gp.words.data_ptr()
+                meta.group_plan_stride = gp.stride
+                meta.group_plan_slots = gp.slots
             self._plans[key] = meta
         return meta
 
@@ -274,12 +353,13 @@ def get_scheduler_metadata(
     waves_per_workgroup: int = 0,
     fuse_kv_write: bool = False,
     own_tables: bool = False,
+    group_plan: GroupPlan | None = None,
 ) -> SchedulerMetadata:
     """Counterpart of ``vllm_cpu_attn.get_scheduler_metadata`` (keyword names from
     vflorence/layers/attention.py:18-29 and vflorence/engine/model_runner.py:308-319).
 
     ``group_start``/``group_order``/``max_group_size``/``waves_per_workgroup``/
-    ``own_tables`` are this library's additions.  ``seq_lens``, ``query_start_loc``, ``causal`` and ``isa`` are
+    ``own_tables``/``group_plan`` are this library's additions.  ``seq_lens``, ``query_start_loc``, ``causal`` and ``isa`` are
     accepted for signature compatibility; the plan does not need them (callers that
     know the lengths on the host pass ``group_order`` instead).
     """
@@ -301,6 +381,15 @@ def get_scheduler_metadata(
     if group_order is not None:
         if group_order.dtype != torch.int32 or group_order.shape != (num_groups,):
             raise ValueError(f"group_order must be int32 [{num_groups}]")
+    if group_plan is not None:
+        if not own_tables or group_start is None:
+            raise ValueError("a group plan needs own_tables row groups (group_start)")
+        w = group_plan.words
+        if (w.device.type != "cuda" or w.dtype != torch.int32 or not w.is_contiguous()
+                or w.numel() < 4 + group_plan.slots * group_plan.stride
+                or group_plan.slots < num_groups):
+            raise ValueError("group_plan must be a device copy of build_group_plan's output "
+                             f"with at least {num_groups} slots")
     return SchedulerMetadata(
         num_heads=num_heads,
         head_dim=head_dim,
@@ -313,6 +402,7 @@ def get_scheduler_metadata(
         waves_per_workgroup=waves_per_workgroup,
         fuse_kv_write=fuse_kv_write,
         own_tables=own_tables,
+        group_plan=group_plan,
     )
 
 
