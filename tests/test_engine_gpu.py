@@ -403,3 +403,54 @@ def test_continuous_batching_stress_florence2_large_shape():
     assert max(sizes) <= 512 and len(sizes) > 50
     assert len(llm.runner._graphs) <= len(row_buckets(512))
     assert_clean(llm)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16])
+def test_beam_step_uploads_the_group_plan_of_its_tables(dtype):
+    """A beam-search step's beam groups run from the group plan the runner builds on the
+    host: the plan in HBM (its used part) equals build_group_plan over the step's
+    uploaded tables, lengths and group starts, and the self-attention metadata points at
+    it."""
+    from vflorence_amd import Request, SamplingParams, hip_attn
+    from vflorence_amd.utils.context import get_context, set_context
+
+    fx = fixtures()["small"]
+    llm = engine(fx["config"], fx["checksum"], max_num_seqs=24, dtype=dtype,
+                 max_decoder_len=32, max_encoder_len=128)
+    params = SamplingParams(**{**fx["cases"]["beam4_early"]["params"], "max_tokens": 20,
+                               "min_length": 21})
+    for p in fx["prompts"][:5]:
+        llm.add_request(Request(p), params)
+    runner, sched = llm.runner, llm.scheduler
+    with torch.inference_mode():
+        for _ in range(19):  # forks and copy-on-write have made tables diverge
+            llm.step()
+        batch = sched.schedule()
+        if batch.fresh:
+            runner._encode(batch.fresh)
+        runner._prepare(batch)
+        torch.cuda.synchronize()
+        ctx = get_context()
+        sm = ctx.self_metadata
+        assert sm.group_plan is not None and runner._step_grouped
+        buf = runner._buffers
+        padded = ctx.context_lens.shape[0]
+        gs = ctx.self_metadata.group_start.cpu()
+        groups = int(np.searchsorted(gs.numpy(), padded))
+        want = hip_attn.build_group_plan(
+            ctx.block_tables.cpu(), ctx.context_lens.cpu(), gs[: groups + 1], num_slots=buf.rows,
+            max_group_size=hip_attn.MAX_GROUP_SIZE, num_blocks=runner.config.num_blocks)
+        used = 4 + groups * want.stride
+        got = sm.group_plan.words[:used].cpu()
+        # compare header and the entries each slot holds (the rest of a slot is unused)
+        assert int(got[0]) == groups == int(want.words[0])
+        shared = 0
+        for s in range(groups):
+            a = got[4 + s * want.stride:]
+            b = want.words[4 + s * want.stride:]
+            n = int(b[2])
+            assert torch.equal(a[:4 + 2 * n], b[:4 + 2 * n]), s
+            shared += sum(bin(int(b[5 + 2 * e]) & 0xFF).count("1") > 1 for e in range(n))
+        assert shared > 0  # beams share prefix blocks
+        set_context()
+    llm.abort()

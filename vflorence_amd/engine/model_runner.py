@@ -39,6 +39,7 @@ from ..layers.logits_processor import LogitsProcessor
 from ..sampling_params import SamplingParams
 from ..utils.context import set_context
 from ..utils.loader import load_model
+from .._lib import check, lib
 
 logger = logging.getLogger(__name__)
 
@@ -49,7 +50,9 @@ class _StepBuffers:
     int32 word layout for ``rows`` sequences and tables ``width`` blocks wide:
     seven int64 vectors of ``rows`` (token ids, positions, slots, copy sources, copy
     destinations, lengths, row request ids), then int32 context lengths, dispatch
-    order, the row groups' starts (``rows + 1``) and the ``[rows, width]`` block tables.
+    order, the row groups' starts (``rows + 1``) and the ``[rows, width]`` block tables;
+    last, 16-byte aligned, the group plan of the beam groups (``rows`` slots).  A step
+    uploads the fixed part and the plan's used slots only.
     """
 
     I64 = ("input_ids", "positions", "slots", "copy_src", "copy_dst", "lengths",
@@ -57,7 +60,10 @@ class _StepBuffers:
 
     def __init__(self, rows: int, width: int, device):
         self.rows, self.width = rows, width
-        words = 2 * len(self.I64) * rows + 3 * rows + 1 + rows * width
+        fixed = 2 * len(self.I64) * rows + 3 * rows + 1 + rows * width
+        self.plan_offset = (fixed + 3) // 4 * 4
+        self.plan_stride = hip_attn.group_plan_stride(hip_attn.MAX_GROUP_SIZE, width)
+        words = self.plan_offset + 4 + rows * self.plan_stride
         self.host = torch.zeros(words, dtype=torch.int32, pin_memory=True)
         self.dev = torch.zeros(words, dtype=torch.int32, device=device)
         self.copied = torch.cuda.Event()
@@ -65,6 +71,7 @@ class _StepBuffers:
         self.h = self._views(self.host)
         self.d = self._views(self.dev)
         self.np = {k: v.numpy() for k, v in self.h.items()}
+        self.device_plan = hip_attn.GroupPlan(self.d["plan"], self.plan_stride, rows, width)
 
     def _views(self, buf):
         r, w = self.rows, self.width
@@ -75,10 +82,24 @@ class _StepBuffers:
         out["order"] = buf[base + r: base + 2 * r]
         out["group_start"] = buf[base + 2 * r: base + 3 * r + 1]
         out["tables"] = buf[base + 3 * r + 1: base + 3 * r + 1 + r * w].view(r, w)
+        out["plan"] = buf[self.plan_offset:]
         return out
 
-    def upload(self) -> None:
-        self.dev.copy_(self.host, non_blocking=True)
+    def build_plan(self, padded: int, num_blocks: int, block_size: int) -> None:
+        """The beam groups' plan for this step's ``padded`` rows, from the packed tables,
+        lengths and group starts (slots = groups in row order, then empty ones)."""
+        gs = self.np["group_start"]
+        groups = int(np.searchsorted(gs[: padded + 1], padded))
+        h = self.h
+        check(lib.vfl_build_group_plan(
+            h["tables"].data_ptr(), self.width, self.width, h["context_lens"].data_ptr(),
+            padded, h["group_start"].data_ptr(), None, groups, block_size, num_blocks,
+            h["plan"].data_ptr(), self.rows, self.plan_stride))
+        self._plan_words = 4 + groups * self.plan_stride
+
+    def upload(self, grouped: bool = False) -> None:
+        words = self.plan_offset + (self._plan_words if grouped else 0)
+        self.dev[:words].copy_(self.host[:words], non_blocking=True)
         self.copied.record()
 
 
@@ -273,7 +294,9 @@ class ModelRunner:
         # self-attention runs as row groups that read each shared block once; the group
         # list is padded with empty groups so one launch shape serves every n-row batch.
         grouped = core.pack(padded, buf.width, hip_attn.MAX_GROUP_SIZE, h)
-        buf.upload()
+        if grouped:
+            buf.build_plan(padded, self.config.num_blocks, self.block_size)
+        buf.upload(grouped)
         d = buf.d
         if num_pairs:  # copy-on-write first: this step writes into the now-private blocks
             src, dst = h["copy_src"][:num_pairs], h["copy_dst"][:num_pairs]
@@ -287,10 +310,11 @@ class ModelRunner:
             common = dict(num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
                           head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
                           fuse_kv_write=True)
-            if grouped:
+            if grouped:  # the groups' blocks come from the step's plan
                 self_metadata = hip_attn.get_scheduler_metadata(
                     group_start=d["group_start"][: padded + 1],
-                    max_group_size=hip_attn.MAX_GROUP_SIZE, own_tables=True, **common)
+                    max_group_size=hip_attn.MAX_GROUP_SIZE, own_tables=True,
+                    group_plan=buf.device_plan, **common)
             else:  # one row per workgroup, longest context first
                 self_metadata = hip_attn.get_scheduler_metadata(
                     group_order=d["order"][:padded], **common)
