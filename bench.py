@@ -455,7 +455,8 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_cross_attention_ba
 def counter_pass(torch, wl, reps: int):
     """What a byte-counter pass measures: the cross-attention launches over the 12 layers'
     pools (``reps`` rounds); the last decode step's fused self-attention over the 12 layers,
-    with beam groups and with one row per workgroup; then two plain copies of COPY_BYTES
+    with beam groups read from the step's group plan, with beam groups walking the block
+    tables, and with one row per workgroup; then two plain copies of COPY_BYTES
     each (a device-to-device memcpy and an elementwise negation), whose counter readings
     calibrate the counters against a known byte count."""
     from vflorence_amd import workloads
@@ -482,10 +483,16 @@ def counter_pass(torch, wl, reps: int):
     slots = torch.tensor(plan.slot_mapping, dtype=torch.int64, device=dev)
     common = dict(num_reqs=rows, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS,
                   head_dim=HEAD_DIM, dtype=torch.bfloat16, block_size=BLOCK, fuse_kv_write=True)
+    starts_h = torch.arange(0, rows + 1, BEAMS, dtype=torch.int32)
+    gplan = hip_attn.build_group_plan(
+        tables.cpu(), lens.cpu(), starts_h, max_group_size=BEAMS, block_size=BLOCK,
+        num_blocks=wl["layers"][0].self_attn.k_cache.shape[0]).to(dev)
     plans = {
+        "planned": hip_attn.get_scheduler_metadata(
+            group_start=starts_h.to(dev), max_group_size=BEAMS, own_tables=True,
+            group_plan=gplan, **common),
         "grouped": hip_attn.get_scheduler_metadata(
-            group_start=torch.arange(0, rows + 1, BEAMS, dtype=torch.int32, device=dev),
-            max_group_size=BEAMS, own_tables=True, **common),
+            group_start=starts_h.to(dev), max_group_size=BEAMS, own_tables=True, **common),
         "rows": hip_attn.get_scheduler_metadata(
             group_order=torch.tensor(hip_attn.longest_first(plan.context_lens),
                                      dtype=torch.int32, device=dev), **common),
@@ -499,7 +506,8 @@ def counter_pass(torch, wl, reps: int):
                 q, k, v, layer.self_attn.k_cache, layer.self_attn.v_cache, out, lens, slots,
                 scale=HEAD_DIM**-0.5, block_table=tables, scheduler_metadata=sm)
         torch.cuda.synchronize()
-    self_bytes = {"grouped": step_bytes(plan, wl["enc"], grouped=True)[1],
+    grouped_bytes = step_bytes(plan, wl["enc"], grouped=True)[1]
+    self_bytes = {"planned": grouped_bytes, "grouped": grouped_bytes,
                   "rows": step_bytes(plan, wl["enc"], grouped=False)[1]}
     subjects = extra_counter_subjects(torch, wl)
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
