@@ -247,7 +247,7 @@ def schedule_order(n: int, steps: int = DECODE_STEPS) -> list[int]:
 
 
 KERNEL_NAMES = {  # kernel name prefixes of the decode step's launches
-    "cross": "void vfl::paged_decode_mfma_kernel<1, 64, 4, 2, false>",
+    "cross": "void vfl::paged_decode_mfma_kernel<1, 64, 8, 2, false>",
     "self": "void vfl::paged_decode_planned_kernel<1, 64, 2, 4, true>",
     "self_walk": "void vfl::paged_decode_shared_kernel<1, 64, 2, 2, true>",
     "self_rows": "void vfl::paged_decode_mfma_kernel<1, 64, 2, 2, true>",
@@ -405,6 +405,47 @@ def cross_kernel_timing(torch, wl, reps: int):
     return avg, bytes_per
 
 
+COW_PLANNED_PAIRS = 115  # about 10% of the blocks a 64 x 4-beam step holds at mid schedule
+
+
+def cow_planned_volume_timing(torch, wl, reps: int, seed: int):
+    """Copy-on-write at the planned volume of 115 pairs per step over the 24 self pools
+    (12 layers x K, V): 115 x 24 x 2 x 32 KiB = 181 MB moved per launch.  Three disjoint
+    pair sets in rotation (543 MB, more than the last-level cache holds), back to back.
+    Returns (average seconds per launch, algorithmic bytes per launch)."""
+    import numpy as np
+
+    from vflorence_amd import hip_attn
+
+    caches = [c for L in wl["layers"] for c in (L.self_attn.k_cache, L.self_attn.v_cache)]
+    ptrs = hip_attn.cache_pointer_table(caches)
+    nb = caches[0].shape[0]
+    rng = np.random.default_rng(seed + 77)
+    blocks = rng.permutation(nb)[: 6 * COW_PLANNED_PAIRS]
+    dev = caches[0].device
+    sets = []
+    for i in range(3):
+        chunk = blocks[2 * i * COW_PLANNED_PAIRS: 2 * (i + 1) * COW_PLANNED_PAIRS]
+        src = torch.tensor(chunk[:COW_PLANNED_PAIRS], dtype=torch.int64, device=dev)
+        dst = torch.tensor(chunk[COW_PLANNED_PAIRS:], dtype=torch.int64, device=dev)
+        sets.append((src, dst))
+    from vflorence_amd._lib import check, lib
+
+    block_bytes = caches[0][0].numel() * caches[0].element_size()
+    hip_attn.copy_blocks(caches, sets[0][0], sets[0][1], ptrs, staged=False)  # validated once
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    args = [(ptrs.data_ptr(), len(caches), src.data_ptr(), dst.data_ptr(), COW_PLANNED_PAIRS,
+             block_bytes, nb, None, stream) for src, dst in sets]
+    fn = lib.vfl_copy_blocks
+
+    def launch_three():
+        for a in args:
+            check(fn(*a))
+
+    avg = time_kernel(torch, launch_three, reps) / 3
+    return avg, COW_PLANNED_PAIRS * len(caches) * 2 * block_bytes
+
+
 def self_op_timing(torch, reps: int, seed: int):
     """256 ragged sequences (ctx U[1,1024]) over a random permutation of a 20k-block pool;
     three independent pools in rotation.  Returns (attention kernel avg s, bytes of the
@@ -520,7 +561,7 @@ def counter_pass(torch, wl, reps: int):
     c_bytes = workloads.cross_attention_bytes(wl["enc"], REQUESTS * BEAMS, NUM_HEADS, HEAD_DIM,
                                               2, BLOCK)
     print(json.dumps({"counter_pass": True, "cross_launches": NUM_LAYERS * (reps + 1),
-                      "cross_grid_threads": REQUESTS * NUM_HEADS * 64 * 4,
+                      "cross_grid_threads": REQUESTS * NUM_HEADS * 64 * 8,
                       "cross_algorithmic_bytes": int(c_bytes),
                       "self_step": len(wl["plans"]) - 1,
                       "self_launches_each": NUM_LAYERS,
@@ -633,6 +674,7 @@ GATHER_VARIANTS = {
     1: "(group, head) slices, head-major ids, 1024 x 4 waves",
     2: "(group, 4 heads): 8 KiB of a block read together, 256 x 16 waves",
     3: "(group, 4 heads): each wave reads 8 KiB per block, 256 x 4 waves",
+    4: "(group, head) slices as 0, non-temporal loads (the attention kernels' hint)",
 }
 
 
@@ -972,6 +1014,8 @@ def main():
     print("[bench] timing the cross-attention kernel back to back", flush=True)
     c_avg, _ = cross_kernel_timing(torch, wl, args.kernel_reps)
     c_gbps = c_bytes / c_avg / 1e9
+    print("[bench] copy-on-write at 115 pairs per step", flush=True)
+    cow_avg, cow_bytes = cow_planned_volume_timing(torch, wl, args.kernel_reps, args.seed)
     if in_step is not None and sum(in_step["cross"]) / len(in_step["cross"]) < 0.5 * c_avg:
         # another profiler (rocprofv3) owns the device timestamps: torch.profiler's are void
         print("[bench] in-step kernel durations unusable (another profiler is attached)",
@@ -1046,7 +1090,7 @@ def main():
         "wall_s_timed": round(wall, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": ("paged_decode_mfma_kernel<bf16, D=64, 4 waves, 2 blocks/stage> "
+            "kernel": ("paged_decode_mfma_kernel<bf16, D=64, 8 waves, 2 blocks/stage> "
                        "(cross-attention, 4 beams per group)"),
             "achieved": round(c_step_gbps, 1),
             "peak": HBM_PEAK_GBPS,
@@ -1083,6 +1127,14 @@ def main():
                 "gbps": (round(sum(step_bytes(p, wl_enc, grouped=grouped)[3]
                                    for p in wl_plans if p.copies) / sum(cow) / 1e9, 1)
                          if cow else None),
+            },
+            "copy_on_write_115_pairs": {
+                "pairs": COW_PLANNED_PAIRS,
+                "pools": 2 * NUM_LAYERS,
+                "bytes": int(cow_bytes),
+                "back_to_back_us": round(cow_avg * 1e6, 2),
+                "gbps": round(cow_bytes / cow_avg / 1e9, 1),
+                "frac": round(cow_bytes / cow_avg / 1e9 / HBM_PEAK_GBPS, 4),
             },
             "decoder_linear_256_rows_cold_weights": linear,
         },

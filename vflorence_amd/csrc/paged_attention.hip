@@ -486,13 +486,14 @@ static bool kernel_exists(int dtype, int block_size, int head_dim) {
 constexpr int MAX_GROUP = 8;
 constexpr int MAX_WAVES = 8;
 
-// Waves per (group, head) workgroup.  Measured on MI355X (bf16, head_dim 64): four
-// waves is best both for 256 ragged self-attention rows (4096 workgroups) and for
-// 64 x 4-beam cross-attention (1024 workgroups); eight only pays when there are
-// few workgroups to spread over 256 CUs.  Never more waves than blocks.
+// Waves per (group, head) workgroup.  Measured on MI355X (bf16, head_dim 64, K/V pages
+// loaded non-temporally): 64 x 4-beam cross-attention (1024 workgroups) runs 30.3 us
+// with eight waves, 32.8-33.6 with four, 36.1 with two; 256 ragged self-attention rows
+// (4096 workgroups) run within noise of each other with two, four or eight (92.6-97.1
+// us).  So eight below 2048 workgroups, four above.  Never more waves than blocks.
 static int default_waves(int64_t num_groups, int num_heads, int64_t max_blocks) {
   const int64_t wgs = num_groups * num_heads;
-  int nw = wgs >= 512 ? 4 : 8;
+  int nw = wgs >= 2048 ? 4 : 8;
   while (nw > 1 && nw / 2 >= max_blocks) nw /= 2;
   return nw;
 }
