@@ -76,7 +76,12 @@ int vfl_version(void);
  * Replaces vllm_cpu_attn.get_isa(dtype, block_size, head_dim)
  * (vflorence/engine/model_runner.py:38).  There is one code path, so this returns
  * the GPU target the library was built for ("gfx950"), or NULL when the
- * (dtype, block_size, head_dim) combination has no kernel.
+ * (dtype, block_size, head_dim) combination has no kernel.  Kernels exist for fp32,
+ * bf16 and fp16, block size 16, and the reference's head sizes (32, 48, 64, 80, 96,
+ * 112, 128, 160, 192, 224, 256, 512: vflorence/layers/attention.py:6).  Row groups
+ * keeping their own tables, group plans and the fused KV write have kernels for 16-bit
+ * caches of head size 64 and 128; other calls give the same results through the
+ * one-row kernels (and a separate KV write).
  */
 const char *vfl_get_isa(int dtype, int block_size, int head_dim);
 
@@ -230,7 +235,8 @@ int vfl_attention_with_kv_cache(const void *query, int64_t query_stride_token,
  * table, or a slot that no row of this call attends to; and the block holding a
  * row's new token is read by no other row.  Then the result -- cache contents and
  * out -- equals reshape_and_cache followed by attention_with_kv_cache.  Callers that
- * cannot vouch for it use those two entry points.  fp32 caches run the two steps.
+ * cannot vouch for it use those two entry points.  fp32 caches, and head sizes other
+ * than 64 and 128, run the two steps.
  *
  * key / value: [num_rows][num_heads][head_dim] with token / head strides in
  * elements (the strided views of a fused qkv projection).  Other arguments as for

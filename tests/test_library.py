@@ -55,7 +55,13 @@ def test_version_and_isa():
     with pytest.raises(ValueError):
         hip_attn.get_isa(torch.bfloat16, 32, 64)
     with pytest.raises(ValueError):
-        hip_attn.get_isa(torch.bfloat16, 16, 80)
+        hip_attn.get_isa(torch.bfloat16, 16, 72)
+    # the reference's head sizes (vflorence/layers/attention.py:6), every dtype
+    for d in (32, 48, 64, 80, 96, 112, 128, 160, 192, 224, 256, 512):
+        for dt in (torch.float32, torch.bfloat16, torch.float16):
+            assert hip_attn.get_isa(dt, 16, d) == "gfx950", (dt, d)
+        rc, m = plan(8, 8, 4, d, 20)
+        assert rc == 0 and m.head_dim == d
 
 
 def plan(rows, groups, heads, dim, max_blocks, gmax=1, nw=0, dtype=1, tables=0):
@@ -92,7 +98,8 @@ def test_scheduler_metadata_plan():
     [
         dict(gmax=9),  # beams per group above the compiled maximum
         dict(gmax=0),
-        dict(dim=80),  # no kernel
+        dict(dim=72),  # not one of the reference's head sizes: no kernel
+        dict(dim=1024),
         dict(groups=300),  # more groups than rows
         dict(nw=3),  # not a power of two
         dict(nw=16),
@@ -125,7 +132,7 @@ def test_attention_validates_before_launch():
     # table narrower than the plan
     assert call(stride=4) == -1
     # unsupported head size
-    assert call(dim=96) == -2
+    assert call(dim=72) == -2
     # grouped counts without a group table
     rc2, meta2 = plan(4, 2, 16, 64, 8)
     assert call(groups=2, meta_=meta2) == -1

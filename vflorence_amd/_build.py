@@ -15,7 +15,8 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = ("kv_cache.hip", "paged_attention.hip", "decoder_ops.hip", "decode_linear.hip")
+SOURCES = ("kv_cache.hip", "paged_attention.hip", "attention_dims.hip", "decoder_ops.hip",
+           "decode_linear.hip")
 OUTPUT = os.path.join(HERE, "libvflorence_amd.so")
 ARCH = os.environ.get("VFL_OFFLOAD_ARCH", "gfx950")
 
@@ -81,19 +82,40 @@ def build_probe_library(verbose: bool = False) -> str:
 
 
 def build_library(verbose: bool = False) -> str:
-    """Compile every HIP source into OUTPUT; always recompiles."""
+    """Compile every HIP source into OUTPUT; always recompiles.  The sources compile to
+    objects in parallel (one hipcc per file), then link into the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    # The host pass does not know the gfx950 feature flag; that warning is expected.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+
+    def compile_one(src: str):
+        obj = os.path.join(objdir, os.path.splitext(os.path.basename(src))[0] + ".o")
+        cmd = [hipcc(), *flags, "-c", os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if noise not in ln]
+        return obj, proc.returncode, msgs
+
+    workers = max(1, min(len(SOURCES), os.cpu_count() or 1))
+    with ThreadPoolExecutor(workers) as pool:
+        results = list(pool.map(compile_one, SOURCES))
+    for _, rc, msgs in results:
+        if rc != 0:
+            raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
+        if verbose and msgs:
+            print("\n".join(msgs), flush=True)
     tmp = OUTPUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, *[os.path.join(CSRC, s) for s in SOURCES], "-o", tmp]
+    cmd = [hipcc(), *HIPCC_FLAGS, *[obj for obj, _, _ in results], "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    # The host pass does not know the gfx950 feature flag; that warning is expected.
-    noise = "'-packed-fp32-ops' is not a recognized feature"
-    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if noise not in ln]
     if proc.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
-    if verbose and msgs:
-        print("\n".join(msgs), flush=True)
+        raise RuntimeError("hipcc link failed:\n" + proc.stdout + proc.stderr)
     os.replace(tmp, OUTPUT)
     return OUTPUT
 

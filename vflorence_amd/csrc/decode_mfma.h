@@ -26,10 +26,19 @@
 
 namespace vfl {
 
-// Loads of one block for this lane: D/32 16-byte K chunks (token `col`, dims
+// 32-wide K chunks of a head of size D (a multiple of 16): the last one is half empty
+// when D is an odd multiple of 16, its dims past D zero in both the query and K operand.
+template <int D> constexpr int k_chunks() { return (D + 31) / 32; }
+// Whether lane row group rg's 8 dims of K chunk kk lie inside the head.
+template <int D> __device__ __forceinline__ bool k_chunk_ok(int kk, int rg) {
+  if constexpr (D % 32 == 0) return true;
+  else return 32 * kk + 8 * rg < D;
+}
+
+// Loads of one block for this lane: k_chunks<D>() 16-byte K chunks (token `col`, dims
 // 32*kk + 8*rg ..) and D/16 8-byte V chunks (dim 16*c + col, tokens 4*rg .. 4*rg+3).
 template <int D> struct MfmaBlock {
-  uint4 k[D / 32];
+  uint4 k[k_chunks<D>()];
   uint2 v[D / 16];
 };
 
@@ -65,10 +74,11 @@ __device__ __forceinline__ void mfma_load_block(const uint16_t *__restrict__ kc,
                                                 int64_t block_elems, int head_off, int k_lane,
                                                 int v_lane, MfmaBlock<D> &blk) {
   const int64_t base = (ok ? (int64_t)id : 0) * block_elems + head_off;
+  const int rg = (int)(__lane_id() >> 4);
 #pragma unroll
-  for (int kk = 0; kk < D / 32; ++kk) {
+  for (int kk = 0; kk < k_chunks<D>(); ++kk) {
     blk.k[kk] = make_uint4(0, 0, 0, 0);
-    if (ok) blk.k[kk] = load_stream16(kc + base + k_lane + 32 * kk);
+    if (ok && k_chunk_ok<D>(kk, rg)) blk.k[kk] = load_stream16(kc + base + k_lane + 32 * kk);
   }
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
@@ -80,14 +90,14 @@ __device__ __forceinline__ void mfma_load_block(const uint16_t *__restrict__ kc,
 // Fold one block into the lane's state.  tok0 is the block's first token index;
 // MASKED handles tokens at or past Lc and invalid block ids (ok == false).
 template <int DT, int D, bool MASKED>
-__device__ __forceinline__ void mfma_consume(const uint4 (&qop)[D / 32], MfmaBlock<D> &blk,
+__device__ __forceinline__ void mfma_consume(const uint4 (&qop)[k_chunks<D>()], MfmaBlock<D> &blk,
                                              bool ok, int tok0, int Lc, int rg,
                                              float scale_log2, float &m, float &l,
                                              floatx4_t (&acc)[D / 16]) {
   using Ops = Mfma<DT>;
   floatx4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int kk = 0; kk < D / 32; ++kk) s = Ops::qk(blk.k[kk], qop[kk], s);
+  for (int kk = 0; kk < k_chunks<D>(); ++kk) s = Ops::qk(blk.k[kk], qop[kk], s);
   float sv[4];
   bool valid[4];
 #pragma unroll
@@ -150,14 +160,15 @@ template <int D>
 __device__ __forceinline__ void write_new_token(const uint16_t *kc, const uint16_t *vc, int id,
                                                 int64_t block_elems, int head_off, int k_lane,
                                                 int v_lane, int col, int rg, int t_new,
-                                                const uint4 (&newk)[D / 32],
+                                                const uint4 (&newk)[k_chunks<D>()],
                                                 const uint32_t (&newv)[D / 16],
                                                 MfmaBlock<D> &blk) {
   uint16_t *tile_k = const_cast<uint16_t *>(kc) + (int64_t)id * block_elems + head_off;
   uint16_t *tile_v = const_cast<uint16_t *>(vc) + (int64_t)id * block_elems + head_off;
   if (col == t_new) {
 #pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) {
+    for (int kk = 0; kk < k_chunks<D>(); ++kk) {
+      if (!k_chunk_ok<D>(kk, rg)) continue;
       blk.k[kk] = newk[kk];
       *reinterpret_cast<uint4 *>(tile_k + k_lane + 32 * kk) = newk[kk];
     }
@@ -191,9 +202,10 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
     int64_t num_rows, int64_t num_groups, int H, int64_t num_blocks, float scale_log2,
     KvWrite kvw) {
   constexpr int BS = 16;
-  constexpr int KCH = D / 32;
+  constexpr int KCH = k_chunks<D>();
   constexpr int VCH = D / 16;
   constexpr int MAXG = 16;  // query rows per group held in the tile columns
+  static_assert(D % 16 == 0, "head size must be a multiple of 16");
   // Cross-wave merge buffers: [wave][dim][beam] (+1 column of padding) and (m, l).
   __shared__ float s_acc[NW > 1 ? NW : 1][D][MAXG + 1];
   __shared__ float s_ml[NW > 1 ? NW : 1][2][MAXG];
@@ -263,7 +275,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
 #pragma unroll
   for (int kk = 0; kk < KCH; ++kk) {
     qop[kk] = make_uint4(0, 0, 0, 0);
-    if (col < nrows)
+    if (col < nrows && k_chunk_ok<D>(kk, rg))
       qop[kk] = load16_unaligned<DT>(q + (row0 + col) * q_st + h * q_sh + 32 * kk + 8 * rg);
   }
   floatx4_t acc[VCH];
@@ -296,7 +308,10 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
       const uint16_t *ks = kvw.k + row0 * kvw.k_st + h * kvw.k_sh;
       const uint16_t *vs = kvw.v + row0 * kvw.v_st + h * kvw.v_sh;
 #pragma unroll
-      for (int kk = 0; kk < KCH; ++kk) newk[kk] = load16_unaligned<DT>(ks + 32 * kk + 8 * rg);
+      for (int kk = 0; kk < KCH; ++kk) {
+        newk[kk] = make_uint4(0, 0, 0, 0);
+        if (k_chunk_ok<D>(kk, rg)) newk[kk] = load16_unaligned<DT>(ks + 32 * kk + 8 * rg);
+      }
 #pragma unroll
       for (int c = 0; c < VCH; ++c) newv[c] = vs[16 * c + col];
     }

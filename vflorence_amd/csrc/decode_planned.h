@@ -74,6 +74,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
     int64_t num_rows, int H, int64_t num_blocks, float scale_log2, KvWrite kvw) {
   constexpr int BS = 16;
   constexpr int KCH = D / 32;
+  static_assert(D % 32 == 0, "built for head sizes 64 and 128");
   constexpr int VCH = D / 16;
   constexpr int MAXG = 16;
   constexpr int NCH = D / 32;  // 16-byte chunks per lane of a new K or V row

@@ -190,6 +190,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_shared_kernel(
     KvWrite kvw) {
   constexpr int BS = 16;
   constexpr int KCH = D / 32;
+  static_assert(D % 32 == 0, "built for head sizes 64 and 128");
   constexpr int VCH = D / 16;
   constexpr int MAXG = 16;
   __shared__ float s_acc[NW > 1 ? NW : 1][D][MAXG + 1];

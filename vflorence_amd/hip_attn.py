@@ -25,9 +25,13 @@ _DTYPE_CODES = {
     torch.float16: _lib.VFL_FLOAT16,
 }
 
-# Head sizes with a compiled kernel (the reference accepts more, for its CPU ISAs:
-# vflorence/layers/attention.py:6).  BART and Florence-2 use 64.
-SUPPORTED_HEAD_DIMS = frozenset({64, 128})
+# Head sizes with a compiled kernel: the reference's list (vflorence/layers/attention.py:6).
+SUPPORTED_HEAD_DIMS = frozenset({32, 48, 64, 80, 96, 112, 128, 160, 192, 224, 256, 512})
+# Head sizes with every kernel built: beam groups keeping their own tables, the group
+# plan and the fused KV write (BART and Florence-2 use 64).  Other head sizes run one
+# row (or one shared-table group) per workgroup with the KV write as its own launch;
+# the entry points take the same arguments and fall back by themselves.
+NATIVE_HEAD_DIMS = frozenset({64, 128})
 SUPPORTED_BLOCK_SIZES = frozenset({16})
 MAX_GROUP_SIZE = 8
 # Waves per workgroup for the fused KV-write + self-attention launch (measured: two
