@@ -77,11 +77,12 @@ int vfl_version(void);
  * (vflorence/engine/model_runner.py:38).  There is one code path, so this returns
  * the GPU target the library was built for ("gfx950"), or NULL when the
  * (dtype, block_size, head_dim) combination has no kernel.  Kernels exist for fp32,
- * bf16 and fp16, block size 16, and the reference's head sizes (32, 48, 64, 80, 96,
- * 112, 128, 160, 192, 224, 256, 512: vflorence/layers/attention.py:6).  Row groups
- * keeping their own tables, group plans and the fused KV write have kernels for 16-bit
- * caches of head size 64 and 128; other calls give the same results through the
- * one-row kernels (and a separate KV write).
+ * bf16 and fp16, block sizes 16 and 32 (the reference's aarch64 and x86 sizes,
+ * vflorence/config.py:42), and the reference's head sizes (32, 48, 64, 80, 96, 112,
+ * 128, 160, 192, 224, 256, 512: vflorence/layers/attention.py:6).  Row groups keeping
+ * their own tables, group plans and the fused KV write have kernels for 16-bit caches
+ * of head size 64 and 128 in 16-token blocks; other calls give the same results
+ * through the one-row kernels (and a separate KV write).
  */
 const char *vfl_get_isa(int dtype, int block_size, int head_dim);
 

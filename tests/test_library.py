@@ -53,7 +53,10 @@ def test_version_and_isa():
     assert hip_attn.get_isa(torch.bfloat16, 16, 64) == "gfx950"
     assert hip_attn.get_isa(torch.float32, 16, 128) == "gfx950"
     with pytest.raises(ValueError):
-        hip_attn.get_isa(torch.bfloat16, 32, 64)
+        hip_attn.get_isa(torch.bfloat16, 24, 64)
+    # 32-token blocks: the reference's block size on x86 (vflorence/config.py:42)
+    assert hip_attn.get_isa(torch.bfloat16, 32, 64) == "gfx950"
+    assert hip_attn.get_isa(torch.float32, 32, 80) == "gfx950"
     with pytest.raises(ValueError):
         hip_attn.get_isa(torch.bfloat16, 16, 72)
     # the reference's head sizes (vflorence/layers/attention.py:6), every dtype
@@ -179,7 +182,7 @@ def test_reshape_and_copy_validate_before_launch():
                                      1, None) == 0
     # block sizes without an attention kernel are refused before anything launches
     # (the 16-bit V layout would land outside the block-head slice)
-    for bs in (8, 32, 18):
+    for bs in (8, 24, 18, 64):
         assert lib.vfl_reshape_and_cache(None, None, 0, 0, 0, 0, None, None, None, 4, 16, 64,
                                          bs, 10, 1, None) == -2
         assert b"block_size" in lib.vfl_last_error()
@@ -240,7 +243,7 @@ def test_cpu_tensors_are_rejected():
     x = torch.zeros(3, 2, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="no CPU path"):
         hip_attn.reshape_and_cache(x, x, k, k, torch.zeros(3, dtype=torch.int64))
-    # a pool of another block size is refused on the host, whatever the device
-    k32 = torch.zeros(4, 2, 32, 64, dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="block_size=32"):
-        hip_attn.reshape_and_cache(x, x, k32, k32, torch.zeros(3, dtype=torch.int64))
+    # a pool of a block size with no kernel is refused on the host, whatever the device
+    k24 = torch.zeros(4, 2, 24, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="block_size=24"):
+        hip_attn.reshape_and_cache(x, x, k24, k24, torch.zeros(3, dtype=torch.int64))

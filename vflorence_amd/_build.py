@@ -15,8 +15,8 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = ("kv_cache.hip", "paged_attention.hip", "attention_dims.hip", "decoder_ops.hip",
-           "decode_linear.hip")
+SOURCES = ("kv_cache.hip", "paged_attention.hip", "attention_dims.hip", "attention_block32.hip",
+           "decoder_ops.hip", "decode_linear.hip")
 OUTPUT = os.path.join(HERE, "libvflorence_amd.so")
 ARCH = os.environ.get("VFL_OFFLOAD_ARCH", "gfx950")
 

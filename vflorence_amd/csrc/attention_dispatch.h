@@ -27,6 +27,7 @@ struct AttnArgs {
   const int32_t *plan;  // group plan (paged_decode_planned_kernel), or nullptr
   int64_t plan_stride, plan_slots;
   bool q_vec;  // query rows 16-byte aligned
+  int bs_shift;  // pool blocks of 16 << bs_shift tokens
 };
 
 // Head sizes the reference's attention op accepts (vflorence/layers/attention.py:6).
@@ -44,14 +45,16 @@ inline bool head_dim_supported(int d) {
 // plan, the fused KV write): BART's and Florence-2's 64, and 128.
 inline bool head_dim_native(int d) { return d == 64 || d == 128; }
 
-// fp32 caches: VALU kernel over the logical V layout, G query rows per group.
-template <int D, int G, int NW>
+
+// fp32 caches: VALU kernel over the logical V layout, G query rows per group; pool
+// blocks of 16 << SHIFT tokens.
+template <int D, int G, int NW, int SHIFT = 0>
 int launch_valu(const AttnArgs &a) {
   constexpr int DT = VFL_FLOAT32;
   using T = typename Elem<DT>::T;
   constexpr int BS = 16;
   const dim3 grid((unsigned)(a.num_groups * a.H));
-  paged_decode_kernel<DT, D, BS, G, NW, stage_blocks<DT, D, G>(), stage_pipeline<G>()>
+  paged_decode_kernel<DT, D, BS, G, NW, stage_blocks<DT, D, G>(), stage_pipeline<G>(), SHIFT>
       <<<grid, dim3(NW * 64), 0, a.stream>>>(
       (const T *)a.q, a.q_st, a.q_sh, (const T *)a.kc, (const T *)a.vc, (T *)a.out, a.seq_lens,
       a.bt, a.bt_stride, a.max_blocks, a.group_start, a.group_order, a.num_rows, a.num_groups,
@@ -79,10 +82,10 @@ int valu_group(const AttnArgs &a, int gmax, int nw) {
 
 // bf16 / fp16 caches, one row or a group sharing one table per workgroup, no fused
 // KV write: the matrix-core kernel of decode_mfma.h.
-template <int DT, int D, int NW, int U>
+template <int DT, int D, int NW, int U, int SHIFT = 0>
 int launch_mfma_rows(const AttnArgs &a) {
   const dim3 grid((unsigned)(a.num_groups * a.H));
-  paged_decode_mfma_kernel<DT, D, NW, U, false><<<grid, dim3(NW * 64), 0, a.stream>>>(
+  paged_decode_mfma_kernel<DT, D, NW, U, false, SHIFT><<<grid, dim3(NW * 64), 0, a.stream>>>(
       (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
       (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
       a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw);
@@ -93,5 +96,9 @@ int launch_mfma_rows(const AttnArgs &a) {
 // shared-table group per workgroup, no fused KV write (the caller makes the separate
 // write first) and no own-table groups (every row its own group).
 int dispatch_other_head_dim(const AttnArgs &a, int dtype, int head_dim, int gmax, int nw);
+
+// Pools of 32-token blocks (attention_block32.hip): every head size on the one-row /
+// shared-table kernels, which read a block as two 16-token parts.
+int dispatch_block32(const AttnArgs &a, int dtype, int head_dim, int gmax, int nw);
 
 }  // namespace vfl

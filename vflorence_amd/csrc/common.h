@@ -36,9 +36,13 @@ template <> struct Elem<VFL_FLOAT16> {
 
 inline int elem_bytes(int dtype) { return dtype == VFL_FLOAT32 ? 4 : 2; }
 
-// Tokens per KV block: the only block size with attention kernels (the 16-bit V layout
-// interleaves tokens by four inside it).
-constexpr int KV_BLOCK_SIZE = 16;
+// Tokens per KV block: 16 (this build's pools) or the 32 the reference uses on x86
+// (vflorence/config.py:42); the attention kernels walk 16-token parts, 1 << shift per
+// block.  Any other size has no kernel (-1): the 16-bit V layout interleaves tokens by
+// four inside a block, so a size that is not a multiple of 16 would break the parts.
+inline int block_shift(int block_size) {
+  return block_size == 16 ? 0 : (block_size == 32 ? 1 : -1);
+}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));

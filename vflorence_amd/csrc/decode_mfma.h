@@ -193,7 +193,11 @@ __device__ __forceinline__ void write_new_token(const uint16_t *kc, const uint16
 // guarantees that a row's slot, when it is the cache position of the row's last
 // context token, lies in a block no other row reads; the write then needs no ordering
 // against other workgroups.  A slot elsewhere is still written, without substitution.
-template <int DT, int D, int NW, int U, bool FUSE>
+// SHIFT: pool blocks hold 16 << SHIFT tokens (0, or 1 for the reference's 32-token
+// blocks); the kernel walks 16-token chunks, chunk b being part b & mask of table entry
+// b >> SHIFT (the same offset, 16 * D elements per part, in K and in the
+// 4-token-interleaved V).
+template <int DT, int D, int NW, int U, bool FUSE, int SHIFT>
 __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
     const uint16_t *__restrict__ q, int64_t q_st, int64_t q_sh, const uint16_t *kc,
     const uint16_t *vc, uint16_t *__restrict__ out, const int32_t *__restrict__ seq_lens,
@@ -202,6 +206,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
     int64_t num_rows, int64_t num_groups, int H, int64_t num_blocks, float scale_log2,
     KvWrite kvw) {
   constexpr int BS = 16;
+  constexpr int bs_shift = SHIFT;
+  static_assert(!FUSE || SHIFT == 0, "the fused KV write is built for 16-token blocks");
   constexpr int KCH = k_chunks<D>();
   constexpr int VCH = D / 16;
   constexpr int MAXG = 16;  // query rows per group held in the tile columns
@@ -225,8 +231,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
   nrows = (int)min((int64_t)nrows, num_rows - row0);
   if (nrows <= 0) return;
   const int L = seq_lens[row0];
-  int nblk = L > 0 ? (L + BS - 1) / BS : 0;
-  nblk = min(nblk, max_blocks);
+  int nblk = L > 0 ? (L + BS - 1) / BS : 0;  // 16-token chunks
+  nblk = min(nblk, max_blocks << bs_shift);
   const int Lc = min(L, nblk * BS);
   const int col = lane & 15;  // query row (beam) of this lane's tile column
   const int rg = lane >> 4;   // row group: tokens 4*rg .. 4*rg+3 of a block
@@ -284,9 +290,14 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
   float m = NEG_INF_F, l = 0.f;
 
   WaveBlockIds ids;
-  ids.init(bt + (int64_t)row0 * bt_stride, b0, b1);
-  const int64_t block_elems = (int64_t)H * BS * D;
-  const int head_off = h * BS * D;
+  if constexpr (SHIFT == 0)
+    ids.init(bt + (int64_t)row0 * bt_stride, b0, b1);
+  else
+    ids.init(bt + (int64_t)row0 * bt_stride, b0 >> SHIFT,
+             b1 > b0 ? ((b1 - 1) >> SHIFT) + 1 : b0 >> SHIFT);
+  constexpr int part_mask = (1 << SHIFT) - 1;
+  const int64_t block_elems = (int64_t)H * (BS << bs_shift) * D;
+  const int head_off = h * (BS << bs_shift) * D;
   const int k_lane = col * D + 8 * rg;
   const int v_lane = (rg * D + col) * 4;  // vtile_index(4 * rg, col, D)
 
@@ -323,9 +334,10 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
     bool ok[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int id = ids.get(b + u);
+      const int id = ids.get((b + u) >> bs_shift);
       ok[u] = id >= 0 && id < num_blocks;
-      mfma_load_block<DT, D>(kc, vc, id, ok[u], block_elems, head_off, k_lane, v_lane, blk[u]);
+      mfma_load_block<DT, D>(kc, vc, id, ok[u], block_elems,
+                             head_off + ((b + u) & part_mask) * BS * D, k_lane, v_lane, blk[u]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -349,9 +361,10 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
   }
   for (; b < b_stop; ++b) {
     MfmaBlock<D> blk;
-    const int id = ids.get(b);
+    const int id = ids.get(b >> bs_shift);
     const bool ok = id >= 0 && id < num_blocks;
-    mfma_load_block<DT, D>(kc, vc, id, ok, block_elems, head_off, k_lane, v_lane, blk);
+    mfma_load_block<DT, D>(kc, vc, id, ok, block_elems, head_off + (b & part_mask) * BS * D,
+                           k_lane, v_lane, blk);
     mfma_consume<DT, D, true>(qop, blk, ok, b * BS, Lc, rg, scale_log2, m, l, acc);
   }
   if constexpr (FUSE) {

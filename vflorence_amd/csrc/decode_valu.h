@@ -107,7 +107,9 @@ __device__ __forceinline__ void consume(const uint4 (&qv)[G][ValuLayout<DT, D>::
 
 // Issue the loads of U consecutive blocks (one stage) into registers.  Block ids
 // outside the pool load nothing and are marked invalid; chunks past the row stay zero.
-template <int DT, int D, int BS, int U>
+// b counts BS-token chunks; a pool block holds 1 << SHIFT of them (32-token blocks:
+// two), chunk b being part b & mask of table entry b >> SHIFT.
+template <int DT, int D, int BS, int U, int SHIFT>
 __device__ __forceinline__ void load_stage(const typename Elem<DT>::T *__restrict__ kc,
                                            const typename Elem<DT>::T *__restrict__ vc,
                                            WaveBlockIds &ids, int b, int64_t block_elems,
@@ -116,11 +118,13 @@ __device__ __forceinline__ void load_stage(const typename Elem<DT>::T *__restric
   using Lay = ValuLayout<DT, D>;
   constexpr int VEC = Lay::VEC, CPL = Lay::CPL, TPL = Lay::TPL;
   constexpr int NLD = BS / TPL;
+  constexpr int bs_shift = SHIFT, part_mask = (1 << SHIFT) - 1;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int id = ids.get(b + u);
+    const int id = ids.get((b + u) >> bs_shift);
     ok[u] = id >= 0 && id < num_blocks;
-    const int64_t base = (ok[u] ? (int64_t)id : 0) * block_elems + lane_off;
+    const int64_t base = (ok[u] ? (int64_t)id : 0) * block_elems + lane_off +
+                         ((b + u) & part_mask) * BS * D;
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
 #pragma unroll
@@ -170,7 +174,9 @@ template <int DT> __device__ __forceinline__ typename Elem<DT>::T to_elem(float 
     return (typename Elem<DT>::T)f32_to_f16(v);
 }
 
-template <int DT, int D, int BS, int G, int NW, int U, bool PIPE>
+// SHIFT: pool blocks hold BS << SHIFT tokens (0, or 1 for the reference's 32-token
+// blocks); the kernel walks BS-token parts of them.
+template <int DT, int D, int BS, int G, int NW, int U, bool PIPE, int SHIFT>
 __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
     const typename Elem<DT>::T *__restrict__ q, int64_t q_st, int64_t q_sh,
     const typename Elem<DT>::T *__restrict__ kc, const typename Elem<DT>::T *__restrict__ vc,
@@ -179,6 +185,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
     const int32_t *__restrict__ group_start, const int32_t *__restrict__ group_order,
     int64_t num_rows, int64_t num_groups, int H, int64_t num_blocks, float scale_log2) {
   using Lay = ValuLayout<DT, D>;
+  constexpr int bs_shift = SHIFT;
   constexpr int VEC = Lay::VEC, CPL = Lay::CPL, LPT = Lay::LPT, TPL = Lay::TPL;
   constexpr int NLD = BS / TPL;  // loads per block per head and chunk slot
   static_assert(64 % LPT == 0 && BS % TPL == 0, "unsupported tile");
@@ -204,8 +211,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
   nrows = (int)min((int64_t)nrows, num_rows - row0);
   if (nrows <= 0) return;
   const int L = seq_lens[row0];
-  int nblk = L > 0 ? (L + BS - 1) / BS : 0;
-  nblk = min(nblk, max_blocks);
+  int nblk = L > 0 ? (L + BS - 1) / BS : 0;  // BS-token chunks
+  nblk = min(nblk, max_blocks << bs_shift);
   const int Lc = min(L, nblk * BS);
   const int tok = lane / LPT;
   const int c = lane % LPT;
@@ -244,9 +251,13 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
   }
 
   WaveBlockIds ids;
-  ids.init(bt + (int64_t)row0 * bt_stride, b0, b1);
-  const int64_t block_elems = (int64_t)H * BS * D;
-  const int lane_off = h * BS * D + tok * D;
+  if constexpr (SHIFT == 0)
+    ids.init(bt + (int64_t)row0 * bt_stride, b0, b1);
+  else
+    ids.init(bt + (int64_t)row0 * bt_stride, b0 >> SHIFT,
+             b1 > b0 ? ((b1 - 1) >> SHIFT) + 1 : b0 >> SHIFT);
+  const int64_t block_elems = (int64_t)H * (BS << bs_shift) * D;
+  const int lane_off = h * (BS << bs_shift) * D + tok * D;
 
   // Whole blocks of this wave's run are consumed U at a time.  With PIPE the loads
   // of stage s+1 are issued before stage s is consumed (two register stages live),
@@ -260,17 +271,17 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
     if (stages > 0) {
       uint4 ka[SLOTS], va[SLOTS], kb[SLOTS], vb[SLOTS];
       bool oka[U], okb[U];
-      load_stage<DT, D, BS, U>(kc, vc, ids, b, block_elems, lane_off, c, num_blocks, ka, va,
+      load_stage<DT, D, BS, U, SHIFT>(kc, vc, ids, b, block_elems, lane_off, c, num_blocks, ka, va,
                                oka);
       for (int st = 0; st < stages; st += 2) {
         if (st + 1 < stages)
-          load_stage<DT, D, BS, U>(kc, vc, ids, b + U, block_elems, lane_off, c, num_blocks,
+          load_stage<DT, D, BS, U, SHIFT>(kc, vc, ids, b + U, block_elems, lane_off, c, num_blocks,
                                    kb, vb, okb);
         consume_stage<DT, D, BS, G, U>(qv, ka, va, oka, nrows, scale_log2, m, l, acc);
         b += U;
         if (st + 1 >= stages) break;
         if (st + 2 < stages)
-          load_stage<DT, D, BS, U>(kc, vc, ids, b + U, block_elems, lane_off, c, num_blocks,
+          load_stage<DT, D, BS, U, SHIFT>(kc, vc, ids, b + U, block_elems, lane_off, c, num_blocks,
                                    ka, va, oka);
         consume_stage<DT, D, BS, G, U>(qv, kb, vb, okb, nrows, scale_log2, m, l, acc);
         b += U;
@@ -280,8 +291,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
     for (int st = 0; st < stages; ++st, b += U) {
       uint4 kr[SLOTS], vr[SLOTS];
       bool ok[U];
-      load_stage<DT, D, BS, U>(kc, vc, ids, b, block_elems, lane_off, c, num_blocks, kr, vr,
-                               ok);
+      load_stage<DT, D, BS, U, SHIFT>(kc, vc, ids, b, block_elems, lane_off, c, num_blocks, kr,
+                                      vr, ok);
       consume_stage<DT, D, BS, G, U>(qv, kr, vr, ok, nrows, scale_log2, m, l, acc);
     }
   }
@@ -289,7 +300,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
   for (; b < b1; ++b) {
     uint4 kr[NLD * CPL], vr[NLD * CPL];
     bool ok[1];
-    load_stage<DT, D, BS, 1>(kc, vc, ids, b, block_elems, lane_off, c, num_blocks, kr, vr, ok);
+    load_stage<DT, D, BS, 1, SHIFT>(kc, vc, ids, b, block_elems, lane_off, c, num_blocks, kr, vr,
+                                    ok);
     bool valid[NLD];
 #pragma unroll
     for (int i = 0; i < NLD; ++i) valid[i] = ok[0] && (b * BS + i * TPL + tok) < Lc;

@@ -255,12 +255,12 @@ extern "C" int vfl_reshape_and_cache(const void *key, const void *value,
     set_error("reshape_and_cache: head_dim %d must be a multiple of %d", head_dim, vec);
     return VFL_E_UNSUPPORTED;
   }
-  // Only pools that an attention kernel reads are written: the 16-bit V layout
-  // interleaves tokens by four inside a 16-token block, so any other block size would
-  // place V outside its block-head slice.
-  if (block_size != KV_BLOCK_SIZE) {
-    set_error("reshape_and_cache: block_size %d has no attention kernel (supported: %d)",
-              block_size, KV_BLOCK_SIZE);
+  // Only pools that an attention kernel reads are written (16- and 32-token blocks): the
+  // 16-bit V layout interleaves tokens by four inside a block, so a block size that is
+  // not a multiple of 4 would place V outside its block-head slice.
+  if (block_shift(block_size) < 0) {
+    set_error("reshape_and_cache: block_size %d has no attention kernel (supported: 16, 32)",
+              block_size);
     return VFL_E_UNSUPPORTED;
   }
   if (num_tokens == 0) return VFL_OK;

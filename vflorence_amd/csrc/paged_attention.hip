@@ -64,13 +64,13 @@ static int launch_mfma(const AttnArgs &a) {
     return launch_status("attention_with_kv_cache");
   }
   if (a.kvw.slots)
-    paged_decode_mfma_kernel<DT, D, NW, MFMA_STAGE_BLOCKS, true>
+    paged_decode_mfma_kernel<DT, D, NW, MFMA_STAGE_BLOCKS, true, 0>
         <<<grid, dim3(NW * 64), 0, a.stream>>>(
         (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
         (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
         a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw);
   else
-    paged_decode_mfma_kernel<DT, D, NW, MFMA_STAGE_BLOCKS, false>
+    paged_decode_mfma_kernel<DT, D, NW, MFMA_STAGE_BLOCKS, false, 0>
         <<<grid, dim3(NW * 64), 0, a.stream>>>(
         (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
         (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
@@ -92,6 +92,7 @@ static int mfma_waves(const AttnArgs &a, int nw) {
 }
 
 static int dispatch(const AttnArgs &a, int dtype, int head_dim, int gmax, int nw) {
+  if (a.bs_shift != 0) return dispatch_block32(a, dtype, head_dim, gmax, nw);
   if (dtype == VFL_FLOAT32) {
     if (head_dim == 64) return valu_group<64>(a, gmax, nw);
     if (head_dim == 128) return valu_group<128>(a, gmax, nw);
@@ -107,7 +108,7 @@ static int dispatch(const AttnArgs &a, int dtype, int head_dim, int gmax, int nw
 
 static bool kernel_exists(int dtype, int block_size, int head_dim) {
   return (dtype == VFL_FLOAT32 || dtype == VFL_BFLOAT16 || dtype == VFL_FLOAT16) &&
-         block_size == 16 && head_dim_supported(head_dim);
+         block_shift(block_size) >= 0 && head_dim_supported(head_dim);
 }
 
 constexpr int MAX_GROUP = 8;
@@ -302,9 +303,10 @@ static int attention_impl(const void *query, int64_t query_stride_token,
   a.plan_stride = a.plan_slots = 0;
   a.q_vec = (uintptr_t)query % 16 == 0 && query_stride_token % 8 == 0 &&
             query_stride_head % 8 == 0;
+  a.bs_shift = block_shift(block_size);
   // Kernels with own-table groups, plans and the fused write exist for 16-bit caches
-  // of head size 64 and 128.
-  const bool full_set = dtype != VFL_FLOAT32 && head_dim_native(head_dim);
+  // of head size 64 and 128 in 16-token blocks.
+  const bool full_set = dtype != VFL_FLOAT32 && head_dim_native(head_dim) && block_size == 16;
   if (meta->group_plan != nullptr && a.own_tables && full_set) {
     if ((uintptr_t)meta->group_plan % 16 != 0 || meta->group_plan_stride < PLAN_HEADER ||
         meta->group_plan_stride % 4 != 0 || meta->group_plan_slots < num_groups ||
@@ -367,9 +369,9 @@ extern "C" int vfl_self_attention_with_kv_write(
               "VFL_GROUP_OWN_TABLES (every row keeps its own block table)");
     return VFL_E_INVALID;
   }
-  if (dtype == VFL_FLOAT32 || !head_dim_native(head_dim)) {
-    // No fused kernel for fp32 or for head sizes other than 64 and 128: the same two
-    // steps as the reference.
+  if (dtype == VFL_FLOAT32 || !head_dim_native(head_dim) || block_size != 16) {
+    // No fused kernel for fp32, for head sizes other than 64 and 128, or for 32-token
+    // blocks: the same two steps as the reference.
     int st = vfl_reshape_and_cache(key, value, key_stride_token, key_stride_head,
                                    value_stride_token, value_stride_head, k_cache, v_cache,
                                    slot_mapping, num_rows, num_heads, head_dim, block_size,

@@ -32,7 +32,10 @@ SUPPORTED_HEAD_DIMS = frozenset({32, 48, 64, 80, 96, 112, 128, 160, 192, 224, 25
 # row (or one shared-table group) per workgroup with the KV write as its own launch;
 # the entry points take the same arguments and fall back by themselves.
 NATIVE_HEAD_DIMS = frozenset({64, 128})
-SUPPORTED_BLOCK_SIZES = frozenset({16})
+# Pool block sizes: 16 (this build's engine), and 32, the reference's on x86
+# (vflorence/config.py:42), read by the one-row kernels as two 16-token parts (beam
+# groups, group plans and the fused KV write then fall back as for other head sizes).
+SUPPORTED_BLOCK_SIZES = frozenset({16, 32})
 MAX_GROUP_SIZE = 8
 # Waves per workgroup for the fused KV-write + self-attention launch (measured: two
 # beat four on both short decode-step contexts and 256 ragged rows up to 1024 tokens).
