@@ -21,6 +21,9 @@ OUTPUT = os.path.join(HERE, "libvflorence_amd.so")
 ARCH = os.environ.get("VFL_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
+# -amdgpu-mfma-vgpr-form: matrix-core results in ordinary VGPRs, so accumulators that the
+# online softmax rescales between products are not copied to and from AGPRs around every
+# product (the beam-group self-attention kernel lost 144 such moves, 12 VGPRs).
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -31,6 +34,8 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 ]
 
 

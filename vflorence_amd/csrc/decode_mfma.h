@@ -125,14 +125,8 @@ __device__ __forceinline__ void mfma_consume(const uint4 (&qop)[k_chunks<D>()], 
     p[j] = fast_exp2(sv[j] - ms);
     l += p[j];
   }
-  uint32_t hi[4], lo[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    hi[j] = Ops::narrow(p[j]);
-    lo[j] = Ops::narrow(p[j] - Ops::widen(hi[j]));
-  }
-  const uint2 phi = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-  const uint2 plo = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
+  uint2 phi, plo;
+  split_weights<DT>(p, phi, plo);
   if constexpr (MASKED) {
     // Stale or garbage V of masked tokens must not meet a zero weight (0 * NaN).
     const uint32_t keep01 = (valid[0] ? 0xffffu : 0u) | (valid[1] ? 0xffff0000u : 0u);
@@ -381,8 +375,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
     uint16_t *orow = out + ((int64_t)(row0 + col) * H + h) * D + 4 * rg;
 #pragma unroll
     for (int c = 0; c < VCH; ++c) {
-      const uint32_t a = Mfma<DT>::narrow(acc[c][0] * inv) | (Mfma<DT>::narrow(acc[c][1] * inv) << 16);
-      const uint32_t bb = Mfma<DT>::narrow(acc[c][2] * inv) | (Mfma<DT>::narrow(acc[c][3] * inv) << 16);
+      const uint32_t a = Mfma<DT>::narrow2(acc[c][0] * inv, acc[c][1] * inv);
+      const uint32_t bb = Mfma<DT>::narrow2(acc[c][2] * inv, acc[c][3] * inv);
       *reinterpret_cast<uint2 *>(orow + 16 * c) = make_uint2(a, bb);
     }
   } else {

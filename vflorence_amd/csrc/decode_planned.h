@@ -301,8 +301,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
     uint16_t *orow = out + (row * H + h) * D + 4 * rg;
 #pragma unroll
     for (int c = 0; c < VCH; ++c) {
-      const uint32_t a = Mfma<DT>::narrow(acc[c][0] * inv) | (Mfma<DT>::narrow(acc[c][1] * inv) << 16);
-      const uint32_t bb = Mfma<DT>::narrow(acc[c][2] * inv) | (Mfma<DT>::narrow(acc[c][3] * inv) << 16);
+      const uint32_t a = Mfma<DT>::narrow2(acc[c][0] * inv, acc[c][1] * inv);
+      const uint32_t bb = Mfma<DT>::narrow2(acc[c][2] * inv, acc[c][3] * inv);
       *reinterpret_cast<uint2 *>(orow + 16 * c) = make_uint2(a, bb);
     }
   } else {

@@ -110,14 +110,8 @@ __device__ __forceinline__ void mfma_consume_cols(const uint4 (&qop)[D / 32], Mf
     p[j] = fast_exp2(sv[j] - ms);
     l += p[j];
   }
-  uint32_t hi[4], lo[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    hi[j] = Ops::narrow(p[j]);
-    lo[j] = Ops::narrow(p[j] - Ops::widen(hi[j]));
-  }
-  const uint2 phi = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-  const uint2 plo = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
+  uint2 phi, plo;
+  split_weights<DT>(p, phi, plo);
   const uint32_t keep01 = (keep[0] ? 0xffffu : 0u) | (keep[1] ? 0xffff0000u : 0u);
   const uint32_t keep23 = (keep[2] ? 0xffffu : 0u) | (keep[3] ? 0xffff0000u : 0u);
 #pragma unroll
@@ -399,8 +393,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_shared_kernel(
     uint16_t *orow = out + (row * H + h) * D + 4 * rg;
 #pragma unroll
     for (int c = 0; c < VCH; ++c) {
-      const uint32_t a = Mfma<DT>::narrow(acc[c][0] * inv) | (Mfma<DT>::narrow(acc[c][1] * inv) << 16);
-      const uint32_t bb = Mfma<DT>::narrow(acc[c][2] * inv) | (Mfma<DT>::narrow(acc[c][3] * inv) << 16);
+      const uint32_t a = Mfma<DT>::narrow2(acc[c][0] * inv, acc[c][1] * inv);
+      const uint32_t bb = Mfma<DT>::narrow2(acc[c][2] * inv, acc[c][3] * inv);
       *reinterpret_cast<uint2 *>(orow + 16 * c) = make_uint2(a, bb);
     }
   } else {
