@@ -248,7 +248,7 @@ def schedule_order(n: int, steps: int = DECODE_STEPS) -> list[int]:
 
 KERNEL_NAMES = {  # kernel name prefixes of the decode step's launches
     "cross": "void vfl::paged_decode_mfma_kernel<1, 64, 8, 2, false, 0>",
-    "self": "void vfl::paged_decode_planned_kernel<1, 64, 2, 4, true>",
+    "self": "void vfl::paged_decode_planned_kernel<1, 64, 2, 6, true>",
     "self_walk": "void vfl::paged_decode_shared_kernel<1, 64, 2, 2, true>",
     "self_rows": "void vfl::paged_decode_mfma_kernel<1, 64, 2, 2, true, 0>",
     "cow": "vfl::copy_blocks_kernel",

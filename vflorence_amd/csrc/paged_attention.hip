@@ -23,8 +23,10 @@ constexpr int MFMA_STAGE_BLOCKS = 2;
 constexpr int SHARED_STAGE_BLOCKS = 2;
 
 // Stage size of the planned group kernel: every wave requests this many blocks per
-// round trip.
-constexpr int PLANNED_STAGE_BLOCKS = 4;
+// round trip.  Measured on the 64 x 4-beam decode step (two passes each, one box): 4 / 5
+// / 6 / 8 blocks ran the step in 0.5382 / 0.5361 / 0.5350 / 0.5354 ms; six needs 204
+// VGPRs, still two waves per SIMD (all the launch's waves resident).
+constexpr int PLANNED_STAGE_BLOCKS = 6;
 
 template <int DT, int D, int NW>
 static int launch_planned(const AttnArgs &a) {
