@@ -163,7 +163,7 @@ class ModelRunner:
         self._cross_buffers = attention.CrossStagingBuffers(
             config.max_num_seqs, math.ceil(config.max_encoder_len / self.block_size), self.device)
         # decode steps captured per batch size (rows), replayed while the shapes repeat
-        self._graphs: dict[tuple[int, bool], tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self._graphs: dict[tuple[int, bool, int], tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self._step_grouped = False
         self._buckets = row_buckets(config.max_num_seqs)
         self._self_metadata: dict[tuple[int, bool], hip_attn.SchedulerMetadata] = {}
@@ -425,7 +425,11 @@ class ModelRunner:
         if not self.config.cuda_graphs:
             return self.decode_fn(input_ids, positions)
         n = input_ids.shape[0]
-        key = (n, self._step_grouped)  # grouped steps launch another kernel
+        # grouped steps launch another kernel; the cross-attention's wave count follows
+        # the batch's number of requests (one capture per count the batches use)
+        cross_meta = self._cross_staged[0][4]
+        cross_waves = cross_meta.plan(n, self._cross_buffers.max_pages).waves_per_workgroup
+        key = (n, self._step_grouped, cross_waves)
         entry = self._graphs.get(key)
         if entry is None:
             side = torch.cuda.Stream()

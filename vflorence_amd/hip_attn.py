@@ -259,6 +259,9 @@ class SchedulerMetadata:
     max_group_size: int = 1
     waves_per_workgroup: int = 0
     own_tables: bool = False
+    # Groups that do work when the launch holds more group slots (fixed-address staging:
+    # unused slots exit at once); the default wave count is chosen for these.
+    active_groups: int | None = None
     # The caller's promise that each row writes its new token at the slot of its last
     # context position, in a block no other row reads (the block manager's
     # copy-on-write invariant); lets the self-attention op fuse the KV write.
@@ -284,6 +287,20 @@ class SchedulerMetadata:
                     # step's short contexts are latency-bound; more waves only add a
                     # merge), two beyond (ragged contexts up to 1024 tokens)
                     waves = 1 if max_blocks <= FUSED_ONE_WAVE_BLOCKS else FUSED_WAVES
+            elif waves == 0 and self.active_groups is not None:
+                # the library's default for a launch of just the working groups
+                active = max(1, min(self.active_groups, groups))
+                probe = SchedMeta()
+                check(
+                    lib.vfl_get_scheduler_metadata(
+                        active, active, self.num_heads, self.head_dim, self.block_size,
+                        max_blocks, self.max_group_size, _dtype_code(self.dtype), 0,
+                        _lib.VFL_GROUP_OWN_TABLES if self.own_tables
+                        else _lib.VFL_GROUP_SHARED_TABLE,
+                        ctypes.byref(probe),
+                    )
+                )
+                waves = probe.waves_per_workgroup
             check(
                 lib.vfl_get_scheduler_metadata(
                     num_rows, groups, self.num_heads, self.head_dim, self.block_size,
@@ -361,12 +378,13 @@ def get_scheduler_metadata(
     fuse_kv_write: bool = False,
     own_tables: bool = False,
     group_plan: GroupPlan | None = None,
+    active_groups: int | None = None,
 ) -> SchedulerMetadata:
     """Counterpart of ``vllm_cpu_attn.get_scheduler_metadata`` (keyword names from
     vflorence/layers/attention.py:18-29 and vflorence/engine/model_runner.py:308-319).
 
     ``group_start``/``group_order``/``max_group_size``/``waves_per_workgroup``/
-    ``own_tables``/``group_plan`` are this library's additions.  ``seq_lens``, ``query_start_loc``, ``causal`` and ``isa`` are
+    ``own_tables``/``group_plan``/``active_groups`` are this library's additions.  ``seq_lens``, ``query_start_loc``, ``causal`` and ``isa`` are
     accepted for signature compatibility; the plan does not need them (callers that
     know the lengths on the host pass ``group_order`` instead).
     """
@@ -410,6 +428,7 @@ def get_scheduler_metadata(
         fuse_kv_write=fuse_kv_write,
         own_tables=own_tables,
         group_plan=group_plan,
+        active_groups=active_groups,
     )
 
 

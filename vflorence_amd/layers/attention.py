@@ -109,9 +109,15 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=N
     # every (group, head) workgroup is resident at once: balance long and short groups
     # over the CUs (hip_attn.balanced_order)
     run = hip_attn.resident_run(device, attn.num_heads) if device.type == "cuda" else 1
+    active = None
     if buffers is not None:
         seq_lens, group_start, group_order, block_table = _stage_into(buffers, pages, enc_lens,
                                                                       starts, run)
+        # n slots, about n / (beams per request) of them working: waves per workgroup as
+        # for a launch of that many groups (4 beams of 64 requests: 1024 workgroups and
+        # eight waves, not the 4096 slots' four).  Slots over beam width, not the exact
+        # group count, so every batch of one row bucket and beam width launches alike.
+        active = -(-n // max_group)
         max_group = hip_attn.MAX_GROUP_SIZE  # one launch shape for every batch of n rows
     else:
         block_table = torch.nn.utils.rnn.pad_sequence(
@@ -147,6 +153,7 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=N
         group_start=group_start,
         group_order=group_order,
         max_group_size=max_group,
+        active_groups=active,
     )
     return [
         (
