@@ -247,7 +247,7 @@ def schedule_order(n: int, steps: int = DECODE_STEPS) -> list[int]:
 
 
 KERNEL_NAMES = {  # kernel name prefixes of the decode step's launches
-    "cross": "void vfl::paged_decode_mfma_kernel<1, 64, 8, 2, false, 0>",
+    "cross": "void vfl::paged_decode_mfma_kernel<1, 64, 4, 2, false, 0>",
     "self": "void vfl::paged_decode_planned_kernel<1, 64, 2, 6, true>",
     "self_walk": "void vfl::paged_decode_shared_kernel<1, 64, 2, 2, true>",
     "self_rows": "void vfl::paged_decode_mfma_kernel<1, 64, 2, 2, true, 0>",
@@ -675,6 +675,10 @@ GATHER_VARIANTS = {
     2: "(group, 4 heads): 8 KiB of a block read together, 256 x 16 waves",
     3: "(group, 4 heads): each wave reads 8 KiB per block, 256 x 4 waves",
     4: "(group, head) slices as 0, non-temporal loads (the attention kernels' hint)",
+    5: "(group, head) slices, non-temporal, 1024 x 8 waves, 2 blocks per iteration "
+       "(the kernel's shape)",
+    6: "(group, head) slices, non-temporal, 1024 x 8 waves, 4 blocks per iteration",
+    7: "(group, head) slices, non-temporal, 1024 x 16 waves, 2 blocks per iteration",
 }
 
 
@@ -1090,7 +1094,7 @@ def main():
         "wall_s_timed": round(wall, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": ("paged_decode_mfma_kernel<bf16, D=64, 8 waves, 2 blocks/stage> "
+            "kernel": ("paged_decode_mfma_kernel<bf16, D=64, 4 waves, 2 blocks/stage> "
                        "(cross-attention, 4 beams per group)"),
             "achieved": round(c_step_gbps, 1),
             "peak": HBM_PEAK_GBPS,

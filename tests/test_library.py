@@ -82,10 +82,10 @@ def test_scheduler_metadata_plan():
     assert (m.num_rows, m.num_groups, m.num_heads, m.head_dim) == (256, 256, 16, 64)
     assert m.max_blocks_per_seq == 64 and m.max_group_size == 1
     assert m.waves_per_workgroup in (1, 2, 4, 8)
-    # 256 ragged rows (4096 workgroups): four; 64 x 4 beams (1024 workgroups): eight
+    # 256 ragged rows (4096 workgroups) and 64 x 4 beams (1024 workgroups): four
     assert m.waves_per_workgroup == 4
     rc, m = plan(256, 64, 16, 64, 64, gmax=4)
-    assert rc == 0 and m.waves_per_workgroup == 8 and m.max_group_size == 4
+    assert rc == 0 and m.waves_per_workgroup == 4 and m.max_group_size == 4
     # few workgroups: more waves each
     rc, m = plan(8, 8, 16, 64, 64)
     assert rc == 0 and m.waves_per_workgroup == 8

@@ -117,13 +117,15 @@ constexpr int MAX_GROUP = 8;
 constexpr int MAX_WAVES = 8;
 
 // Waves per (group, head) workgroup.  Measured on MI355X (bf16, head_dim 64, K/V pages
-// loaded non-temporally): 64 x 4-beam cross-attention (1024 workgroups) runs 30.3 us
-// with eight waves, 32.8-33.6 with four, 36.1 with two; 256 ragged self-attention rows
-// (4096 workgroups) run within noise of each other with two, four or eight (92.6-97.1
-// us).  So eight below 2048 workgroups, four above.  Never more waves than blocks.
+// loaded non-temporally), 64 x 4-beam cross-attention (1024 workgroups) in the decode
+// step: two / four / eight waves 34.9 / 29.5 / 30.6 us (four keeps all 1024 workgroups
+// resident at once); 256 ragged self-attention rows (4096 workgroups) run within noise
+// of each other with two, four or eight.  So four, and eight only below two workgroups
+// per CU, where a workgroup's blocks need the extra waves.  Never more waves than
+// blocks.
 static int default_waves(int64_t num_groups, int num_heads, int64_t max_blocks) {
   const int64_t wgs = num_groups * num_heads;
-  int nw = wgs >= 2048 ? 4 : 8;
+  int nw = wgs >= 512 ? 4 : 8;
   while (nw > 1 && nw / 2 >= max_blocks) nw /= 2;
   return nw;
 }

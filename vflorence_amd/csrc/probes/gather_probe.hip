@@ -76,6 +76,33 @@ __global__ __launch_bounds__(256) void probe_slices_nt(Args a) {
   if (acc == 0x12345678u) a.out[id] = acc;
 }
 
+// A with non-temporal loads, NW waves per workgroup and UB blocks per iteration (the
+// cross-attention kernel runs eight waves and two blocks per stage).
+template <int NW, int UB>
+__global__ __launch_bounds__(NW * 64) void probe_slices_ntw(Args a) {
+  int id = blockIdx.x;
+  int g = a.order[id / 16], h = id % 16;
+  const int n = a.nb[g];
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int lo = n * wave / NW, hi = n * (wave + 1) / NW;
+  uint32_t acc = 0;
+  const int32_t *pg = a.pages + (int64_t)g * a.W;
+  for (int i = lo; i < hi; i += UB) {
+    uint4 r[4 * UB];
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      const int b = i + u < hi ? pg[i + u] : pg[i];
+      const int64_t base = ((int64_t)b * 16 + h) * 1024 + lane * 8;
+      const uint4 *kp = (const uint4 *)(a.k + base), *vp = (const uint4 *)(a.v + base);
+      r[u * 4 + 0] = ld_nt(kp); r[u * 4 + 1] = ld_nt(kp + 64);
+      r[u * 4 + 2] = ld_nt(vp); r[u * 4 + 3] = ld_nt(vp + 64);
+    }
+#pragma unroll
+    for (int j = 0; j < 4 * UB; ++j) acc ^= fold(r[j]);
+  }
+  if (acc == 0x12345678u) a.out[id] = acc;
+}
+
 // B: workgroup = (group, quad of 4 heads), 16 waves: wave = (head in quad, run).
 __global__ __launch_bounds__(1024) void probe_quads(Args a) {
   int id = blockIdx.x;
@@ -136,6 +163,9 @@ extern "C" int probe_launch(int variant, const void *k, const void *v, const int
     case 2: probe_quads<<<G * 4, 1024, 0, s>>>(a); break;
     case 3: probe_quads_wave<<<G * 4, 256, 0, s>>>(a); break;
     case 4: probe_slices_nt<<<G * 16, 256, 0, s>>>(a); break;
+    case 5: probe_slices_ntw<8, 2><<<G * 16, 512, 0, s>>>(a); break;
+    case 6: probe_slices_ntw<8, 4><<<G * 16, 512, 0, s>>>(a); break;
+    case 7: probe_slices_ntw<16, 2><<<G * 16, 1024, 0, s>>>(a); break;
     default: return -1;
   }
   return hipGetLastError() == hipSuccess ? 0 : -2;

@@ -117,7 +117,9 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=N
         # for a launch of that many groups (4 beams of 64 requests: 1024 workgroups and
         # eight waves, not the 4096 slots' four).  Slots over beam width, not the exact
         # group count, so every batch of one row bucket and beam width launches alike.
-        active = -(-n // max_group)
+        # (padding rows share one empty page list and group together: not counted)
+        beams = max((b - a for a, b in zip(starts, starts[1:]) if enc_lens[a] > 0), default=1)
+        active = -(-n // beams)
         max_group = hip_attn.MAX_GROUP_SIZE  # one launch shape for every batch of n rows
     else:
         block_table = torch.nn.utils.rnn.pad_sequence(
