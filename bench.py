@@ -250,7 +250,7 @@ KERNEL_NAMES = {  # kernel name prefixes of the decode step's launches
     "cross": "void vfl::paged_decode_mfma_kernel<1, 64, 4, 2, false, 0>",
     "self": "void vfl::paged_decode_planned_kernel<1, 64, 2, 6, true>",
     "self_walk": "void vfl::paged_decode_shared_kernel<1, 64, 2, 2, true>",
-    "self_rows": "void vfl::paged_decode_mfma_kernel<1, 64, 2, 2, true, 0>",
+    "self_rows": "void vfl::paged_decode_mfma_kernel<1, 64, 4, 2, true, 0>",
     "cow": "vfl::copy_blocks_kernel",
 }
 

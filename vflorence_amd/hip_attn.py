@@ -37,9 +37,10 @@ NATIVE_HEAD_DIMS = frozenset({64, 128})
 # groups, group plans and the fused KV write then fall back as for other head sizes).
 SUPPORTED_BLOCK_SIZES = frozenset({16, 32})
 MAX_GROUP_SIZE = 8
-# Waves per workgroup for the fused KV-write + self-attention launch (measured: two
-# beat four on both short decode-step contexts and 256 ragged rows up to 1024 tokens).
-FUSED_WAVES = 2
+# Waves per workgroup for the fused KV-write + self-attention launch over contexts longer
+# than FUSED_ONE_WAVE_BLOCKS blocks (measured, 256 ragged rows up to 1024 tokens, three
+# pools in rotation: one / two / four / eight waves 102.0 / 96.1 / 95.3 / 119.0 us).
+FUSED_WAVES = 4
 FUSED_ONE_WAVE_BLOCKS = 4
 # Waves per workgroup of the fused launch over own-table row groups (beams): measured
 # best from 1 to 8 blocks of context (64 x 4 beams, MI355X); more waves cost occupancy.
