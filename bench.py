@@ -507,6 +507,8 @@ def counter_pass(torch, wl, reps: int):
         k, v, table, lens, sm = wl["staged"][i]
         out = torch.empty_like(wl["qc"][i])
         launches.append(raw_attention_launcher(torch, wl["qc"][i], k, v, out, lens, table, sm))
+    k, v, table, lens, sm = wl["staged"][0]
+    cross_waves = sm.plan(REQUESTS * BEAMS, table.shape[1]).waves_per_workgroup
     for _ in range(reps):
         for f in launches:
             f()
@@ -561,7 +563,7 @@ def counter_pass(torch, wl, reps: int):
     c_bytes = workloads.cross_attention_bytes(wl["enc"], REQUESTS * BEAMS, NUM_HEADS, HEAD_DIM,
                                               2, BLOCK)
     print(json.dumps({"counter_pass": True, "cross_launches": NUM_LAYERS * (reps + 1),
-                      "cross_grid_threads": REQUESTS * NUM_HEADS * 64 * 8,
+                      "cross_grid_threads": REQUESTS * NUM_HEADS * 64 * cross_waves,
                       "cross_algorithmic_bytes": int(c_bytes),
                       "self_step": len(wl["plans"]) - 1,
                       "self_launches_each": NUM_LAYERS,
