@@ -68,22 +68,27 @@ __device__ __forceinline__ uint2 load_stream8(const uint16_t *p) {
   return make_uint2(v.x, v.y);
 }
 
+// Load one block's K rows and V 4-token groups into MFMA operand order.  `tokens`
+// (1..16) leaves the K rows and V groups of later tokens unread (zero): a partial last
+// block then reads only its tokens, whose weights are all the masked consume uses.
 template <int DT, int D>
 __device__ __forceinline__ void mfma_load_block(const uint16_t *__restrict__ kc,
                                                 const uint16_t *__restrict__ vc, int id, bool ok,
                                                 int64_t block_elems, int head_off, int k_lane,
-                                                int v_lane, MfmaBlock<D> &blk) {
+                                                int v_lane, MfmaBlock<D> &blk, int tokens = 16) {
   const int64_t base = (ok ? (int64_t)id : 0) * block_elems + head_off;
   const int rg = (int)(__lane_id() >> 4);
+  const bool k_ok = ok && (int)(__lane_id() & 15) < tokens;
+  const bool v_ok = ok && 4 * rg < tokens;
 #pragma unroll
   for (int kk = 0; kk < k_chunks<D>(); ++kk) {
     blk.k[kk] = make_uint4(0, 0, 0, 0);
-    if (ok && k_chunk_ok<D>(kk, rg)) blk.k[kk] = load_stream16(kc + base + k_lane + 32 * kk);
+    if (k_ok && k_chunk_ok<D>(kk, rg)) blk.k[kk] = load_stream16(kc + base + k_lane + 32 * kk);
   }
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) {
     blk.v[c] = make_uint2(0, 0);
-    if (ok) blk.v[c] = load_stream8(vc + base + v_lane + 64 * c);
+    if (v_ok) blk.v[c] = load_stream8(vc + base + v_lane + 64 * c);
   }
 }
 
@@ -358,7 +363,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
     const int id = ids.get(b >> bs_shift);
     const bool ok = id >= 0 && id < num_blocks;
     mfma_load_block<DT, D>(kc, vc, id, ok, block_elems, head_off + (b & part_mask) * BS * D,
-                           k_lane, v_lane, blk);
+                           k_lane, v_lane, blk, min(BS, Lc - b * BS));
     mfma_consume<DT, D, true>(qop, blk, ok, b * BS, Lc, rg, scale_log2, m, l, acc);
   }
   if constexpr (FUSE) {
