@@ -681,6 +681,7 @@ GATHER_VARIANTS = {
        "(the kernel's shape)",
     6: "(group, head) slices, non-temporal, 1024 x 8 waves, 4 blocks per iteration",
     7: "(group, head) slices, non-temporal, 1024 x 16 waves, 2 blocks per iteration",
+    8: "(group, head) slices, non-temporal, a group's 16 heads on one XCD",
 }
 
 

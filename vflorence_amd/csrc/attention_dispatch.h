@@ -53,7 +53,7 @@ int launch_valu(const AttnArgs &a) {
   constexpr int DT = VFL_FLOAT32;
   using T = typename Elem<DT>::T;
   constexpr int BS = 16;
-  const dim3 grid((unsigned)(a.num_groups * a.H));
+  const dim3 grid((unsigned)xcd_grid(a.num_groups, a.H));
   paged_decode_kernel<DT, D, BS, G, NW, stage_blocks<DT, D, G>(), stage_pipeline<G>(), SHIFT>
       <<<grid, dim3(NW * 64), 0, a.stream>>>(
       (const T *)a.q, a.q_st, a.q_sh, (const T *)a.kc, (const T *)a.vc, (T *)a.out, a.seq_lens,
@@ -84,7 +84,7 @@ int valu_group(const AttnArgs &a, int gmax, int nw) {
 // KV write: the matrix-core kernel of decode_mfma.h.
 template <int DT, int D, int NW, int U, int SHIFT = 0>
 int launch_mfma_rows(const AttnArgs &a) {
-  const dim3 grid((unsigned)(a.num_groups * a.H));
+  const dim3 grid((unsigned)xcd_grid(a.num_groups, a.H));
   paged_decode_mfma_kernel<DT, D, NW, U, false, SHIFT><<<grid, dim3(NW * 64), 0, a.stream>>>(
       (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
       (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,

@@ -44,6 +44,25 @@ inline int block_shift(int block_size) {
   return block_size == 16 ? 0 : (block_size == 32 ? 1 : -1);
 }
 
+// Workgroup ids of the attention launches, one workgroup per (group position, head).
+// MI355X deals a launch's workgroup ids to its 8 XCDs round robin (id % 8), each XCD
+// with its own L2.  The ids are laid out so that all H heads of a group position run
+// on one XCD: id = 8 (H (pos / 8) + h) + pos % 8.  The heads' slices of a block then
+// come through one L2, and within an XCD its CUs still see positions p, p + 16, p + 32,
+// ... (with 16 heads), the pattern the balanced dispatch order is built for.  Read-only
+// probe of the cross-attention's pages: 26.9 against 27.6 us per layer with
+// consecutive ids per group.  The grid covers positions rounded up to 8; the extra
+// workgroups exit.
+constexpr int XCDS = 8;
+inline int64_t xcd_grid(int64_t positions, int H) {
+  return (positions + XCDS - 1) / XCDS * XCDS * H;
+}
+__device__ __forceinline__ void xcd_position(unsigned id, unsigned H, int64_t &pos, int &h) {
+  const unsigned j = id / XCDS;
+  h = (int)(j % H);
+  pos = (int64_t)XCDS * (j / H) + id % XCDS;
+}
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 

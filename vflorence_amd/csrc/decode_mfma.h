@@ -217,10 +217,13 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int h = (int)(blockIdx.x % (unsigned)H);
-  int g = (int)(blockIdx.x / (unsigned)H);
+  int64_t pos;
+  int h;
+  xcd_position(blockIdx.x, (unsigned)H, pos, h);
+  if (pos >= num_groups) return;  // workgroup-uniform
+  int g = (int)pos;
   if (group_order) g = group_order[g];
-  if (g < 0 || g >= num_groups || h >= H) return;  // workgroup-uniform
+  if (g < 0 || g >= num_groups || h >= H) return;
   int row0 = g, nrows = 1;
   if (group_start) {
     row0 = group_start[g];

@@ -87,8 +87,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int h = (int)(blockIdx.x % (unsigned)H);
-  const int64_t slot = blockIdx.x / (unsigned)H;
+  int64_t slot;
+  int h;
+  xcd_position(blockIdx.x, (unsigned)H, slot, h);
   if (slot >= num_slots || h >= H) return;  // workgroup-uniform
 
   // Level 1: the used-slot count, the slot's header and its first entries, together.

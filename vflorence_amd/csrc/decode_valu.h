@@ -196,9 +196,12 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  // 1-D grid, head fastest: a group's heads are dispatched together.
-  const int h = (int)(blockIdx.x % (unsigned)H);
-  int g = (int)(blockIdx.x / (unsigned)H);
+  // 1-D grid over (group position, head), a position's heads on one XCD.
+  int64_t pos;
+  int h;
+  xcd_position(blockIdx.x, (unsigned)H, pos, h);
+  if (pos >= num_groups) return;  // workgroup-uniform
+  int g = (int)pos;
   if (group_order) g = group_order[g];
   // Workgroup-uniform exits only (before any barrier).
   if (g < 0 || g >= num_groups || h >= H) return;

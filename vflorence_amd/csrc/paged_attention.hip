@@ -30,7 +30,7 @@ constexpr int PLANNED_STAGE_BLOCKS = 6;
 
 template <int DT, int D, int NW>
 static int launch_planned(const AttnArgs &a) {
-  const dim3 grid((unsigned)(a.plan_slots * a.H));
+  const dim3 grid((unsigned)xcd_grid(a.plan_slots, a.H));
   if (a.kvw.slots)
     paged_decode_planned_kernel<DT, D, NW, PLANNED_STAGE_BLOCKS, true>
         <<<grid, dim3(NW * 64), 0, a.stream>>>(
@@ -49,7 +49,7 @@ static int launch_planned(const AttnArgs &a) {
 template <int DT, int D, int NW>
 static int launch_mfma(const AttnArgs &a) {
   if (a.plan) return launch_planned<DT, D, NW>(a);
-  const dim3 grid((unsigned)(a.num_groups * a.H));
+  const dim3 grid((unsigned)xcd_grid(a.num_groups, a.H));
   if (a.own_tables) {
     if (a.kvw.slots)
       paged_decode_shared_kernel<DT, D, NW, SHARED_STAGE_BLOCKS, true>
@@ -176,7 +176,7 @@ extern "C" int vfl_get_scheduler_metadata(int64_t num_rows, int64_t num_groups, 
     set_error("get_scheduler_metadata: waves_per_workgroup %d not in {0, 1, 2, 4, 8}", nw);
     return VFL_E_UNSUPPORTED;
   }
-  if (num_groups * num_heads > 2147483647LL) {
+  if (xcd_grid(num_groups, num_heads) > 2147483647LL) {
     set_error("get_scheduler_metadata: too many groups x heads for one grid");
     return VFL_E_UNSUPPORTED;
   }
@@ -254,8 +254,8 @@ static int attention_impl(const void *query, int64_t query_stride_token,
               (long long)num_groups, (long long)num_rows);
     return VFL_E_INVALID;
   }
-  if (num_groups < 0 || num_groups > num_rows || num_groups * num_heads > 2147483647LL ||
-      num_heads > 65535) {
+  if (num_groups < 0 || num_groups > num_rows || num_heads <= 0 || num_heads > 65535 ||
+      xcd_grid(num_groups, num_heads) > 2147483647LL) {
     set_error("%s: num_groups %lld / num_heads %d out of range", who, (long long)num_groups,
               num_heads);
     return VFL_E_INVALID;
@@ -314,7 +314,7 @@ static int attention_impl(const void *query, int64_t query_stride_token,
   if (meta->group_plan != nullptr && a.own_tables && full_set) {
     if ((uintptr_t)meta->group_plan % 16 != 0 || meta->group_plan_stride < PLAN_HEADER ||
         meta->group_plan_stride % 4 != 0 || meta->group_plan_slots < num_groups ||
-        meta->group_plan_slots * num_heads > 2147483647LL ||
+        xcd_grid(meta->group_plan_slots, num_heads) > 2147483647LL ||
         meta->max_group_size > PLAN_MAX_ROWS) {
       set_error("%s: group plan of %lld slots x %lld words (16-byte aligned, stride a "
                 "multiple of 4, at least num_groups %lld slots, groups of <= %d rows)",

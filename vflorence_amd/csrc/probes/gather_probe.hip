@@ -103,6 +103,36 @@ __global__ __launch_bounds__(NW * 64) void probe_slices_ntw(Args a) {
   if (acc == 0x12345678u) a.out[id] = acc;
 }
 
+// A with non-temporal loads and the 16 heads of each group on one XCD: workgroup ids go
+// to the 8 XCDs round robin (id % 8), so XCD x takes the order positions x, x + 8, ...,
+// each for all 16 heads (a block's 32 KiB of K, and of V, read through one L2).
+__global__ __launch_bounds__(256) void probe_slices_xcd(Args a) {
+  const int id = blockIdx.x;
+  const int x = id % 8, j = id / 8;
+  const int pos = 8 * (j / 16) + x;
+  if (pos >= a.G) return;
+  const int g = a.order[pos], h = j % 16;
+  const int n = a.nb[g];
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int lo = n * wave / 4, hi = n * (wave + 1) / 4;
+  uint32_t acc = 0;
+  const int32_t *pg = a.pages + (int64_t)g * a.W;
+  for (int i = lo; i < hi; i += 2) {
+    uint4 r[8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int b = i + u < hi ? pg[i + u] : pg[i];
+      const int64_t base = ((int64_t)b * 16 + h) * 1024 + lane * 8;
+      const uint4 *kp = (const uint4 *)(a.k + base), *vp = (const uint4 *)(a.v + base);
+      r[u * 4 + 0] = ld_nt(kp); r[u * 4 + 1] = ld_nt(kp + 64);
+      r[u * 4 + 2] = ld_nt(vp); r[u * 4 + 3] = ld_nt(vp + 64);
+    }
+#pragma unroll
+    for (int j2 = 0; j2 < 8; ++j2) acc ^= fold(r[j2]);
+  }
+  if (acc == 0x12345678u) a.out[pos * 16 + h] = acc;
+}
+
 // B: workgroup = (group, quad of 4 heads), 16 waves: wave = (head in quad, run).
 __global__ __launch_bounds__(1024) void probe_quads(Args a) {
   int id = blockIdx.x;
@@ -166,6 +196,7 @@ extern "C" int probe_launch(int variant, const void *k, const void *v, const int
     case 5: probe_slices_ntw<8, 2><<<G * 16, 512, 0, s>>>(a); break;
     case 6: probe_slices_ntw<8, 4><<<G * 16, 512, 0, s>>>(a); break;
     case 7: probe_slices_ntw<16, 2><<<G * 16, 1024, 0, s>>>(a); break;
+    case 8: probe_slices_xcd<<<(G + 7) / 8 * 8 * 16, 256, 0, s>>>(a); break;
     default: return -1;
   }
   return hipGetLastError() == hipSuccess ? 0 : -2;
