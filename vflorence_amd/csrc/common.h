@@ -308,6 +308,15 @@ struct WaveBlockIds {
     end = b1;
     fetch(b0);
   }
+  // Ids 0..63 of a table row `width` entries wide, requested before the row's length
+  // is known (one dependent load level less); limit() then bounds later fetches to the
+  // row's blocks.
+  __device__ __forceinline__ void prefetch(const int32_t *r, int width) {
+    row = r;
+    end = width;
+    fetch(0);
+  }
+  __device__ __forceinline__ void limit(int b1) { end = b1; }
   // b is wave-uniform and b0 <= b < b1.
   __device__ __forceinline__ int get(int b) {
     if (b - base >= 64) fetch(b);

@@ -232,6 +232,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
   if (row0 < 0 || row0 >= num_rows) return;
   nrows = (int)min((int64_t)nrows, num_rows - row0);
   if (nrows <= 0) return;
+  WaveBlockIds ids;
+  ids.prefetch(bt + (int64_t)row0 * bt_stride, max_blocks);
   const int L = seq_lens[row0];
   int nblk = L > 0 ? (L + BS - 1) / BS : 0;  // 16-token chunks
   nblk = min(nblk, max_blocks << bs_shift);
@@ -291,12 +293,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
   for (int c = 0; c < VCH; ++c) acc[c] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   float m = NEG_INF_F, l = 0.f;
 
-  WaveBlockIds ids;
-  if constexpr (SHIFT == 0)
-    ids.init(bt + (int64_t)row0 * bt_stride, b0, b1);
-  else
-    ids.init(bt + (int64_t)row0 * bt_stride, b0 >> SHIFT,
-             b1 > b0 ? ((b1 - 1) >> SHIFT) + 1 : b0 >> SHIFT);
+  ids.limit(b1 > b0 ? ((b1 - 1) >> SHIFT) + 1 : 0);
   constexpr int part_mask = (1 << SHIFT) - 1;
   const int64_t block_elems = (int64_t)H * (BS << bs_shift) * D;
   const int head_off = h * (BS << bs_shift) * D;
