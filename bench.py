@@ -672,16 +672,16 @@ def extra_counter_subjects(torch, wl):
 
 
 GATHER_VARIANTS = {
-    0: "(group, head) slices, group-major workgroup ids, 1024 x 4 waves (the kernel's mapping)",
+    0: "(group, head) slices, consecutive workgroup ids per group, 1024 x 4 waves",
     1: "(group, head) slices, head-major ids, 1024 x 4 waves",
     2: "(group, 4 heads): 8 KiB of a block read together, 256 x 16 waves",
     3: "(group, 4 heads): each wave reads 8 KiB per block, 256 x 4 waves",
     4: "(group, head) slices as 0, non-temporal loads (the attention kernels' hint)",
-    5: "(group, head) slices, non-temporal, 1024 x 8 waves, 2 blocks per iteration "
-       "(the kernel's shape)",
+    5: "(group, head) slices, non-temporal, 1024 x 8 waves, 2 blocks per iteration",
     6: "(group, head) slices, non-temporal, 1024 x 8 waves, 4 blocks per iteration",
     7: "(group, head) slices, non-temporal, 1024 x 16 waves, 2 blocks per iteration",
-    8: "(group, head) slices, non-temporal, a group's 16 heads on one XCD",
+    8: "(group, head) slices, non-temporal, a group's 16 heads on one XCD (the kernel's "
+       "mapping and loads, 1024 x 4 waves, 2 blocks per iteration)",
 }
 
 
