@@ -366,6 +366,44 @@ int vfl_linear(const void *x, int64_t x_stride, const void *packed_weight, const
                void *y, int64_t y_stride, int64_t rows, int out_features, int in_features,
                int flags, int dtype, void *stream);
 
+/*
+ * Deferred LayerNorm across the decoder's projections (no vllm_cpu_attn counterpart:
+ * BART's post-LN sublayers, h' = LN(h + y), vflorence/models/bart.py:259-261).
+ *
+ * vfl_linear_residual: a sublayer's output projection.  y becomes the pre-norm sum
+ *   v[r][n] = rnd(rnd(sum_k x[r][k] W[n][k] + bias[n]) + h[r][n])
+ * (rnd: rounding to the dtype, where the separate projection and residual + LayerNorm
+ * kernels round) and y_stats[r][t] = (mean, sum of squared deviations) of v[r] over
+ * features 32 t .. 32 t + 31.  h is `residual` itself when r_stats is NULL, else
+ * LN(residual) under r_stats, r_gamma, r_beta, r_eps (an earlier call's v and stats).
+ * out_features a multiple of 32; flags: VFL_LINEAR_X_PACKED only; y 8-byte aligned with
+ * a row stride a multiple of 4; y_stats [rows][out_features / 32] float pairs, not
+ * aliasing r_stats.
+ *
+ * vfl_linear_norm: a projection of h' = LN(v) given v and its statistics x_stats
+ * ([rows][in_features / 32] pairs), with the LayerNorm folded into the weight:
+ *   y[r][n] = act(rstd_r * (sum_k v[r][k] W'[n][k] - mean_r * u[n]) + folded_bias[n])
+ * for packed_weight = the packed W' = rnd(W diag(gamma)), u[n] = sum_k W'[n][k] and
+ * folded_bias = bias + W beta (fp32, in the caller's order), where the row's mean and
+ * rstd combine its tiles: mean = sum_t m_t / T, M2 = sum_t M2_t + 32 sum_t (m_t - mean)^2,
+ * rstd = 1 / sqrt(M2 / (32 T) + eps).  flags: VFL_LINEAR_GELU and VFL_LINEAR_Y_PACKED.
+ *
+ * vfl_layer_norm_apply: out = rnd((v - mean) * rstd * gamma + beta) per row from v's
+ * statistics (dim a multiple of 32; 8-byte aligned operands, row strides multiples of 4).
+ */
+int vfl_linear_residual(const void *x, int64_t x_stride, const void *packed_weight,
+                        const void *bias, const void *residual, int64_t r_stride,
+                        const float *r_stats, const void *r_gamma, const void *r_beta,
+                        float r_eps, void *y, int64_t y_stride, float *y_stats, int64_t rows,
+                        int out_features, int in_features, int flags, int dtype, void *stream);
+int vfl_linear_norm(const void *x, int64_t x_stride, const float *x_stats, float eps,
+                    const void *packed_weight, const float *u, const float *folded_bias,
+                    void *y, int64_t y_stride, int64_t rows, int out_features, int in_features,
+                    int flags, int dtype, void *stream);
+int vfl_layer_norm_apply(const void *v, int64_t v_stride, const float *v_stats,
+                         const void *gamma, const void *beta, float eps, void *out,
+                         int64_t out_stride, int64_t rows, int dim, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

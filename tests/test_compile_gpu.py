@@ -125,3 +125,40 @@ def test_compiled_step_writes_the_caches_in_place(dtype):
     assert "vflorence::self_attention" in touching, touching
     assert all(n.startswith("vflorence::") for n in touching), touching
     llm.abort()
+
+
+def test_compiled_deferred_layer_norm_steps_equal_eager_steps():
+    """bf16 at a width the decode-step kernels serve (d_model 256, ffn 1024): the decoder
+    runs with deferred LayerNorms (linear_residual / linear_norm / layer_norm_apply), and
+    the compiled step -- one graph, the custom ops opaque -- gives the eager step's tokens."""
+    from transformers import BartConfig
+
+    from vflorence_amd import LLM, Request, SamplingParams
+    from vflorence_amd.utils.loader import synthetic_state_dict
+
+    cfg = BartConfig(vocab_size=512, d_model=256, encoder_layers=1, decoder_layers=2,
+                     encoder_attention_heads=4, decoder_attention_heads=4,
+                     encoder_ffn_dim=1024, decoder_ffn_dim=1024, max_position_embeddings=256,
+                     bos_token_id=0, pad_token_id=1, eos_token_id=2, decoder_start_token_id=2,
+                     forced_eos_token_id=None, tie_word_embeddings=False)
+    prompts = [[0] + [5 + (7 * i + 3 * r) % 500 for i in range(40 + 9 * r)] + [2]
+               for r in range(6)]
+    params = SamplingParams(max_tokens=12, num_beams=2, repetition_penalty=1.0,
+                            eos_token_id=[2], length_penalty=1.0, no_repeat_ngram_size=0,
+                            min_length=13, forced_bos_token_id=None, forced_eos_token_id=None,
+                            suppress_tokens=[], begin_suppress_tokens=[], early_stopping=True)
+    got = []
+    for compiled in (False, True):
+        torch._dynamo.reset()
+        before = graphs()
+        sd = synthetic_state_dict(cfg, seed=1, device="cuda")
+        llm = LLM(cfg, state_dict=sd, compile=compiled, dtype=torch.bfloat16, max_num_seqs=16,
+                  max_decoder_len=32, max_encoder_len=128)
+        dec = llm.runner.model.model.decoder
+        assert dec.deferred_norms
+        got.append([o.completion_token_ids
+                    for o in llm.generate([Request(p) for p in prompts], params)])
+        if compiled:  # one graph for every step and batch size (counters are per process)
+            assert graphs() - before == 1, graphs() - before
+    assert got[0] == got[1]
+    assert all(len(t) == 12 for t in got[0])

@@ -36,6 +36,9 @@ EXPORTED_SYMBOLS = (
     "vfl_linear_packed_elems",
     "vfl_pack_linear_weight",
     "vfl_linear",
+    "vfl_linear_residual",
+    "vfl_linear_norm",
+    "vfl_layer_norm_apply",
 )
 
 
@@ -110,6 +113,19 @@ _SIGNATURES = {
     "vfl_linear": (
         ctypes.c_int,
         [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "vfl_linear_residual": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _f32, _vp, _i64, _vp, _i64, _i32, _i32,
+         _i32, _i32, _vp],
+    ),
+    "vfl_linear_norm": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _f32, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "vfl_layer_norm_apply": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _vp, _vp, _f32, _vp, _i64, _i64, _i32, _i32, _vp],
     ),
 }
 

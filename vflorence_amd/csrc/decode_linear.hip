@@ -79,14 +79,144 @@ template <int DT> __device__ __forceinline__ float gelu_of_stored(float v) {
   return x * 0.5f * (1.0f + erff(x * 0.70710678118654752440f));
 }
 
+// Deferred LayerNorm across the decoder's projections.  BART's sublayers end in
+// h' = LN(h + y) (post-LN, bart.py:259-261); a separate residual + LayerNorm launch per
+// sublayer costs ~5 us in a decode step's graph, more than its bytes.  Instead:
+// - the sublayer's output projection (LIN_RESIDUAL) stores the pre-norm sum
+//   v = round(round(acc + bias) + h) -- the value the LayerNorm kernel normalizes -- and,
+//   per row and 32-feature tile, the tile's mean and sum of squared deviations;
+// - the projections that read h' (LIN_NORM_IN) multiply v itself, with LayerNorm's
+//   weight folded into their packed weight (W' = W diag(gamma), rounded) and its bias
+//   into theirs (b' = b + W beta), and finish in the epilogue:
+//   y = rstd_r (acc - mean_r u[n]) + b'[n] with u[n] = sum_k W'[n][k];
+// - the residual of the next sublayer is h' itself, normalized element by element in
+//   that sublayer's output projection (or by vfl_layer_norm_apply).
+// A row's mean and 1/std combine its T tiles: mean = sum_t m_t / T,
+// M2 = sum_t M2_t + 32 sum_t (m_t - mean)^2, rstd = 1 / sqrt(M2 / (32 T) + eps).
+constexpr int LIN_PLAIN = 0, LIN_NORM_IN = 1, LIN_RESIDUAL = 2;
+constexpr int LIN_STAT_TILE = 32;   // features per statistics tile
+
+struct LinNorm {
+  const float2 *x_stats;  // LIN_NORM_IN: [rows][K / 32] of x
+  const float *u, *fbias; // LIN_NORM_IN: [N] fp32
+  float eps;
+  const uint16_t *res;    // LIN_RESIDUAL: h, [rows][N] with row stride res_stride
+  int64_t res_stride;
+  const float2 *res_stats;  // null: h is plain; else h = LN(res) with these statistics
+  const uint16_t *res_gamma, *res_beta;
+  float res_eps;
+  float2 *y_stats;        // LIN_RESIDUAL: [rows][N / 32] of the stored v
+};
+
+// The workgroup's 32 rows' means and 1/stds from their T tiles' (mean, M2) at
+// st[row * T + t]: thread (row r = tid / 16, j = tid % 16) takes tiles j, j + 16, ...;
+// the 16 threads of a row (one DPP row of a wave) combine them in a fixed order.
+// Requested after the main loop, so the loads' latency overlaps the partial-tile
+// reduction; results in s_ms[r] = (mean, rstd) before the reduction's last barrier.
+struct RowStatLoads {
+  float2 p[2];
+  __device__ __forceinline__ void issue(const float2 *st, int T, int m0, int M) {
+    const int r = (int)(threadIdx.x >> 4), j = (int)(threadIdx.x & 15);
+    const float2 *row = st + (int64_t)min(m0 + r, M - 1) * T;
+    p[0] = j < T ? row[j] : make_float2(0.f, 0.f);
+    p[1] = j + 16 < T ? row[j + 16] : make_float2(0.f, 0.f);
+  }
+  __device__ __forceinline__ void finish(const float2 *st, int T, int m0, int M, float eps,
+                                         float2 *s_ms) {
+    const int r = (int)(threadIdx.x >> 4), j = (int)(threadIdx.x & 15);
+    const float2 *row = st + (int64_t)min(m0 + r, M - 1) * T;
+    float s = p[0].x + p[1].x;
+    for (int t = j + 32; t < T; t += 16) s += row[t].x;
+    const float mean = group_sum<16>(s) / (float)T;
+    float m2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (j + 16 * i < T) {
+        const float d = p[i].x - mean;
+        m2 += p[i].y + (float)LIN_STAT_TILE * d * d;
+      }
+    }
+    for (int t = j + 32; t < T; t += 16) {
+      const float2 v = row[t];
+      const float d = v.x - mean;
+      m2 += v.y + (float)LIN_STAT_TILE * d * d;
+    }
+    m2 = group_sum<16>(m2);
+    if (j == 0) s_ms[r] = make_float2(mean, rsqrtf(m2 / (float)(LIN_STAT_TILE * T) + eps));
+  }
+};
+
+template <int DT> __device__ __forceinline__ float round_elem(float v) {
+  return Mfma<DT>::widen(Mfma<DT>::narrow(v));
+}
+
+// LIN_RESIDUAL's epilogue, run by all waves of the workgroup (the statistics of a tile
+// row span two finishing waves and meet in LDS).  Finishing wave (qf, qt), lane: row m,
+// features qn .. qn + 3 of the tile at n0.  The values are rounded where the separate
+// projection store and LayerNorm kernel round them: y, the normalized residual, v.
+template <int DT>
+__device__ __forceinline__ void residual_epilogue(
+    const floatx4_t *s_part, int wv, int lane, int qf, int qt, int qn, int m, int M, int N,
+    int n0, const float (&bv)[4], const float (&rs)[4], const float (&ga)[4],
+    const float (&be)[4], const float2 *s_ms, uint16_t *y, int64_t ldy, const LinNorm &nrm) {
+  constexpr int SUB = 4;
+  __shared__ float s_tstat[2][2][2][16];  // [sum, M2][qf][qt][row of the quarter]
+  const bool fin = wv < SUB;
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+  if (fin) {
+    const floatx4_t v = (s_part[wv * 64 + lane] + s_part[(2 * SUB + wv) * 64 + lane]) +
+                        (s_part[(SUB + wv) * 64 + lane] + s_part[(3 * SUB + wv) * 64 + lane]);
+    float mean = 0.f, rstd = 1.f;
+    if (nrm.res_stats) {
+      const float2 ms = s_ms[m % LIN_TILE];  // the workgroup's row m - m0
+      mean = ms.x;
+      rstd = ms.y;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float yj = round_elem<DT>(v[j] + bv[j]);
+      const float hj = nrm.res_stats ? round_elem<DT>((rs[j] - mean) * rstd * ga[j] + be[j])
+                                     : rs[j];
+      o[j] = round_elem<DT>(yj + hj);
+    }
+  }
+  // The tile row's sum: 4 values per lane, the quarter's 4 lanes of the row, then the
+  // two quarters (fixed order); then the same for the squared deviations from its mean.
+  const float qs = rows_sum4((o[0] + o[1]) + (o[2] + o[3]));
+  if (fin && lane < 16) s_tstat[0][qf][qt][lane] = qs;
+  lds_barrier();
+  const float tmean =
+      fin ? (s_tstat[0][0][qt][lane & 15] + s_tstat[0][1][qt][lane & 15]) / (float)LIN_STAT_TILE
+          : 0.f;
+  float dd = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float d = o[j] - tmean;
+    dd = fmaf(d, d, dd);
+  }
+  const float qd = rows_sum4(dd);
+  if (fin && lane < 16) s_tstat[1][qf][qt][lane] = qd;
+  lds_barrier();
+  if (!fin || m >= M) return;
+  *reinterpret_cast<uint2 *>(y + (int64_t)m * ldy + qn) =
+      make_uint2(Mfma<DT>::narrow2(o[0], o[1]), Mfma<DT>::narrow2(o[2], o[3]));
+  if (qf == 0 && lane < 16)
+    nrm.y_stats[(int64_t)m * (N / LIN_STAT_TILE) + n0 / LIN_STAT_TILE] =
+        make_float2(tmean, s_tstat[1][0][qt][lane] + s_tstat[1][1][qt][lane]);
+}
+
 // XP: x is packed (no ds_bpermute); GELU: exact GELU after the bias; YP: y is written
 // packed (rows padded to 32; padding rows are left unwritten); PIPE: batches of
-// LIN_PIPE_BATCH steps, double-buffered (for more than LIN_BATCH steps per wave).
-template <int DT, bool XP, bool GELU, bool YP, bool PIPE>
+// LIN_PIPE_BATCH steps, double-buffered (for more than LIN_BATCH steps per wave);
+// MODE: LIN_PLAIN, LIN_NORM_IN (x is a pre-norm sum, nrm.x_stats its statistics) or
+// LIN_RESIDUAL (y = v and nrm.y_stats, as described above).
+template <int DT, bool XP, bool GELU, bool YP, bool PIPE, int MODE>
 __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
     const uint16_t *__restrict__ x, int64_t ldx, const uint16_t *__restrict__ wp,
     const uint16_t *__restrict__ bias, uint16_t *__restrict__ y, int64_t ldy, int M, int N,
-    int K, bool vec_store) {
+    int K, bool vec_store, LinNorm nrm) {
+  static_assert(MODE != LIN_RESIDUAL || (!GELU && !YP), "the residual epilogue stores v");
+  static_assert(MODE != LIN_NORM_IN || !XP, "a pre-norm x is stored row by row");
   constexpr int FT = LIN_TILE / 16, TT = LIN_TILE / 16;
   constexpr int SUB = FT * TT;  // 16 x 16 quarters of the tile
   constexpr int B = PIPE ? LIN_PIPE_BATCH : LIN_BATCH;
@@ -122,11 +252,10 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
   const int qf = wv / TT, qt = wv % TT;
   const int qn = n0 + 16 * qf + 4 * (lane >> 4);
   float bv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (bias && wv < SUB) {
+  if (bias && wv < SUB && MODE != LIN_NORM_IN) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) bv[j] = qn + j < N ? Mfma<DT>::widen(bias[qn + j]) : 0.f;
   }
-
   floatx4_t acc[FT][TT];
 #pragma unroll
   for (int f = 0; f < FT; ++f)
@@ -182,6 +311,46 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
     }
   }
 
+  // The deferred-LayerNorm epilogues' inputs, requested now so that their latency
+  // overlaps the reduction below: the rows' tile statistics (all threads) and, for the
+  // finishing lanes (row qm, features qn .. qn + 3), the per-feature terms and residual.
+  __shared__ float2 s_ms[MODE == LIN_PLAIN ? 1 : LIN_TILE];
+  RowStatLoads rsl;
+  const float2 *row_st = nullptr;
+  int row_t = 0;
+  float fa[4] = {0.f, 0.f, 0.f, 0.f}, fb[4] = {0.f, 0.f, 0.f, 0.f};  // u, b' or gamma, beta
+  float rs[4] = {0.f, 0.f, 0.f, 0.f};  // residual (or its pre-norm sum)
+  const int qm = min(m0 + 16 * qt + (lane & 15), M - 1);
+  if constexpr (MODE == LIN_NORM_IN) {
+    row_st = nrm.x_stats;
+    row_t = K / LIN_STAT_TILE;
+    if (wv < SUB) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        fa[j] = qn + j < N ? nrm.u[qn + j] : 0.f;
+        fb[j] = qn + j < N ? nrm.fbias[qn + j] : 0.f;
+      }
+    }
+  }
+  if constexpr (MODE == LIN_RESIDUAL) {
+    row_st = nrm.res_stats;  // null: a plain residual
+    row_t = N / LIN_STAT_TILE;
+    if (wv < SUB) {
+      // N is a multiple of 32 here (whole statistics tiles), so qn + 3 < N.
+      const uint16_t *rp = nrm.res + (int64_t)qm * nrm.res_stride + qn;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rs[j] = Mfma<DT>::widen(rp[j]);
+      if (row_st) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          fa[j] = Mfma<DT>::widen(nrm.res_gamma[qn + j]);
+          fb[j] = Mfma<DT>::widen(nrm.res_beta[qn + j]);
+        }
+      }
+    }
+  }
+  if (MODE != LIN_PLAIN && row_st) rsl.issue(row_st, row_t, m0, M);
+
   // Sum the waves' partial tiles: waves 4..7 hand theirs to waves 0..3, which add and
   // publish the four sums.
   if (wv >= LIN_WAVES / 2) {
@@ -205,17 +374,31 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
 #pragma unroll
       for (int t = 0; t < TT; ++t) s_part[(wv * SUB + f * TT + t) * 64 + lane] = acc[f][t];
   }
+  if (MODE != LIN_PLAIN && row_st)
+    rsl.finish(row_st, row_t, m0, M, MODE == LIN_NORM_IN ? nrm.eps : nrm.res_eps, s_ms);
   __syncthreads();
 
-  if (wv >= SUB) return;
   const int m = m0 + 16 * qt + (lane & 15);
+  if constexpr (MODE == LIN_RESIDUAL) {
+    residual_epilogue<DT>(s_part, wv, lane, qf, qt, qn, m, M, N, n0, bv, rs, fa, fb, s_ms, y, ldy,
+                          nrm);
+    return;
+  }
+  if (wv >= SUB) return;
   if (qn >= N || m >= M) return;
   const floatx4_t v = (s_part[wv * 64 + lane] + s_part[(2 * SUB + wv) * 64 + lane]) +
                       (s_part[(SUB + wv) * 64 + lane] + s_part[(3 * SUB + wv) * 64 + lane]);
+  float mean = 0.f, rstd = 1.f;
+  if constexpr (MODE == LIN_NORM_IN) {
+    const float2 ms = s_ms[16 * qt + (lane & 15)];
+    mean = ms.x;
+    rstd = ms.y;
+  }
   uint32_t h[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float o = v[j] + bv[j];
+    const float o = MODE == LIN_NORM_IN ? fmaf(fmaf(-mean, fa[j], v[j]), rstd, fb[j])
+                                        : v[j] + bv[j];
     h[j] = Mfma<DT>::narrow(GELU ? gelu_of_stored<DT>(o) : o);
   }
   if constexpr (YP) {  // 4 consecutive columns of one row: 8 bytes of one lane's chunk
@@ -287,33 +470,37 @@ extern "C" int vfl_pack_linear_weight(const void *weight, int64_t weight_stride,
   return launch_status("pack_linear_weight");
 }
 
-template <bool XP, bool GELU, bool YP, bool PIPE>
+template <bool XP, bool GELU, bool YP, bool PIPE, int MODE>
 static void launch_linear_dt(const dim3 &grid, hipStream_t s, int dtype, const void *x,
                              int64_t x_stride, const void *wp, const void *bias, void *y,
                              int64_t y_stride, int64_t rows, int out_features, int in_features,
-                             bool vec_store) {
+                             bool vec_store, const LinNorm &nrm) {
   if (dtype == VFL_BFLOAT16)
-    decode_linear_kernel<VFL_BFLOAT16, XP, GELU, YP, PIPE><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
+    decode_linear_kernel<VFL_BFLOAT16, XP, GELU, YP, PIPE, MODE>
+        <<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
         (const uint16_t *)x, x_stride, (const uint16_t *)wp, (const uint16_t *)bias,
-        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store, nrm);
   else
-    decode_linear_kernel<VFL_FLOAT16, XP, GELU, YP, PIPE><<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
+    decode_linear_kernel<VFL_FLOAT16, XP, GELU, YP, PIPE, MODE>
+        <<<grid, dim3(64 * LIN_WAVES), 0, s>>>(
         (const uint16_t *)x, x_stride, (const uint16_t *)wp, (const uint16_t *)bias,
-        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store);
+        (uint16_t *)y, y_stride, (int)rows, out_features, in_features, vec_store, nrm);
 }
 
 // More K steps per wave than one batch holds: double-buffered batches.
-template <bool XP, bool GELU, bool YP>
+template <bool XP, bool GELU, bool YP, int MODE = LIN_PLAIN>
 static void launch_linear(const dim3 &grid, hipStream_t s, int dtype, const void *x,
                           int64_t x_stride, const void *wp, const void *bias, void *y,
                           int64_t y_stride, int64_t rows, int out_features, int in_features,
-                          bool vec_store) {
+                          bool vec_store, const LinNorm &nrm = LinNorm{}) {
   if (in_features / LIN_WAVES / 32 > LIN_BATCH)
-    launch_linear_dt<XP, GELU, YP, true>(grid, s, dtype, x, x_stride, wp, bias, y, y_stride,
-                                         rows, out_features, in_features, vec_store);
+    launch_linear_dt<XP, GELU, YP, true, MODE>(grid, s, dtype, x, x_stride, wp, bias, y,
+                                               y_stride, rows, out_features, in_features,
+                                               vec_store, nrm);
   else
-    launch_linear_dt<XP, GELU, YP, false>(grid, s, dtype, x, x_stride, wp, bias, y, y_stride,
-                                          rows, out_features, in_features, vec_store);
+    launch_linear_dt<XP, GELU, YP, false, MODE>(grid, s, dtype, x, x_stride, wp, bias, y,
+                                                y_stride, rows, out_features, in_features,
+                                                vec_store, nrm);
 }
 
 extern "C" int vfl_linear(const void *x, int64_t x_stride, const void *packed_weight,
@@ -380,4 +567,231 @@ extern "C" int vfl_linear(const void *x, int64_t x_stride, const void *packed_we
     VFL_LIN(true, true, true);
 #undef VFL_LIN
   return launch_status("linear");
+}
+
+namespace vfl {
+
+// h = LN(v) from v's tile statistics (the last sublayer's output before the LM head):
+// one wave per row, the row's tiles combined in a fixed order, then the LayerNorm
+// kernel's expression per element.
+template <int DT>
+__global__ __launch_bounds__(128) void layer_norm_apply_kernel(
+    const uint16_t *__restrict__ v, int64_t v_stride, const float2 *__restrict__ st,
+    const uint16_t *__restrict__ gamma, const uint16_t *__restrict__ beta, float eps,
+    uint16_t *__restrict__ out, int64_t out_stride, int64_t rows, int dim) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 2 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // wave-uniform
+  const int T = dim / LIN_STAT_TILE;
+  const float2 *rs = st + row * T;
+  float s = 0.f;
+  for (int t = lane; t < T; t += 64) s += rs[t].x;
+  const float mean = group_sum<64>(s) / (float)T;
+  float m2 = 0.f;
+  for (int t = lane; t < T; t += 64) {
+    const float2 p = rs[t];
+    const float d = p.x - mean;
+    m2 += p.y + (float)LIN_STAT_TILE * d * d;
+  }
+  const float rstd = rsqrtf(group_sum<64>(m2) / (float)dim + eps);
+  for (int i = 4 * lane; i < dim; i += 256) {
+    const uint2 a = *reinterpret_cast<const uint2 *>(v + row * v_stride + i);
+    const uint2 g = *reinterpret_cast<const uint2 *>(gamma + i);
+    const uint2 b = *reinterpret_cast<const uint2 *>(beta + i);
+    const uint32_t aw[2] = {a.x, a.y}, gw[2] = {g.x, g.y}, bw[2] = {b.x, b.y};
+    uint32_t o[2];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const float lo = (Mfma<DT>::widen_lo(aw[w]) - mean) * rstd * Mfma<DT>::widen_lo(gw[w]) +
+                       Mfma<DT>::widen_lo(bw[w]);
+      const float hi = (Mfma<DT>::widen_hi(aw[w]) - mean) * rstd * Mfma<DT>::widen_hi(gw[w]) +
+                       Mfma<DT>::widen_hi(bw[w]);
+      o[w] = Mfma<DT>::narrow2(lo, hi);
+    }
+    *reinterpret_cast<uint2 *>(out + row * out_stride + i) = make_uint2(o[0], o[1]);
+  }
+}
+
+}  // namespace vfl
+
+static int check_norm_rows(int64_t rows, const char *who) {
+  if (rows < 0 || rows > 65535LL * LIN_TILE) {
+    set_error("%s: rows must be in [0, %lld] (got %lld)", who, 65535LL * LIN_TILE,
+              (long long)rows);
+    return rows < 0 ? VFL_E_INVALID : VFL_E_UNSUPPORTED;
+  }
+  return VFL_OK;
+}
+
+extern "C" int vfl_linear_norm(const void *x, int64_t x_stride, const float *x_stats, float eps,
+                               const void *packed_weight, const float *u,
+                               const float *folded_bias, void *y, int64_t y_stride,
+                               int64_t rows, int out_features, int in_features, int flags,
+                               int dtype, void *stream) {
+  clear_error();
+  int st = check_features(out_features, in_features, dtype, "linear_norm");
+  if (st == VFL_OK) st = check_norm_rows(rows, "linear_norm");
+  if (st != VFL_OK) return st;
+  if (flags & ~(VFL_LINEAR_GELU | VFL_LINEAR_Y_PACKED)) {
+    set_error("linear_norm: flags 0x%x (GELU and Y_PACKED only: x is a pre-norm sum)", flags);
+    return VFL_E_INVALID;
+  }
+  const bool yp = flags & VFL_LINEAR_Y_PACKED, gelu = flags & VFL_LINEAR_GELU;
+  if (x_stride < in_features || (!yp && y_stride < out_features) || !(eps >= 0.f)) {
+    set_error("linear_norm: row strides must cover the rows (x %lld y %lld), eps >= 0",
+              (long long)x_stride, (long long)y_stride);
+    return VFL_E_INVALID;
+  }
+  if (yp && out_features % LIN_TILE != 0) {
+    set_error("linear_norm: a packed output needs out_features a multiple of %d (got %d)",
+              LIN_TILE, out_features);
+    return VFL_E_UNSUPPORTED;
+  }
+  if (rows == 0) return VFL_OK;
+  if (!x || !x_stats || !packed_weight || !u || !folded_bias || !y) {
+    set_error("linear_norm: null pointer argument");
+    return VFL_E_INVALID;
+  }
+  if (((uintptr_t)x | (uintptr_t)packed_weight) % 16 != 0 || x_stride % 8 != 0 ||
+      (uintptr_t)x_stats % 8 != 0 || ((uintptr_t)u | (uintptr_t)folded_bias) % 4 != 0 ||
+      (uintptr_t)y % (yp ? 8 : 2) != 0) {
+    set_error("linear_norm: x and the packed weight must be 16-byte aligned, the x row stride "
+              "a multiple of 8 elements, x_stats 8-byte and u / folded_bias 4-byte aligned");
+    return VFL_E_INVALID;
+  }
+  LinNorm nrm{};
+  nrm.x_stats = reinterpret_cast<const float2 *>(x_stats);
+  nrm.u = u;
+  nrm.fbias = folded_bias;
+  nrm.eps = eps;
+  const bool vec_store = (uintptr_t)y % 8 == 0 && y_stride % 4 == 0;
+  const dim3 grid((unsigned)(packed_rows(out_features) / LIN_TILE),
+                  (unsigned)((rows + LIN_TILE - 1) / LIN_TILE));
+  hipStream_t s = (hipStream_t)stream;
+#define VFL_LINN(G, YP)                                                                   \
+  launch_linear<false, G, YP, LIN_NORM_IN>(grid, s, dtype, x, x_stride, packed_weight, nullptr, \
+                                           y, y_stride, rows, out_features, in_features,     \
+                                           vec_store, nrm)
+  if (!gelu && !yp)
+    VFL_LINN(false, false);
+  else if (gelu && yp)
+    VFL_LINN(true, true);
+  else if (gelu)
+    VFL_LINN(true, false);
+  else
+    VFL_LINN(false, true);
+#undef VFL_LINN
+  return launch_status("linear_norm");
+}
+
+extern "C" int vfl_linear_residual(const void *x, int64_t x_stride, const void *packed_weight,
+                                   const void *bias, const void *residual, int64_t r_stride,
+                                   const float *r_stats, const void *r_gamma,
+                                   const void *r_beta, float r_eps, void *y, int64_t y_stride,
+                                   float *y_stats, int64_t rows, int out_features,
+                                   int in_features, int flags, int dtype, void *stream) {
+  clear_error();
+  int st = check_features(out_features, in_features, dtype, "linear_residual");
+  if (st == VFL_OK) st = check_norm_rows(rows, "linear_residual");
+  if (st != VFL_OK) return st;
+  if (flags & ~VFL_LINEAR_X_PACKED) {
+    set_error("linear_residual: flags 0x%x (X_PACKED only: y is the pre-norm sum)", flags);
+    return VFL_E_INVALID;
+  }
+  const bool xp = flags & VFL_LINEAR_X_PACKED;
+  if (out_features % LIN_STAT_TILE != 0) {
+    set_error("linear_residual: out_features must be a multiple of %d (got %d)", LIN_STAT_TILE,
+              out_features);
+    return VFL_E_UNSUPPORTED;
+  }
+  if ((!xp && x_stride < in_features) || y_stride < out_features || r_stride < out_features ||
+      (r_stats && !(r_eps >= 0.f))) {
+    set_error("linear_residual: row strides must cover the rows (x %lld y %lld residual %lld)",
+              (long long)x_stride, (long long)y_stride, (long long)r_stride);
+    return VFL_E_INVALID;
+  }
+  if (rows == 0) return VFL_OK;
+  if (!x || !packed_weight || !residual || !y || !y_stats ||
+      (r_stats && (!r_gamma || !r_beta))) {
+    set_error("linear_residual: null pointer argument");
+    return VFL_E_INVALID;
+  }
+  if ((const void *)y_stats == (const void *)r_stats) {
+    set_error("linear_residual: y_stats must not alias r_stats (every workgroup of a row "
+              "reads the residual's statistics)");
+    return VFL_E_INVALID;
+  }
+  if (((uintptr_t)x | (uintptr_t)packed_weight) % 16 != 0 || (!xp && x_stride % 8 != 0) ||
+      (uintptr_t)y % 8 != 0 || y_stride % 4 != 0 || (uintptr_t)bias % 2 != 0 ||
+      (uintptr_t)residual % 2 != 0 || ((uintptr_t)y_stats | (uintptr_t)r_stats) % 8 != 0 ||
+      ((uintptr_t)r_gamma | (uintptr_t)r_beta) % 2 != 0) {
+    set_error("linear_residual: x and the packed weight must be 16-byte aligned (x row "
+              "stride a multiple of 8 elements), y 8-byte aligned with a row stride a "
+              "multiple of 4, the statistics 8-byte aligned");
+    return VFL_E_INVALID;
+  }
+  LinNorm nrm{};
+  nrm.res = (const uint16_t *)residual;
+  nrm.res_stride = r_stride;
+  nrm.res_stats = reinterpret_cast<const float2 *>(r_stats);
+  nrm.res_gamma = (const uint16_t *)r_gamma;
+  nrm.res_beta = (const uint16_t *)r_beta;
+  nrm.res_eps = r_eps;
+  nrm.y_stats = reinterpret_cast<float2 *>(y_stats);
+  const dim3 grid((unsigned)(out_features / LIN_TILE),
+                  (unsigned)((rows + LIN_TILE - 1) / LIN_TILE));
+  hipStream_t s = (hipStream_t)stream;
+  if (xp)
+    launch_linear<true, false, false, LIN_RESIDUAL>(grid, s, dtype, x, 0, packed_weight, bias, y,
+                                                    y_stride, rows, out_features, in_features,
+                                                    true, nrm);
+  else
+    launch_linear<false, false, false, LIN_RESIDUAL>(grid, s, dtype, x, x_stride, packed_weight,
+                                                     bias, y, y_stride, rows, out_features,
+                                                     in_features, true, nrm);
+  return launch_status("linear_residual");
+}
+
+extern "C" int vfl_layer_norm_apply(const void *v, int64_t v_stride, const float *v_stats,
+                                    const void *gamma, const void *beta, float eps, void *out,
+                                    int64_t out_stride, int64_t rows, int dim, int dtype,
+                                    void *stream) {
+  clear_error();
+  if (dtype != VFL_BFLOAT16 && dtype != VFL_FLOAT16) {
+    set_error("layer_norm_apply: dtype %d has no kernel (bf16 and fp16 only)", dtype);
+    return VFL_E_UNSUPPORTED;
+  }
+  if (rows < 0 || dim <= 0 || dim % LIN_STAT_TILE != 0 || v_stride < dim ||
+      out_stride < dim || !(eps >= 0.f)) {
+    set_error("layer_norm_apply: bad sizes (rows %lld dim %d, a multiple of %d; strides "
+              "covering dim; eps >= 0)", (long long)rows, dim, LIN_STAT_TILE);
+    return VFL_E_INVALID;
+  }
+  if (rows == 0) return VFL_OK;
+  if (rows > 2LL * 2147483647LL) {
+    set_error("layer_norm_apply: too many rows");
+    return VFL_E_UNSUPPORTED;
+  }
+  if (!v || !v_stats || !gamma || !beta || !out) {
+    set_error("layer_norm_apply: null pointer argument");
+    return VFL_E_INVALID;
+  }
+  if (((uintptr_t)v | (uintptr_t)out | (uintptr_t)gamma | (uintptr_t)beta |
+       (uintptr_t)v_stats) % 8 != 0 || v_stride % 4 != 0 || out_stride % 4 != 0) {
+    set_error("layer_norm_apply: v, out, gamma, beta and v_stats must be 8-byte aligned and "
+              "the row strides multiples of 4 elements");
+    return VFL_E_INVALID;
+  }
+  const dim3 grid((unsigned)((rows + 1) / 2));
+  hipStream_t s = (hipStream_t)stream;
+  const float2 *st = reinterpret_cast<const float2 *>(v_stats);
+  if (dtype == VFL_BFLOAT16)
+    layer_norm_apply_kernel<VFL_BFLOAT16><<<grid, dim3(128), 0, s>>>(
+        (const uint16_t *)v, v_stride, st, (const uint16_t *)gamma, (const uint16_t *)beta, eps,
+        (uint16_t *)out, out_stride, rows, dim);
+  else
+    layer_norm_apply_kernel<VFL_FLOAT16><<<grid, dim3(128), 0, s>>>(
+        (const uint16_t *)v, v_stride, st, (const uint16_t *)gamma, (const uint16_t *)beta, eps,
+        (uint16_t *)out, out_stride, rows, dim);
+  return launch_status("layer_norm_apply");
 }

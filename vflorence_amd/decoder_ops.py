@@ -162,6 +162,181 @@ def _(x, packed_weight, bias, out_features, rows=-1, flags=0):
     return x.new_empty(*lead, out_features)
 
 
+# Deferred LayerNorm (vfl_linear_residual / vfl_linear_norm / vfl_layer_norm_apply): a
+# post-LN sublayer's output h' = LN(v) travels as the pre-norm sum v and per-row,
+# per-32-feature (mean, sum of squared deviations) statistics; its consumers fold the
+# LayerNorm into their weights and finish it in their epilogue.
+STAT_TILE = 32
+
+
+def fold_layer_norm(weight: torch.Tensor, bias: torch.Tensor | None, gamma: torch.Tensor,
+                    beta: torch.Tensor, out: tuple | None = None) -> tuple:
+    """The operands of ``linear_norm`` for ``linear(LN(v))`` with this LayerNorm's
+    ``gamma`` / ``beta``: the packed ``W' = rnd(W diag(gamma))``, ``u = sum_k W'[:, k]``
+    and ``b' = bias + W beta`` (both fp32).  With ``out`` (an earlier result of the same
+    shapes) they are rewritten in place, so HIP graphs captured over them stay valid."""
+    _require_gpu(weight, gamma, beta)
+    if gamma.shape != (weight.shape[1],) or beta.shape != gamma.shape:
+        raise ValueError("fold_layer_norm: gamma / beta must be [in_features]")
+    with torch.no_grad():
+        w32 = weight.float()
+        folded = (w32 * gamma.float()).to(weight.dtype)
+        u = folded.float().sum(dim=1)
+        fb = w32 @ beta.float()
+        if bias is not None:
+            fb = fb + bias.float()
+        if out is None:
+            return pack_linear_weight(folded), u, fb
+        packed, u_out, fb_out = out
+        pack_linear_weight(folded, out=packed)
+        u_out.copy_(u)
+        fb_out.copy_(fb)
+        return out
+
+
+def _stats_shape(rows: int, features: int) -> tuple:
+    return (rows, features // STAT_TILE, 2)
+
+
+@torch.library.custom_op("vflorence_amd::linear_residual", mutates_args=())
+def linear_residual(x: torch.Tensor, packed_weight: torch.Tensor, bias: torch.Tensor | None,
+                    residual: torch.Tensor, r_stats: torch.Tensor | None,
+                    r_gamma: torch.Tensor | None, r_beta: torch.Tensor | None, r_eps: float,
+                    out_features: int, rows: int = -1,
+                    flags: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """A post-LN sublayer's output projection: ``v = rnd(rnd(x @ W.T + bias) + h)`` with
+    h = ``residual`` (r_stats None) or LN(residual) under r_stats / r_gamma / r_beta /
+    r_eps, and v's tile statistics.  x is ``[rows, in]`` (or, with ``LINEAR_X_PACKED``, a
+    packed activation of ``rows`` rows); residual and v are ``[rows, out_features]``."""
+    dev = _require_gpu(x, packed_weight, residual)
+    padded_out = (out_features + 31) // 32 * 32
+    if (out_features <= 0 or out_features % STAT_TILE or packed_weight.dim() != 1
+            or packed_weight.numel() % padded_out):
+        raise ValueError("linear_residual: packed_weight must hold a packed [out, in] weight "
+                         f"with out a multiple of {STAT_TILE}")
+    in_features = packed_weight.numel() // padded_out
+    if flags & ~LINEAR_X_PACKED:
+        raise ValueError("linear_residual: only LINEAR_X_PACKED applies")
+    if flags & LINEAR_X_PACKED:
+        if rows <= 0 or x.dim() != 1 or x.numel() != packed_elems(rows, in_features):
+            raise ValueError(f"linear_residual: x is not a packed [{rows}, {in_features}] "
+                             "activation")
+        x2, x_stride = x, 0
+    else:
+        if x.dim() != 2 or x.shape[1] != in_features:
+            raise ValueError(f"linear_residual: x must be [rows, {in_features}]")
+        x2 = x if x.stride(-1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 \
+            else x.contiguous()
+        rows, x_stride = x2.shape[0], x2.stride(0)
+    if residual.shape != (rows, out_features) or residual.stride(-1) != 1:
+        raise ValueError(f"linear_residual: residual must be [{rows}, {out_features}], unit "
+                         "stride")
+    dt = x.dtype
+    if packed_weight.dtype != dt or residual.dtype != dt or (bias is not None
+                                                             and bias.dtype != dt):
+        raise ValueError("linear_residual: x, weight, bias and residual must share one dtype")
+    if r_stats is not None:
+        if (r_gamma is None or r_beta is None or r_stats.dtype != torch.float32
+                or r_stats.shape != _stats_shape(rows, out_features)
+                or not r_stats.is_contiguous() or r_gamma.shape != (out_features,)
+                or r_beta.shape != (out_features,)):
+            raise ValueError("linear_residual: r_stats [rows, out/32, 2] float32 and gamma / "
+                             "beta [out] describe a deferred residual")
+    v = torch.empty(rows, out_features, dtype=dt, device=dev)
+    stats = torch.empty(_stats_shape(rows, out_features), dtype=torch.float32, device=dev)
+    g = None if r_gamma is None else r_gamma.contiguous()
+    b = None if r_beta is None else r_beta.contiguous()
+    check(lib.vfl_linear_residual(
+        x2.data_ptr(), x_stride, packed_weight.data_ptr(),
+        None if bias is None else bias.contiguous().data_ptr(), residual.data_ptr(),
+        residual.stride(0), None if r_stats is None else r_stats.data_ptr(),
+        None if g is None else g.data_ptr(), None if b is None else b.data_ptr(), r_eps,
+        v.data_ptr(), v.stride(0), stats.data_ptr(), rows, out_features, in_features, flags,
+        _dtype_code(dt), _stream(dev)))
+    return v, stats
+
+
+@linear_residual.register_fake
+def _(x, packed_weight, bias, residual, r_stats, r_gamma, r_beta, r_eps, out_features,
+      rows=-1, flags=0):
+    n = rows if flags & LINEAR_X_PACKED else x.shape[0]
+    return (x.new_empty(n, out_features),
+            x.new_empty(_stats_shape(n, out_features), dtype=torch.float32))
+
+
+@torch.library.custom_op("vflorence_amd::linear_norm", mutates_args=())
+def linear_norm(x: torch.Tensor, x_stats: torch.Tensor, eps: float,
+                packed_weight: torch.Tensor, u: torch.Tensor, folded_bias: torch.Tensor,
+                out_features: int, flags: int = 0) -> torch.Tensor:
+    """``act(LN(x) @ W.T + bias)`` for a pre-norm sum x ``[rows, in]`` with its tile
+    statistics, given ``fold_layer_norm``'s operands (LN's eps here); ``LINEAR_GELU``
+    and ``LINEAR_Y_PACKED`` as for ``linear``."""
+    dev = _require_gpu(x, x_stats, packed_weight, u, folded_bias)
+    padded_out = (out_features + 31) // 32 * 32
+    if out_features <= 0 or packed_weight.dim() != 1 or packed_weight.numel() % padded_out:
+        raise ValueError(f"linear_norm: packed_weight does not hold a packed [{out_features}, "
+                         "in] weight")
+    in_features = packed_weight.numel() // padded_out
+    if flags & ~(LINEAR_GELU | LINEAR_Y_PACKED):
+        raise ValueError("linear_norm: only LINEAR_GELU and LINEAR_Y_PACKED apply")
+    if x.dim() != 2 or x.shape[1] != in_features or x.stride(-1) != 1 or x.stride(0) % 8 \
+            or x.data_ptr() % 16:
+        raise ValueError(f"linear_norm: x must be [rows, {in_features}], unit stride, 16-byte "
+                         "aligned rows")
+    rows = x.shape[0]
+    if (x_stats.dtype != torch.float32 or x_stats.shape != _stats_shape(rows, in_features)
+            or not x_stats.is_contiguous()):
+        raise ValueError("linear_norm: x_stats must be [rows, in/32, 2] float32")
+    if (u.shape != (out_features,) or folded_bias.shape != (out_features,)
+            or u.dtype != torch.float32 or folded_bias.dtype != torch.float32):
+        raise ValueError("linear_norm: u / folded_bias must be [out_features] float32")
+    if packed_weight.dtype != x.dtype:
+        raise ValueError("linear_norm: x and the weight must share one dtype")
+    if flags & LINEAR_Y_PACKED:
+        out = torch.empty(packed_elems(rows, out_features), dtype=x.dtype, device=dev)
+        y_stride = 0
+    else:
+        out = torch.empty(rows, out_features, dtype=x.dtype, device=dev)
+        y_stride = out.stride(0)
+    check(lib.vfl_linear_norm(x.data_ptr(), x.stride(0), x_stats.data_ptr(), eps,
+                              packed_weight.data_ptr(), u.contiguous().data_ptr(),
+                              folded_bias.contiguous().data_ptr(), out.data_ptr(), y_stride,
+                              rows, out_features, in_features, flags, _dtype_code(x.dtype),
+                              _stream(dev)))
+    return out
+
+
+@linear_norm.register_fake
+def _(x, x_stats, eps, packed_weight, u, folded_bias, out_features, flags=0):
+    if flags & LINEAR_Y_PACKED:
+        return x.new_empty(packed_elems(x.shape[0], out_features))
+    return x.new_empty(x.shape[0], out_features)
+
+
+@torch.library.custom_op("vflorence_amd::layer_norm_apply", mutates_args=())
+def layer_norm_apply(v: torch.Tensor, stats: torch.Tensor, gamma: torch.Tensor,
+                     beta: torch.Tensor, eps: float) -> torch.Tensor:
+    """LN(v) from v's tile statistics (v ``[rows, dim]``, dim a multiple of 32)."""
+    dev = _require_gpu(v, stats, gamma, beta)
+    rows, dim = v.shape
+    if (stats.dtype != torch.float32 or stats.shape != _stats_shape(rows, dim)
+            or not stats.is_contiguous() or gamma.shape != (dim,) or beta.shape != (dim,)):
+        raise ValueError("layer_norm_apply: stats [rows, dim/32, 2] float32, gamma / beta [dim]")
+    v2 = v if v.stride(-1) == 1 and v.stride(0) % 4 == 0 and v.data_ptr() % 8 == 0 \
+        else v.contiguous()
+    out = torch.empty(rows, dim, dtype=v.dtype, device=dev)
+    check(lib.vfl_layer_norm_apply(v2.data_ptr(), v2.stride(0), stats.data_ptr(),
+                                   gamma.contiguous().data_ptr(), beta.contiguous().data_ptr(),
+                                   eps, out.data_ptr(), out.stride(0), rows, dim,
+                                   _dtype_code(v.dtype), _stream(dev)))
+    return out
+
+
+@layer_norm_apply.register_fake
+def _(v, stats, gamma, beta, eps):
+    return v.new_empty(v.shape)
+
+
 class TopkRules:
     """The history-free generation rules of one SamplingParams, packed for the kernel:
     a device int32 array ``[eos | suppressed | begin-suppressed | forced BOS | forced EOS]``

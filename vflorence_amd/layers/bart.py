@@ -19,6 +19,7 @@ positions)`` over one token per running sequence.
 from __future__ import annotations
 
 import math
+from typing import NamedTuple
 
 import torch
 import torch.nn.functional as F
@@ -38,6 +39,29 @@ def _residual_norm(h: torch.Tensor, y: torch.Tensor, norm: nn.LayerNorm) -> torc
     return norm(h + y)
 
 
+class PreNorm(NamedTuple):
+    """A post-LN sublayer's output h' = LN(v) before its LayerNorm is applied: the
+    pre-norm sum ``v`` ``[rows, d]``, its per-row, per-32-feature (mean, sum of squared
+    deviations) ``stats`` ``[rows, d / 32, 2]`` and the LayerNorm's parameters.  The
+    projections that read h' finish the normalization in their epilogue (their weights
+    fold gamma and beta) and the next sublayer's output projection normalizes it as its
+    residual, so no separate LayerNorm launch runs between the decoder's sublayers."""
+    v: torch.Tensor
+    stats: torch.Tensor
+    gamma: torch.Tensor
+    beta: torch.Tensor
+    eps: float
+
+
+def apply_pre_norm(h: "PreNorm | torch.Tensor") -> torch.Tensor:
+    """The normalized tensor of a PreNorm (a plain tensor is returned as is)."""
+    if isinstance(h, PreNorm):
+        from ..decoder_ops import layer_norm_apply
+
+        return layer_norm_apply(h.v, h.stats, h.gamma, h.beta, h.eps)
+    return h
+
+
 class DecodeLinear(nn.Linear):
     """nn.Linear whose decode-step calls -- at most 256 rows on the GPU times a 16-bit
     weight of up to 3072 outputs and 4096 inputs -- run on the split-K kernel
@@ -55,6 +79,19 @@ class DecodeLinear(nn.Linear):
         super().__init__(*args, **kwargs)
         self._packed = None
         self._packed_key = None
+        # The LayerNorm whose output this projection reads, when that output arrives as a
+        # PreNorm (held in a tuple: a reference, not a submodule), and the operands with
+        # it folded in (fold_layer_norm), refreshed by repack.
+        self._in_norm = ()
+        self._folded = None
+        self._folded_key = None
+
+    def set_input_norm(self, norm: nn.LayerNorm | None) -> None:
+        """Declare the LayerNorm whose output this projection reads (None: its input is
+        a plain tensor), so that it can take that input as a PreNorm."""
+        self._in_norm = () if norm is None else (norm,)
+        self._folded = None
+        self._folded_key = None
 
     def _weight_key(self):
         w = self.weight
@@ -71,6 +108,7 @@ class DecodeLinear(nn.Linear):
                 and decoder_ops.linear_fits(1, w, max_in=None, max_out=None)):
             self._packed = None
             self._packed_key = self._weight_key()
+            self._refold()
             return
         out = self._packed
         if out is not None and (out.dtype != w.dtype or out.device != w.device
@@ -79,6 +117,42 @@ class DecodeLinear(nn.Linear):
         with torch.no_grad():
             self._packed = decoder_ops.pack_linear_weight(w.detach(), out=out)
         self._packed_key = self._weight_key()
+        self._refold()
+
+    def _fold_key(self):
+        norm = self._in_norm[0]
+        return (self._weight_key(),) + tuple(
+            (t.data_ptr(), None if t.is_inference() else t._version)
+            for t in (norm.weight, norm.bias) + (() if self.bias is None else (self.bias,)))
+
+    def _refold(self) -> None:
+        """Fold the input LayerNorm into a copy of the packed weight and the bias (in
+        place when a copy of the right size exists)."""
+        if not self._in_norm or self._packed is None:
+            self._folded = None
+            self._folded_key = None
+            return
+        from .. import decoder_ops
+
+        norm = self._in_norm[0]
+        out = self._folded
+        if out is not None and out[0].numel() != self._packed.numel():
+            out = None
+        self._folded = decoder_ops.fold_layer_norm(self.weight.detach(), None if self.bias is None
+                                                   else self.bias.detach(), norm.weight.detach(),
+                                                   norm.bias.detach(), out=out)
+        self._folded_key = self._fold_key()
+
+    def folded_operands(self, rows: int, max_in: int | None = LINEAR_MAX_IN,
+                        max_out: int | None = LINEAR_MAX_OUT):
+        """(packed W', u, b') for a PreNorm input of ``rows`` rows, or None when this
+        projection has no input LayerNorm or the kernel does not serve the call."""
+        if not self._in_norm or self.kernel_weight(rows, max_in, max_out) is None:
+            return None
+        if not torch.compiler.is_compiling() and (self._folded_key is None
+                                                  or self._fold_key() != self._folded_key):
+            self._refold()
+        return self._folded
 
     def packed_weight(self) -> torch.Tensor | None:
         """The weight in the kernel's packed layout (None when the kernel cannot take
@@ -109,6 +183,36 @@ class DecodeLinear(nn.Linear):
 
                 return decoder_ops.linear(x, packed, self.bias, self.out_features)
         return F.linear(x, self.weight, self.bias)
+
+    def project(self, h: "PreNorm | torch.Tensor", flags: int = 0,
+                max_out: int | None = LINEAR_MAX_OUT) -> torch.Tensor:
+        """This projection of h, a plain tensor or a PreNorm of this projection's input
+        LayerNorm (the deferred path; the caller has checked ``folded_operands``)."""
+        from .. import decoder_ops
+
+        if isinstance(h, PreNorm):
+            packed, u, fb = self.folded_operands(h.v.shape[0], max_out=max_out)
+            return decoder_ops.linear_norm(h.v, h.stats, h.eps, packed, u, fb,
+                                           self.out_features, flags)
+        packed = self.kernel_weight(h.shape[0], max_out=max_out)
+        return decoder_ops.linear(h, packed, self.bias, self.out_features, flags=flags)
+
+    def project_residual(self, x: torch.Tensor, residual: "PreNorm | torch.Tensor",
+                         norm: nn.LayerNorm, rows: int = -1, flags: int = 0,
+                         max_in: int | None = LINEAR_MAX_IN) -> PreNorm:
+        """``norm(residual + self(x))`` as a PreNorm (post-LN sublayer output)."""
+        from .. import decoder_ops
+
+        n = rows if flags & decoder_ops.LINEAR_X_PACKED else x.shape[0]
+        packed = self.kernel_weight(n, max_in=max_in)
+        if isinstance(residual, PreNorm):
+            v, st = decoder_ops.linear_residual(x, packed, self.bias, residual.v, residual.stats,
+                                                residual.gamma, residual.beta, residual.eps,
+                                                self.out_features, rows, flags)
+        else:
+            v, st = decoder_ops.linear_residual(x, packed, self.bias, residual, None, None, None,
+                                                0.0, self.out_features, rows, flags)
+        return PreNorm(v, st, norm.weight, norm.bias, norm.eps)
 
 
 def _activation(name: str):
@@ -180,10 +284,17 @@ class BartDecoderSelfAttention(_Heads):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         n = x.shape[0]
-        q, k, v = (t.view(n, self.num_heads, self.head_dim)
-                   for t in self.qkv_proj(x).chunk(3, dim=-1))
+        return self.out_proj(self._attend(self.qkv_proj(x), n))
+
+    def _attend(self, qkv: torch.Tensor, n: int) -> torch.Tensor:
+        q, k, v = (t.view(n, self.num_heads, self.head_dim) for t in qkv.chunk(3, dim=-1))
         out = decoder_self_attention(q, k, v, self.k_cache, self.v_cache, self.scaling)
-        return self.out_proj(out.view(n, self.embed_dim))
+        return out.view(n, self.embed_dim)
+
+    def attend(self, h: "PreNorm | torch.Tensor") -> torch.Tensor:
+        """The attention output ``[n, d]`` before ``out_proj``, for the deferred path."""
+        n = (h.v if isinstance(h, PreNorm) else h).shape[0]
+        return self._attend(self.qkv_proj.project(h), n)
 
 
 class BartDecoderCrossAttention(_Heads):
@@ -200,10 +311,17 @@ class BartDecoderCrossAttention(_Heads):
         self.k_cache = self.v_cache = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        n = x.shape[0]
-        q = self.q_proj(x).view(n, self.num_heads, self.head_dim)
-        out = decoder_cross_attention(q, self.layer_idx, self.scaling)
-        return self.out_proj(out.view(n, self.embed_dim))
+        return self.out_proj(self._attend(self.q_proj(x)))
+
+    def _attend(self, q: torch.Tensor) -> torch.Tensor:
+        n = q.shape[0]
+        out = decoder_cross_attention(q.view(n, self.num_heads, self.head_dim), self.layer_idx,
+                                      self.scaling)
+        return out.view(n, self.embed_dim)
+
+    def attend(self, h: "PreNorm | torch.Tensor") -> torch.Tensor:
+        """The attention output ``[n, d]`` before ``out_proj``, for the deferred path."""
+        return self._attend(self.q_proj.project(h))
 
 
 class BartEncoderLayer(nn.Module):
@@ -260,6 +378,36 @@ class BartDecoderLayer(nn.Module):
         h = _residual_norm(h, self.encoder_attn(h), self.encoder_attn_layer_norm)
         return _residual_norm(h, self._feed_forward(h), self.final_layer_norm)
 
+    def deferred_ready(self, h: "PreNorm | torch.Tensor", rows: int) -> bool:
+        """Whether this layer's decode step can run with deferred LayerNorms for an input
+        h of ``rows`` rows: every projection on the kernels, the LayerNorm-reading ones
+        with their folded weights, exact GELU, 16-bit, d a multiple of 32."""
+        sa, ca = self.self_attn, self.encoder_attn
+        if not self._exact_gelu or sa.embed_dim % 32:
+            return False
+        qkv = (sa.qkv_proj.folded_operands(rows) if isinstance(h, PreNorm)
+               else sa.qkv_proj.kernel_weight(rows))
+        return (qkv is not None and ca.q_proj.folded_operands(rows) is not None
+                and self.fc1.folded_operands(rows, max_out=None) is not None
+                and sa.out_proj.kernel_weight(rows) is not None
+                and ca.out_proj.kernel_weight(rows) is not None
+                and self.fc2.kernel_weight(rows, max_in=None) is not None)
+
+    def forward_deferred(self, h: "PreNorm | torch.Tensor") -> PreNorm:
+        """The layer on the decode step's kernels with each sublayer's LayerNorm deferred
+        to the projections that read its output (``deferred_ready`` said yes): 6 launches
+        of vfl_linear_* and the two attention ops, no LayerNorm launch.  Returns the
+        final LayerNorm's input as a PreNorm."""
+        from .. import decoder_ops as ops
+
+        sa, ca = self.self_attn, self.encoder_attn
+        rows = (h.v if isinstance(h, PreNorm) else h).shape[0]
+        h1 = sa.out_proj.project_residual(sa.attend(h), h, self.self_attn_layer_norm)
+        h2 = ca.out_proj.project_residual(ca.attend(h1), h1, self.encoder_attn_layer_norm)
+        mid = self.fc1.project(h2, flags=ops.LINEAR_GELU | ops.LINEAR_Y_PACKED, max_out=None)
+        return self.fc2.project_residual(mid, h2, self.final_layer_norm, rows=rows,
+                                         flags=ops.LINEAR_X_PACKED, max_in=None)
+
 
 def _embed_scale(config) -> float:
     return math.sqrt(config.d_model) if config.scale_embedding else 1.0
@@ -292,10 +440,29 @@ class BartDecoder(nn.Module):
         self.layers = nn.ModuleList(BartDecoderLayer(config, i)
                                     for i in range(config.decoder_layers))
         self.layernorm_embedding = nn.LayerNorm(d)
+        # Decode steps on the GPU defer each sublayer's LayerNorm to the projections that
+        # read its output (PreNorm); False runs the separate residual + LayerNorm kernel.
+        self.deferred_norms = True
+        # The LayerNorm each projection reads (for the deferred path): the first layer's
+        # q|k|v reads the embedding LayerNorm's output as a plain tensor.
+        for i, layer in enumerate(self.layers):
+            if i > 0:
+                layer.self_attn.qkv_proj.set_input_norm(self.layers[i - 1].final_layer_norm)
+            layer.encoder_attn.q_proj.set_input_norm(layer.self_attn_layer_norm)
+            layer.fc1.set_input_norm(layer.encoder_attn_layer_norm)
 
     def forward(self, input_ids, positions):
         h = _residual_norm(self.embed_tokens(input_ids), self.embed_positions(positions),
                            self.layernorm_embedding)
+        rows = h.shape[0]
+        if (h.is_cuda and h.dim() == 2 and h.dtype in (torch.bfloat16, torch.float16)
+                and self.deferred_norms):
+            for layer in self.layers:
+                if not layer.deferred_ready(h, rows):
+                    h = layer(apply_pre_norm(h))
+                else:
+                    h = layer.forward_deferred(h)
+            return apply_pre_norm(h)
         for layer in self.layers:
             h = layer(h)
         return h
