@@ -376,9 +376,9 @@ int vfl_linear(const void *x, int64_t x_stride, const void *packed_weight, const
  * kernels round) and y_stats[r][t] = (mean, sum of squared deviations) of v[r] over
  * features 32 t .. 32 t + 31.  h is `residual` itself when r_stats is NULL, else
  * LN(residual) under r_stats, r_gamma, r_beta, r_eps (an earlier call's v and stats).
- * out_features a multiple of 32; flags: VFL_LINEAR_X_PACKED only; y 8-byte aligned with
- * a row stride a multiple of 4; y_stats [rows][out_features / 32] float pairs, not
- * aliasing r_stats.
+ * out_features a multiple of 32; flags: VFL_LINEAR_X_PACKED only; y and residual 8-byte
+ * aligned with row strides multiples of 4, r_gamma / r_beta 8-byte aligned; y_stats
+ * [rows][out_features / 32] float pairs, not aliasing r_stats.
  *
  * vfl_linear_norm: a projection of h' = LN(v) given v and its statistics x_stats
  * ([rows][in_features / 32] pairs), with the LayerNorm folded into the weight:

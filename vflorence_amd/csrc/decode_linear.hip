@@ -100,6 +100,7 @@ struct LinNorm {
   const float2 *x_stats;  // LIN_NORM_IN: [rows][K / 32] of x
   const float *u, *fbias; // LIN_NORM_IN: [N] fp32
   float eps;
+  bool vec4;              // LIN_NORM_IN: u and fbias 16-byte aligned
   const uint16_t *res;    // LIN_RESIDUAL: h, [rows][N] with row stride res_stride
   int64_t res_stride;
   const float2 *res_stats;  // null: h is plain; else h = LN(res) with these statistics
@@ -150,59 +151,89 @@ template <int DT> __device__ __forceinline__ float round_elem(float v) {
   return Mfma<DT>::widen(Mfma<DT>::narrow(v));
 }
 
-// LIN_RESIDUAL's epilogue, run by all waves of the workgroup (the statistics of a tile
-// row span two finishing waves and meet in LDS).  Finishing wave (qf, qt), lane: row m,
-// features qn .. qn + 3 of the tile at n0.  The values are rounded where the separate
-// projection store and LayerNorm kernel round them: y, the normalized residual, v.
-template <int DT>
-__device__ __forceinline__ void residual_epilogue(
-    const floatx4_t *s_part, int wv, int lane, int qf, int qt, int qn, int m, int M, int N,
-    int n0, const float (&bv)[4], const float (&rs)[4], const float (&ga)[4],
-    const float (&be)[4], const float2 *s_ms, uint16_t *y, int64_t ldy, const LinNorm &nrm) {
-  constexpr int SUB = 4;
-  __shared__ float s_tstat[2][2][2][16];  // [sum, M2][qf][qt][row of the quarter]
-  const bool fin = wv < SUB;
-  float o[4] = {0.f, 0.f, 0.f, 0.f};
-  if (fin) {
-    const floatx4_t v = (s_part[wv * 64 + lane] + s_part[(2 * SUB + wv) * 64 + lane]) +
-                        (s_part[(SUB + wv) * 64 + lane] + s_part[(3 * SUB + wv) * 64 + lane]);
-    float mean = 0.f, rstd = 1.f;
-    if (nrm.res_stats) {
-      const float2 ms = s_ms[m % LIN_TILE];  // the workgroup's row m - m0
-      mean = ms.x;
-      rstd = ms.y;
+// LIN_RESIDUAL's epilogue inputs and epilogue.  Finishing wave w < 2 takes token
+// quarter w and both feature quarters of the tile, so each lane holds 8 of a row's 32
+// tile features (4 of each quarter: n0 + 16 f + 4 (lane / 16) .. +3) and the tile row's
+// statistics need only the 4 lanes of the row (rows_sum4), no LDS exchange.
+struct ResidualIn {
+  float b[2][4], r[2][4], g[2][4], be[2][4];  // bias, residual (or its pre-norm sum), LN's
+  template <int DT>
+  __device__ __forceinline__ void issue(const uint16_t *bias, const LinNorm &nrm, int wv,
+                                        int lane, int m0, int n0, int M) {
+    if (wv >= 2) return;
+    const int64_t row = min(m0 + 16 * wv + (lane & 15), M - 1);
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int n = n0 + 16 * f + 4 * (lane >> 4);  // n + 3 < N: N is a multiple of 32
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[f][j] = bias ? Mfma<DT>::widen(bias[n + j]) : 0.f;
+      unpack4<DT>(*reinterpret_cast<const uint2 *>(nrm.res + row * nrm.res_stride + n), r[f]);
+      if (nrm.res_stats) {
+        unpack4<DT>(*reinterpret_cast<const uint2 *>(nrm.res_gamma + n), g[f]);
+        unpack4<DT>(*reinterpret_cast<const uint2 *>(nrm.res_beta + n), be[f]);
+      }
     }
+  }
+  template <int DT> __device__ __forceinline__ static void unpack4(uint2 w, float (&o)[4]) {
+    o[0] = Mfma<DT>::widen_lo(w.x);
+    o[1] = Mfma<DT>::widen_hi(w.x);
+    o[2] = Mfma<DT>::widen_lo(w.y);
+    o[3] = Mfma<DT>::widen_hi(w.y);
+  }
+};
+
+// The values are rounded where the separate projection store and LayerNorm kernel round
+// them: y, the normalized residual, v.
+template <int DT>
+__device__ __forceinline__ void residual_epilogue(const floatx4_t *s_part, int wv, int lane,
+                                                  int m0, int n0, int M, int N,
+                                                  const ResidualIn &in, const float2 *s_ms,
+                                                  uint16_t *y, int64_t ldy, const LinNorm &nrm) {
+  constexpr int SUB = 4, TT = 2;
+  if (wv >= TT) return;
+  const int r = 16 * wv + (lane & 15);  // the workgroup's row
+  const int m = m0 + r;
+  float mean = 0.f, rstd = 1.f;
+  if (nrm.res_stats) {
+    mean = s_ms[r].x;
+    rstd = s_ms[r].y;
+  }
+  float o[2][4];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const int q = f * TT + wv;  // quarter (feature quarter f, token quarter wv)
+    const floatx4_t v = (s_part[q * 64 + lane] + s_part[(2 * SUB + q) * 64 + lane]) +
+                        (s_part[(SUB + q) * 64 + lane] + s_part[(3 * SUB + q) * 64 + lane]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float yj = round_elem<DT>(v[j] + bv[j]);
-      const float hj = nrm.res_stats ? round_elem<DT>((rs[j] - mean) * rstd * ga[j] + be[j])
-                                     : rs[j];
-      o[j] = round_elem<DT>(yj + hj);
+      const float yj = round_elem<DT>(v[j] + in.b[f][j]);
+      const float hj = nrm.res_stats
+                           ? round_elem<DT>((in.r[f][j] - mean) * rstd * in.g[f][j] + in.be[f][j])
+                           : in.r[f][j];
+      o[f][j] = round_elem<DT>(yj + hj);
     }
   }
-  // The tile row's sum: 4 values per lane, the quarter's 4 lanes of the row, then the
-  // two quarters (fixed order); then the same for the squared deviations from its mean.
-  const float qs = rows_sum4((o[0] + o[1]) + (o[2] + o[3]));
-  if (fin && lane < 16) s_tstat[0][qf][qt][lane] = qs;
-  lds_barrier();
+  // The tile row's mean over the lane's 8 values and the row's 4 lanes, then the sum of
+  // squared deviations from it, in a fixed order.
   const float tmean =
-      fin ? (s_tstat[0][0][qt][lane & 15] + s_tstat[0][1][qt][lane & 15]) / (float)LIN_STAT_TILE
-          : 0.f;
+      rows_sum4(((o[0][0] + o[0][1]) + (o[0][2] + o[0][3])) +
+                ((o[1][0] + o[1][1]) + (o[1][2] + o[1][3]))) / (float)LIN_STAT_TILE;
   float dd = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float d = o[j] - tmean;
-    dd = fmaf(d, d, dd);
-  }
-  const float qd = rows_sum4(dd);
-  if (fin && lane < 16) s_tstat[1][qf][qt][lane] = qd;
-  lds_barrier();
-  if (!fin || m >= M) return;
-  *reinterpret_cast<uint2 *>(y + (int64_t)m * ldy + qn) =
-      make_uint2(Mfma<DT>::narrow2(o[0], o[1]), Mfma<DT>::narrow2(o[2], o[3]));
-  if (qf == 0 && lane < 16)
-    nrm.y_stats[(int64_t)m * (N / LIN_STAT_TILE) + n0 / LIN_STAT_TILE] =
-        make_float2(tmean, s_tstat[1][0][qt][lane] + s_tstat[1][1][qt][lane]);
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float d = o[f][j] - tmean;
+      dd = fmaf(d, d, dd);
+    }
+  const float m2 = rows_sum4(dd);
+  if (m >= M) return;
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+    *reinterpret_cast<uint2 *>(y + (int64_t)m * ldy + n0 + 16 * f + 4 * (lane >> 4)) =
+        make_uint2(Mfma<DT>::narrow2(o[f][0], o[f][1]), Mfma<DT>::narrow2(o[f][2], o[f][3]));
+  if (lane < 16)
+    nrm.y_stats[(int64_t)m * (N / LIN_STAT_TILE) + n0 / LIN_STAT_TILE] = make_float2(tmean, m2);
 }
 
 // XP: x is packed (no ds_bpermute); GELU: exact GELU after the bias; YP: y is written
@@ -252,10 +283,42 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
   const int qf = wv / TT, qt = wv % TT;
   const int qn = n0 + 16 * qf + 4 * (lane >> 4);
   float bv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (bias && wv < SUB && MODE != LIN_NORM_IN) {
+  if (bias && wv < SUB && MODE == LIN_PLAIN) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) bv[j] = qn + j < N ? Mfma<DT>::widen(bias[qn + j]) : 0.f;
   }
+  // The epilogue inputs requested before the operands so that they have landed when
+  // the products have (loads complete in order): the rows' tile statistics (two per
+  // thread) and, for LIN_NORM_IN's finishing lanes (features qn .. qn + 3), u and b'.
+  __shared__ float2 s_ms[MODE == LIN_PLAIN ? 1 : LIN_TILE];
+  RowStatLoads rsl;
+  const float2 *row_st = nullptr;
+  int row_t = 0;
+  float fa[4] = {0.f, 0.f, 0.f, 0.f}, fb[4] = {0.f, 0.f, 0.f, 0.f};  // LIN_NORM_IN: u, b'
+  if constexpr (MODE == LIN_NORM_IN) {
+    row_st = nrm.x_stats;
+    row_t = K / LIN_STAT_TILE;
+    if (wv < SUB) {
+      if (qn + 3 < N && nrm.vec4) {  // one 16-byte load each
+        const float4 a = *reinterpret_cast<const float4 *>(nrm.u + qn);
+        const float4 b = *reinterpret_cast<const float4 *>(nrm.fbias + qn);
+        fa[0] = a.x, fa[1] = a.y, fa[2] = a.z, fa[3] = a.w;
+        fb[0] = b.x, fb[1] = b.y, fb[2] = b.z, fb[3] = b.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          fa[j] = qn + j < N ? nrm.u[qn + j] : 0.f;
+          fb[j] = qn + j < N ? nrm.fbias[qn + j] : 0.f;
+        }
+      }
+    }
+  }
+  if constexpr (MODE == LIN_RESIDUAL) {
+    row_st = nrm.res_stats;  // null: a plain residual
+    row_t = N / LIN_STAT_TILE;
+  }
+  if (MODE != LIN_PLAIN && row_st) rsl.issue(row_st, row_t, m0, M);
+
   floatx4_t acc[FT][TT];
 #pragma unroll
   for (int f = 0; f < FT; ++f)
@@ -311,45 +374,13 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
     }
   }
 
-  // The deferred-LayerNorm epilogues' inputs, requested now so that their latency
-  // overlaps the reduction below: the rows' tile statistics (all threads) and, for the
-  // finishing lanes (row qm, features qn .. qn + 3), the per-feature terms and residual.
-  __shared__ float2 s_ms[MODE == LIN_PLAIN ? 1 : LIN_TILE];
-  RowStatLoads rsl;
-  const float2 *row_st = nullptr;
-  int row_t = 0;
-  float fa[4] = {0.f, 0.f, 0.f, 0.f}, fb[4] = {0.f, 0.f, 0.f, 0.f};  // u, b' or gamma, beta
-  float rs[4] = {0.f, 0.f, 0.f, 0.f};  // residual (or its pre-norm sum)
-  const int qm = min(m0 + 16 * qt + (lane & 15), M - 1);
-  if constexpr (MODE == LIN_NORM_IN) {
-    row_st = nrm.x_stats;
-    row_t = K / LIN_STAT_TILE;
-    if (wv < SUB) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        fa[j] = qn + j < N ? nrm.u[qn + j] : 0.f;
-        fb[j] = qn + j < N ? nrm.fbias[qn + j] : 0.f;
-      }
-    }
-  }
+  // LIN_RESIDUAL's per-feature inputs and residual, requested now so that they overlap
+  // the reduction below (with them before the operands, a 1024-wide output projection
+  // ran 0.3 us slower).
+  ResidualIn rin;
   if constexpr (MODE == LIN_RESIDUAL) {
-    row_st = nrm.res_stats;  // null: a plain residual
-    row_t = N / LIN_STAT_TILE;
-    if (wv < SUB) {
-      // N is a multiple of 32 here (whole statistics tiles), so qn + 3 < N.
-      const uint16_t *rp = nrm.res + (int64_t)qm * nrm.res_stride + qn;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) rs[j] = Mfma<DT>::widen(rp[j]);
-      if (row_st) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          fa[j] = Mfma<DT>::widen(nrm.res_gamma[qn + j]);
-          fb[j] = Mfma<DT>::widen(nrm.res_beta[qn + j]);
-        }
-      }
-    }
+    rin.issue<DT>(bias, nrm, wv, lane, m0, n0, M);
   }
-  if (MODE != LIN_PLAIN && row_st) rsl.issue(row_st, row_t, m0, M);
 
   // Sum the waves' partial tiles: waves 4..7 hand theirs to waves 0..3, which add and
   // publish the four sums.
@@ -380,8 +411,7 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
 
   const int m = m0 + 16 * qt + (lane & 15);
   if constexpr (MODE == LIN_RESIDUAL) {
-    residual_epilogue<DT>(s_part, wv, lane, qf, qt, qn, m, M, N, n0, bv, rs, fa, fb, s_ms, y, ldy,
-                          nrm);
+    residual_epilogue<DT>(s_part, wv, lane, m0, n0, M, N, rin, s_ms, y, ldy, nrm);
     return;
   }
   if (wv >= SUB) return;
@@ -664,6 +694,7 @@ extern "C" int vfl_linear_norm(const void *x, int64_t x_stride, const float *x_s
   nrm.u = u;
   nrm.fbias = folded_bias;
   nrm.eps = eps;
+  nrm.vec4 = ((uintptr_t)u | (uintptr_t)folded_bias) % 16 == 0;
   const bool vec_store = (uintptr_t)y % 8 == 0 && y_stride % 4 == 0;
   const dim3 grid((unsigned)(packed_rows(out_features) / LIN_TILE),
                   (unsigned)((rows + LIN_TILE - 1) / LIN_TILE));
@@ -723,11 +754,12 @@ extern "C" int vfl_linear_residual(const void *x, int64_t x_stride, const void *
   }
   if (((uintptr_t)x | (uintptr_t)packed_weight) % 16 != 0 || (!xp && x_stride % 8 != 0) ||
       (uintptr_t)y % 8 != 0 || y_stride % 4 != 0 || (uintptr_t)bias % 2 != 0 ||
-      (uintptr_t)residual % 2 != 0 || ((uintptr_t)y_stats | (uintptr_t)r_stats) % 8 != 0 ||
-      ((uintptr_t)r_gamma | (uintptr_t)r_beta) % 2 != 0) {
+      (uintptr_t)residual % 8 != 0 || r_stride % 4 != 0 ||
+      ((uintptr_t)y_stats | (uintptr_t)r_stats) % 8 != 0 ||
+      ((uintptr_t)r_gamma | (uintptr_t)r_beta) % 8 != 0) {
     set_error("linear_residual: x and the packed weight must be 16-byte aligned (x row "
-              "stride a multiple of 8 elements), y 8-byte aligned with a row stride a "
-              "multiple of 4, the statistics 8-byte aligned");
+              "stride a multiple of 8 elements), y and the residual 8-byte aligned with row "
+              "strides multiples of 4, gamma / beta and the statistics 8-byte aligned");
     return VFL_E_INVALID;
   }
   LinNorm nrm{};

@@ -231,6 +231,8 @@ def linear_residual(x: torch.Tensor, packed_weight: torch.Tensor, bias: torch.Te
     if residual.shape != (rows, out_features) or residual.stride(-1) != 1:
         raise ValueError(f"linear_residual: residual must be [{rows}, {out_features}], unit "
                          "stride")
+    if residual.stride(0) % 4 or residual.data_ptr() % 8:
+        residual = residual.contiguous()
     dt = x.dtype
     if packed_weight.dtype != dt or residual.dtype != dt or (bias is not None
                                                              and bias.dtype != dt):
