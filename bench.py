@@ -865,6 +865,36 @@ def decoder_linear_timing(torch, rows: int = REQUESTS * BEAMS, rotation_mb: int 
                      "hipblaslt_us": round(graph_time(lambda i: F.linear(x, ws[i], bias),
                                                       copies), 2),
                      "weight_copies": copies}
+        # The deferred-LayerNorm forms the decoder runs: a projection of LN(x) with the
+        # LayerNorm folded in (q|k|v, cross q, fc1), and an output projection adding a
+        # deferred residual and writing the pre-norm sum and its statistics (attention
+        # out, fc2).  Statistics and LayerNorm terms are synthetic (timing only).
+        if not flags & dops.LINEAR_X_PACKED:
+            xst = torch.rand(rows, k // 32, 2, device=dev, generator=g)
+            u = torch.randn(n, device=dev, generator=g)
+            fb = torch.randn(n, device=dev, generator=g)
+
+            def norm_in(i):
+                check(lib.vfl_linear_norm(x.data_ptr(), k, xst.data_ptr(), 1e-5,
+                                          packed[i].data_ptr(), u.data_ptr(), fb.data_ptr(),
+                                          y.data_ptr(), 0 if yp else n, rows, n, k, flags, bf16,
+                                          torch.cuda.current_stream().cuda_stream))
+            out[name]["vfl_linear_norm_us"] = round(graph_time(norm_in, copies), 2)
+        if n == 1024:
+            h = torch.randn(rows, n, device=dev, generator=g).to(torch.bfloat16)
+            hst = torch.rand(rows, n // 32, 2, device=dev, generator=g) + 0.5
+            gam = torch.randn(n, device=dev, generator=g).to(torch.bfloat16)
+            bet = torch.randn(n, device=dev, generator=g).to(torch.bfloat16)
+            vst = torch.empty(rows, n // 32, 2, device=dev)
+
+            def residual(i):
+                check(lib.vfl_linear_residual(xin.data_ptr(), ldx, packed[i].data_ptr(),
+                                              bias.data_ptr(), h.data_ptr(), n, hst.data_ptr(),
+                                              gam.data_ptr(), bet.data_ptr(), 1e-5, y.data_ptr(),
+                                              n, vst.data_ptr(), rows, n, k,
+                                              flags & dops.LINEAR_X_PACKED, bf16,
+                                              torch.cuda.current_stream().cuda_stream))
+            out[name]["vfl_linear_residual_us"] = round(graph_time(residual, copies), 2)
         del ws, packed
         torch.cuda.empty_cache()
     return out
