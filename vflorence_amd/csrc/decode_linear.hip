@@ -157,17 +157,28 @@ template <int DT> __device__ __forceinline__ float round_elem(float v) {
 // statistics need only the 4 lanes of the row (rows_sum4), no LDS exchange.
 struct ResidualIn {
   float b[2][4], r[2][4], g[2][4], be[2][4];  // bias, residual (or its pre-norm sum), LN's
-  template <int DT>
-  __device__ __forceinline__ void issue(const uint16_t *bias, const LinNorm &nrm, int wv,
-                                        int lane, int m0, int n0, int M) {
+  uint2 raw[2];                               // the residual's 8 values as loaded
+  // The residual itself, requested with the operands (its 4 registers are the only ones
+  // held through the products).
+  __device__ __forceinline__ void issue_residual(const LinNorm &nrm, int wv, int lane, int m0,
+                                                 int n0, int M) {
     if (wv >= 2) return;
     const int64_t row = min(m0 + 16 * wv + (lane & 15), M - 1);
 #pragma unroll
+    for (int f = 0; f < 2; ++f)  // n + 3 < N: N is a multiple of 32
+      raw[f] = *reinterpret_cast<const uint2 *>(nrm.res + row * nrm.res_stride + n0 + 16 * f +
+                                                4 * (lane >> 4));
+  }
+  template <int DT>
+  __device__ __forceinline__ void issue(const uint16_t *bias, const LinNorm &nrm, int wv,
+                                        int lane, int n0) {
+    if (wv >= 2) return;
+#pragma unroll
     for (int f = 0; f < 2; ++f) {
-      const int n = n0 + 16 * f + 4 * (lane >> 4);  // n + 3 < N: N is a multiple of 32
+      const int n = n0 + 16 * f + 4 * (lane >> 4);
 #pragma unroll
       for (int j = 0; j < 4; ++j) b[f][j] = bias ? Mfma<DT>::widen(bias[n + j]) : 0.f;
-      unpack4<DT>(*reinterpret_cast<const uint2 *>(nrm.res + row * nrm.res_stride + n), r[f]);
+      unpack4<DT>(raw[f], r[f]);
       if (nrm.res_stats) {
         unpack4<DT>(*reinterpret_cast<const uint2 *>(nrm.res_gamma + n), g[f]);
         unpack4<DT>(*reinterpret_cast<const uint2 *>(nrm.res_beta + n), be[f]);
@@ -318,6 +329,10 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
     row_t = N / LIN_STAT_TILE;
   }
   if (MODE != LIN_PLAIN && row_st) rsl.issue(row_st, row_t, m0, M);
+  // The residual too, for one batch of K steps (a 1024-deep output projection: 6.2
+  // against 6.3 us); a longer, double-buffered K loop ran 0.1 us slower with it here.
+  ResidualIn rin;
+  if constexpr (MODE == LIN_RESIDUAL && !PIPE) rin.issue_residual(nrm, wv, lane, m0, n0, M);
 
   floatx4_t acc[FT][TT];
 #pragma unroll
@@ -374,12 +389,12 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void decode_linear_kernel(
     }
   }
 
-  // LIN_RESIDUAL's per-feature inputs and residual, requested now so that they overlap
-  // the reduction below (with them before the operands, a 1024-wide output projection
-  // ran 0.3 us slower).
-  ResidualIn rin;
+  // LIN_RESIDUAL's per-feature inputs, requested now so that they overlap the reduction
+  // below (with them before the operands, a 1024-wide output projection ran 0.3 us
+  // slower).
   if constexpr (MODE == LIN_RESIDUAL) {
-    rin.issue<DT>(bias, nrm, wv, lane, m0, n0, M);
+    if constexpr (PIPE) rin.issue_residual(nrm, wv, lane, m0, n0, M);
+    rin.issue<DT>(bias, nrm, wv, lane, n0);
   }
 
   // Sum the waves' partial tiles: waves 4..7 hand theirs to waves 0..3, which add and
