@@ -513,12 +513,13 @@ int vfl_engine_beam_update(vfl_engine *e, const float *scores, const int64_t *id
     int32_t row;
     int32_t token;
   };
-  std::vector<Cand> cands;
+  std::vector<Cand> cands, merged;
   std::vector<Row> next;
   next.reserve(e->running.size());
   std::vector<std::pair<int32_t, Cand>> live;  // (parent row, candidate)
   std::vector<int32_t> handed;                 // parent row -> index in next of its owner
   handed.assign(rows, -1);
+  std::vector<uint8_t> has_child(rows, 0);     // parent row -> a live child takes it
 
   int32_t i = 0;
   while (i < rows) {  // a request's rows are adjacent
@@ -529,16 +530,43 @@ int vfl_engine_beam_update(vfl_engine *e, const float *scores, const int64_t *id
     const int32_t nb = q.num_beams;
     const int32_t keep = std::max<int32_t>(2, 1 + (int32_t)q.eos.size()) * nb;
     cands.clear();
+    bool rows_sorted = true;
     for (int32_t r = i; r < j; ++r) {
       const float cum = (float)e->running[r].cum;
       for (int32_t c = 0; c < k; ++c) {
         const float v = scores[(int64_t)r * k + c] + cum;
+        if (c > 0 && !(cands.back().value >= v)) rows_sorted = false;
         cands.push_back({v, r, (int32_t)ids[(int64_t)r * k + c]});
       }
     }
-    std::stable_sort(cands.begin(), cands.end(),
-                     [](const Cand &a, const Cand &b) { return a.value > b.value; });
-    if ((int32_t)cands.size() > keep) cands.resize(keep);
+    // Best first, ties in row-major order (a stable sort).  Each row's list is best
+    // first already, so the best `keep` come from merging the rows' lists (on a tie the
+    // lower row first); otherwise an insertion sort, with no temporary buffer.
+    const int32_t nr = j - i, take = std::min<int32_t>(keep, (int32_t)cands.size());
+    if (rows_sorted && nr <= 16) {
+      int32_t at[16] = {0};
+      merged.clear();
+      for (int32_t t = 0; t < take; ++t) {
+        int32_t best = -1;
+        for (int32_t r = 0; r < nr; ++r)
+          if (at[r] < k && (best < 0 || cands[r * k + at[r]].value > cands[best * k + at[best]].value))
+            best = r;
+        merged.push_back(cands[best * k + at[best]]);
+        ++at[best];
+      }
+      cands.swap(merged);
+    } else {
+      for (size_t a = 1; a < cands.size(); ++a) {
+        const Cand c = cands[a];
+        size_t b = a;
+        while (b > 0 && cands[b - 1].value < c.value) {
+          cands[b] = cands[b - 1];
+          --b;
+        }
+        cands[b] = c;
+      }
+      if ((int32_t)cands.size() > keep) cands.resize(keep);
+    }
 
     live.clear();
     for (int32_t rank = 0; rank < (int32_t)cands.size(); ++rank) {
@@ -585,24 +613,37 @@ int vfl_engine_beam_update(vfl_engine *e, const float *scores, const int64_t *id
       std::vector<int32_t> best = std::move(q.finished.front().tokens);
       e->end_request(slot, std::move(best));
     } else {
-      // A parent's first live child takes over its table; later children of the same
-      // parent share it (one more holder per block), as forking every child and then
-      // releasing every parent would leave them.
+      // A parent's first live child takes over its table and its token list; later
+      // children of the same parent share the table (one more holder per block), as
+      // forking every child and then releasing every parent would leave them, and copy
+      // the first child's tokens with their own last token -- into the token storage of
+      // a parent with no live child where there is one (no allocation).
+      for (const auto &l : live) has_child[l.first] = 1;
+      int32_t spare = i;
       for (const auto &l : live) {
         const int32_t p = l.first;
         Row child;
         child.req = slot;
-        child.tokens.reserve(e->running[p].tokens.size() + 1);
-        child.tokens = e->running[p].tokens;
-        child.tokens.push_back(l.second.token);
         child.cached = e->running[p].cached;
         child.cum = (double)l.second.value;
         if (handed[p] < 0) {
+          child.tokens = std::move(e->running[p].tokens);
+          e->running[p].tokens.clear();
+          child.tokens.push_back(l.second.token);
           child.table = std::move(e->running[p].table);
           e->running[p].table.clear();
           handed[p] = (int32_t)next.size();
         } else {
-          child.table = next[handed[p]].table;
+          while (spare < j && has_child[spare]) ++spare;
+          if (spare < j) {
+            child.tokens = std::move(e->running[spare].tokens);
+            e->running[spare].tokens.clear();
+            ++spare;
+          }
+          const Row &first = next[handed[p]];
+          child.tokens.assign(first.tokens.begin(), first.tokens.end());
+          child.tokens.back() = l.second.token;
+          child.table = first.table;
           e->pool.share(child.table.data(), (int32_t)child.table.size());
         }
         next.push_back(std::move(child));

@@ -180,6 +180,7 @@ class EngineCore:
                               owner=self)
         self._admitted = np.empty(max(1, max_num_seqs), dtype=np.int64)
         self._n = [ctypes.c_int32() for _ in range(4)]
+        self._pack_ptrs = {}  # id(views) -> (views, the arrays' addresses in pack's order)
         self._out_id = ctypes.c_int64()
         self._out_tokens = np.empty(1024, dtype=np.int32)
         self.num_rows = self.num_pairs = 0
@@ -229,12 +230,14 @@ class EngineCore:
         group_start, tables [rows, table_width]); returns whether the rows form beam
         groups."""
         grouped = self._n[3]
-        v = views
-        _check(lib.vfl_engine_pack(
-            self._h, padded, table_width, max_group, _ptr(v["input_ids"]), _ptr(v["positions"]),
-            _ptr(v["slots"]), _ptr(v["lengths"]), _ptr(v["copy_src"]), _ptr(v["copy_dst"]),
-            _ptr(v["context_lens"]), _ptr(v["order"]), _ptr(v["group_start"]), _ptr(v["tables"]),
-            _ptr(v["row_requests"]), ctypes.byref(grouped)))
+        ptrs = self._pack_ptrs.get(id(views))
+        if ptrs is None or ptrs[0] is not views:  # addresses of a views dict, made once
+            names = ("input_ids", "positions", "slots", "lengths", "copy_src", "copy_dst",
+                     "context_lens", "order", "group_start", "tables", "row_requests")
+            ptrs = (views, [views[k].ctypes.data for k in names])
+            self._pack_ptrs = {id(views): ptrs}
+        _check(lib.vfl_engine_pack(self._h, padded, table_width, max_group, *ptrs[1],
+                                   ctypes.byref(grouped)))
         return bool(grouped.value)
 
     def max_table_len(self) -> int:

@@ -197,6 +197,7 @@ class ModelRunner:
         self._self_caches = [c for layer in self.decoder_layers
                              for c in (layer.self_attn.k_cache, layer.self_attn.v_cache)]
         self._cache_ptrs = hip_attn.cache_pointer_table(self._self_caches)
+        self._copier = hip_attn.BlockCopier(self._self_caches)
         mb = 1024**2
         weights = sum(t.nbytes for t in (*self.model.parameters(), *self.model.buffers()))
         kv = sum(c.nbytes for c in self._self_caches)
@@ -300,9 +301,8 @@ class ModelRunner:
         d = buf.d
         if num_pairs:  # copy-on-write first: this step writes into the now-private blocks
             src, dst = h["copy_src"][:num_pairs], h["copy_dst"][:num_pairs]
-            staged = bool(np.intersect1d(src, dst).size)
-            hip_attn.copy_blocks(self._self_caches, d["copy_src"][:num_pairs],
-                                 d["copy_dst"][:num_pairs], self._cache_ptrs, staged=staged)
+            staged = not set(src.tolist()).isdisjoint(dst.tolist())
+            self._copier(d["copy_src"][:num_pairs], d["copy_dst"][:num_pairs], staged=staged)
         # the plan points at fixed views of the step buffers: one per (rows, grouped)
         bs = self.block_size
         self_metadata = self._self_metadata.get((padded, grouped))

@@ -638,6 +638,37 @@ def copy_blocks(
     )
 
 
+class BlockCopier:
+    """``copy_blocks`` over a fixed set of caches, checked once: the per-step call of a
+    runner passes only the pair vectors (device int64, validated by the library's host
+    checks against the pool size)."""
+
+    def __init__(self, caches: list[torch.Tensor]):
+        self.pointer_table = cache_pointer_table(caches)
+        self.device = self.pointer_table.device
+        self.num_caches = len(caches)
+        self.num_blocks = caches[0].shape[0]
+        self.block_bytes = caches[0][0].numel() * caches[0].element_size()
+
+    def __call__(self, src: torch.Tensor, dst: torch.Tensor, staged: bool = False) -> None:
+        n = src.numel()
+        if (src.dtype != torch.int64 or dst.dtype != torch.int64 or dst.numel() != n
+                or not src.is_contiguous() or not dst.is_contiguous()
+                or src.device != self.device or dst.device != self.device):
+            raise ValueError("src/dst must be contiguous int64 vectors of one length on the "
+                             "caches' device")
+        if n == 0:
+            return
+        staging = None
+        if staged:
+            staging = torch.empty(self.num_caches * n * self.block_bytes, dtype=torch.uint8,
+                                  device=self.device)
+        check(lib.vfl_copy_blocks(self.pointer_table.data_ptr(), self.num_caches,
+                                  src.data_ptr(), dst.data_ptr(), n, self.block_bytes,
+                                  self.num_blocks, None if staging is None else staging.data_ptr(),
+                                  _stream(self.device)))
+
+
 def copy_pairs_need_staging(pairs: list[tuple[int, int]]) -> bool:
     """True when a destination block is also a source block; raises on repeated dsts."""
     dsts = [d for _, d in pairs]
