@@ -667,6 +667,38 @@ def extra_counter_subjects(torch, wl):
         out.append({"name": f"decode linear {label}, 256 rows", "launches": copies,
                     "algorithmic_bytes_per_launch": 2 * (n * k + rows * k + rows * n + n)})
         del ws, packed, x
+    # the deferred-LayerNorm forms the decoder runs: q|k|v with the LayerNorm folded into
+    # its weight (pre-norm rows and their tile statistics in), and an attention output
+    # projection adding a deferred residual (pre-norm sum and statistics in and out)
+    for label, n, k, residual in (("3072x1024 q|k|v, LayerNorm folded", 3072, 1024, False),
+                                  ("1024x1024 + deferred residual", 1024, 1024, True)):
+        copies = max(3, (400 << 20) // (n * k * 2))
+        packed = [dops.pack_linear_weight((torch.randn(n, k, device=dev, generator=g)
+                                           / k**0.5).to(torch.bfloat16)) for _ in range(copies)]
+        x = torch.randn(rows, k, device=dev, generator=g).to(torch.bfloat16)
+        gamma = (torch.randn(n if residual else k, device=dev, generator=g) * 0.1 + 1).to(
+            torch.bfloat16)
+        beta = (torch.randn(n if residual else k, device=dev, generator=g) * 0.1).to(
+            torch.bfloat16)
+        torch.cuda.synchronize()
+        if residual:
+            h = torch.randn(rows, n, device=dev, generator=g).to(torch.bfloat16)
+            hst = torch.rand(rows, n // 32, 2, device=dev, generator=g) + 0.5
+            bias = torch.randn(n, device=dev, generator=g).to(torch.bfloat16)
+            for i in range(copies):
+                dops.linear_residual(x, packed[i], bias, h, hst, gamma, beta, 1e-5, n)
+            ab = 2 * (n * k + rows * k + 2 * rows * n + 3 * n) + 2 * rows * (n // 32) * 8
+        else:
+            xst = torch.rand(rows, k // 32, 2, device=dev, generator=g) + 0.5
+            u = torch.randn(n, device=dev, generator=g)
+            fb = torch.randn(n, device=dev, generator=g)
+            for i in range(copies):
+                dops.linear_norm(x, xst, 1e-5, packed[i], u, fb, n)
+            ab = 2 * (n * k + rows * k + rows * n) + rows * (k // 32) * 8 + 8 * n
+        torch.cuda.synchronize()
+        out.append({"name": f"decode linear {label}, 256 rows", "launches": copies,
+                    "algorithmic_bytes_per_launch": ab})
+        del packed, x
     torch.cuda.synchronize()
     return out
 
