@@ -176,6 +176,15 @@ def test_deferred_entry_points_reject_bad_arguments():
         ops().linear_norm(x, torch.zeros(4, 4, 2, device=DEV), 1e-5, w, u, u, 256)
     with pytest.raises(ValueError):  # a packed x has no row statistics
         ops().linear_norm(x, st, 1e-5, w, u, u, 256, flags=ops().LINEAR_X_PACKED)
+    gam = torch.ones(256, dtype=dt, device=DEV)
+    with pytest.raises(ValueError):  # LayerNorm weights of another dtype than the rows
+        ops().linear_residual(x, w, None, h, st, gam.float(), gam, 1e-5, 256)
+    with pytest.raises(ValueError):
+        ops().layer_norm_apply(h, st, gam, gam.float(), 1e-5)
+    with pytest.raises(RuntimeError):  # statistics left on the host
+        ops().linear_residual(x, w, None, h, st.cpu(), gam, gam, 1e-5, 256)
+    with pytest.raises(RuntimeError):  # a bias left on the host
+        ops().linear_residual(x, w, gam.cpu(), h, None, None, None, 0.0, 256)
     with pytest.raises(RuntimeError):  # y_stats aliasing r_stats is refused by the library
         from vflorence_amd._lib import check, lib
 

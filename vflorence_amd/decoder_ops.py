@@ -208,7 +208,8 @@ def linear_residual(x: torch.Tensor, packed_weight: torch.Tensor, bias: torch.Te
     h = ``residual`` (r_stats None) or LN(residual) under r_stats / r_gamma / r_beta /
     r_eps, and v's tile statistics.  x is ``[rows, in]`` (or, with ``LINEAR_X_PACKED``, a
     packed activation of ``rows`` rows); residual and v are ``[rows, out_features]``."""
-    dev = _require_gpu(x, packed_weight, residual)
+    dev = _require_gpu(x, packed_weight, residual,
+                       *(t for t in (bias, r_stats, r_gamma, r_beta) if t is not None))
     padded_out = (out_features + 31) // 32 * 32
     if (out_features <= 0 or out_features % STAT_TILE or packed_weight.dim() != 1
             or packed_weight.numel() % padded_out):
@@ -241,9 +242,10 @@ def linear_residual(x: torch.Tensor, packed_weight: torch.Tensor, bias: torch.Te
         if (r_gamma is None or r_beta is None or r_stats.dtype != torch.float32
                 or r_stats.shape != _stats_shape(rows, out_features)
                 or not r_stats.is_contiguous() or r_gamma.shape != (out_features,)
-                or r_beta.shape != (out_features,)):
+                or r_beta.shape != (out_features,) or r_gamma.dtype != dt
+                or r_beta.dtype != dt):
             raise ValueError("linear_residual: r_stats [rows, out/32, 2] float32 and gamma / "
-                             "beta [out] describe a deferred residual")
+                             "beta [out] of x's dtype describe a deferred residual")
     v = torch.empty(rows, out_features, dtype=dt, device=dev)
     stats = torch.empty(_stats_shape(rows, out_features), dtype=torch.float32, device=dev)
     g = None if r_gamma is None else r_gamma.contiguous()
@@ -322,8 +324,10 @@ def layer_norm_apply(v: torch.Tensor, stats: torch.Tensor, gamma: torch.Tensor,
     dev = _require_gpu(v, stats, gamma, beta)
     rows, dim = v.shape
     if (stats.dtype != torch.float32 or stats.shape != _stats_shape(rows, dim)
-            or not stats.is_contiguous() or gamma.shape != (dim,) or beta.shape != (dim,)):
-        raise ValueError("layer_norm_apply: stats [rows, dim/32, 2] float32, gamma / beta [dim]")
+            or not stats.is_contiguous() or gamma.shape != (dim,) or beta.shape != (dim,)
+            or gamma.dtype != v.dtype or beta.dtype != v.dtype):
+        raise ValueError("layer_norm_apply: stats [rows, dim/32, 2] float32, gamma / beta [dim] "
+                         "of v's dtype")
     v2 = v if v.stride(-1) == 1 and v.stride(0) % 4 == 0 and v.data_ptr() % 8 == 0 \
         else v.contiguous()
     out = torch.empty(rows, dim, dtype=v.dtype, device=dev)
