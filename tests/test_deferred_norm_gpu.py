@@ -183,6 +183,8 @@ def test_deferred_entry_points_reject_bad_arguments():
         ops().layer_norm_apply(h, st, gam, gam.float(), 1e-5)
     with pytest.raises(RuntimeError):  # statistics left on the host
         ops().linear_residual(x, w, None, h, st.cpu(), gam, gam, 1e-5, 256)
+    with pytest.raises(ValueError):  # a bias shorter than the outputs
+        ops().linear_residual(x, w, gam[:128], h, None, None, None, 0.0, 256)
     with pytest.raises(RuntimeError):  # a bias left on the host
         ops().linear_residual(x, w, gam.cpu(), h, None, None, None, 0.0, 256)
     with pytest.raises(RuntimeError):  # y_stats aliasing r_stats is refused by the library

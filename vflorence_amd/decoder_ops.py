@@ -238,6 +238,8 @@ def linear_residual(x: torch.Tensor, packed_weight: torch.Tensor, bias: torch.Te
     if packed_weight.dtype != dt or residual.dtype != dt or (bias is not None
                                                              and bias.dtype != dt):
         raise ValueError("linear_residual: x, weight, bias and residual must share one dtype")
+    if bias is not None and bias.shape != (out_features,):
+        raise ValueError("linear_residual: bias must be [out_features]")
     if r_stats is not None:
         if (r_gamma is None or r_beta is None or r_stats.dtype != torch.float32
                 or r_stats.shape != _stats_shape(rows, out_features)
