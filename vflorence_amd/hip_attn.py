@@ -645,6 +645,7 @@ class BlockCopier:
 
     def __init__(self, caches: list[torch.Tensor]):
         self.pointer_table = cache_pointer_table(caches)
+        self._caches = list(caches)  # the table holds their addresses: keep them alive
         self.device = self.pointer_table.device
         self.num_caches = len(caches)
         self.num_blocks = caches[0].shape[0]
