@@ -168,6 +168,11 @@ class RowView:
                 f"table={self.block_table}, cached={self.num_cached_tokens})")
 
 
+_PACK_I32 = ("context_lens", "order", "group_start", "tables")
+_PACK_NAMES = ("input_ids", "positions", "slots", "lengths", "copy_src", "copy_dst",
+               "context_lens", "order", "group_start", "tables", "row_requests")
+
+
 class EngineCore:
     """The decode loop's host state (``vfl_engine``)."""
 
@@ -180,7 +185,7 @@ class EngineCore:
                               owner=self)
         self._admitted = np.empty(max(1, max_num_seqs), dtype=np.int64)
         self._n = [ctypes.c_int32() for _ in range(4)]
-        self._pack_ptrs = {}  # id(views) -> (views, the arrays' addresses in pack's order)
+        self._pack_ptrs = {}  # id(views) -> (views, arrays, addresses, rows, tables shape)
         self._out_id = ctypes.c_int64()
         self._out_tokens = np.empty(1024, dtype=np.int32)
         self.num_rows = self.num_pairs = 0
@@ -231,12 +236,25 @@ class EngineCore:
         groups."""
         grouped = self._n[3]
         ptrs = self._pack_ptrs.get(id(views))
-        if ptrs is None or ptrs[0] is not views:  # addresses of a views dict, made once
-            names = ("input_ids", "positions", "slots", "lengths", "copy_src", "copy_dst",
-                     "context_lens", "order", "group_start", "tables", "row_requests")
-            ptrs = (views, [views[k].ctypes.data for k in names])
+        # addresses of a views dict's arrays, taken once and kept with the arrays they
+        # belong to (an array replaced under its name is seen and re-read)
+        if (ptrs is None or ptrs[0] is not views
+                or any(views[k] is not a for k, a in zip(_PACK_NAMES, ptrs[1]))):
+            arrays = tuple(views[k] for k in _PACK_NAMES)
+            for k, a in zip(_PACK_NAMES, arrays):
+                want = np.int32 if k in _PACK_I32 else np.int64
+                if a.dtype != want or not a.flags.c_contiguous:
+                    raise ValueError(f"pack: {k} must be a contiguous {want.__name__} array")
+            ptrs = (views, arrays, [a.ctypes.data for a in arrays],
+                    min(len(views[k]) for k in _PACK_NAMES if k not in ("tables", "group_start")),
+                    views["tables"].shape)
             self._pack_ptrs = {id(views): ptrs}
-        _check(lib.vfl_engine_pack(self._h, padded, table_width, max_group, *ptrs[1],
+        cap, tshape = ptrs[3], ptrs[4]
+        if (padded > cap or padded >= len(views["group_start"]) or len(tshape) != 2
+                or tshape[0] < padded or tshape[1] != table_width):
+            raise ValueError(f"pack: {padded} rows of width {table_width} do not fit the views "
+                             f"(rows {cap}, tables {tuple(tshape)})")
+        _check(lib.vfl_engine_pack(self._h, padded, table_width, max_group, *ptrs[2],
                                    ctypes.byref(grouped)))
         return bool(grouped.value)
 
