@@ -302,9 +302,21 @@ def test_scheduler_admission_counts_beams_and_keeps_beams_adjacent():
     assert [r.request_id for r in sched.running] == [0, 0, 0, 1, 1, 1]
     # three children share their parent's one block; all but the last writer copy it
     views = host_views(8, 4)
+    # views too small, of another width, or of the wrong dtype are refused before the
+    # host core writes into them
+    with pytest.raises(ValueError):
+        sched.core.pack(8, 4, 8, host_views(4, 4))
+    with pytest.raises(ValueError):
+        sched.core.pack(8, 4, 8, host_views(8, 2))
+    with pytest.raises(ValueError):
+        sched.core.pack(8, 4, 8, {**host_views(8, 4), "order": np.zeros(8, np.int64)})
     sched.core.pack(8, 4, 8, views)
     pairs = list(zip(views["copy_src"][:batch.num_pairs], views["copy_dst"][:batch.num_pairs]))
     assert batch.num_pairs == 4 and len({d for _, d in pairs}) == 4
+    # an array replaced under its name is written, not the one it replaced
+    old, views["copy_src"] = views["copy_src"], np.full(8, -7, np.int64)
+    sched.core.pack(8, 4, 8, views)
+    assert list(views["copy_src"][:4]) == list(old[:4])
 
 
 def test_block_manager_invariants_under_random_forks():
