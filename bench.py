@@ -62,9 +62,6 @@ def parse_args():
     p.add_argument("--counters", action="store_true",
                    help="counter-collection run for rocprofv3 --pmc: the dominant kernel's "
                         "launches and two copies of known size, nothing timed")
-    p.add_argument("--gather-probe", action="store_true",
-                   help="time read-only probes of the cross-attention's page reads at "
-                        "several granularities against the kernel itself")
     return p.parse_args()
 
 
@@ -703,72 +700,6 @@ def extra_counter_subjects(torch, wl):
     return out
 
 
-GATHER_VARIANTS = {
-    0: "(group, head) slices, consecutive workgroup ids per group, 1024 x 4 waves",
-    1: "(group, head) slices, head-major ids, 1024 x 4 waves",
-    2: "(group, 4 heads): 8 KiB of a block read together, 256 x 16 waves",
-    3: "(group, 4 heads): each wave reads 8 KiB per block, 256 x 4 waves",
-    4: "(group, head) slices as 0, non-temporal loads (the attention kernels' hint)",
-    5: "(group, head) slices, non-temporal, 1024 x 8 waves, 2 blocks per iteration",
-    6: "(group, head) slices, non-temporal, 1024 x 8 waves, 4 blocks per iteration",
-    7: "(group, head) slices, non-temporal, 1024 x 16 waves, 2 blocks per iteration",
-    8: "(group, head) slices, non-temporal, a group's 16 heads on one XCD (the kernel's "
-       "mapping and loads, 1024 x 4 waves, 2 blocks per iteration)",
-}
-
-
-def gather_probe(torch, wl, reps: int):
-    """Read-only probes of the cross-attention's page reads (vflorence_amd/csrc/probes):
-    every request's whole pages, all heads, K and V, over the 12 layers' pools, at the
-    granularities of GATHER_VARIANTS, timed back to back with HIP events; then the
-    cross-attention kernel itself.  Prints one JSON line."""
-    from vflorence_amd import _build, hip_attn
-
-    lib = ctypes.CDLL(_build.PROBE_OUTPUT)
-    lib.probe_launch.argtypes = ([ctypes.c_int] + [ctypes.c_void_p] * 5
-                                 + [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p])
-    dev = torch.device("cuda")
-    pages = [wl["pages"][g * BEAMS] for g in range(REQUESTS)]
-    nb = [len(p) for p in pages]
-    width = max(nb)
-    table = torch.zeros(REQUESTS, width, dtype=torch.int32)
-    for g, p in enumerate(pages):
-        table[g, :len(p)] = p
-    num_pages = wl["layers"][0].encoder_attn.k_cache.shape[0]
-    if int(table.max()) >= num_pages or not all(0 < n <= width for n in nb):
-        raise RuntimeError("page table out of the pool")
-    order = hip_attn.balanced_order(wl["enc"], hip_attn.resident_run(dev, NUM_HEADS))
-    if sorted(order) != list(range(REQUESTS)):
-        raise RuntimeError("group order is not a permutation")
-    table_d = table.to(dev)
-    nb_d = torch.tensor(nb, dtype=torch.int32, device=dev)
-    order_d = torch.tensor(order, dtype=torch.int32, device=dev)
-    out = torch.zeros(REQUESTS * NUM_HEADS, dtype=torch.int32, device=dev)
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    block_bytes = NUM_HEADS * BLOCK * HEAD_DIM * 2 * 2  # K and V
-    layer_bytes = sum(nb) * block_bytes
-
-    def sweep(variant):
-        for L in wl["layers"]:
-            rc = lib.probe_launch(variant, L.encoder_attn.k_cache.data_ptr(),
-                                  L.encoder_attn.v_cache.data_ptr(), table_d.data_ptr(),
-                                  nb_d.data_ptr(), order_d.data_ptr(), width, REQUESTS,
-                                  out.data_ptr(), stream)
-            if rc != 0:
-                raise RuntimeError(f"probe variant {variant} failed to launch ({rc})")
-
-    rows = []
-    for v, name in GATHER_VARIANTS.items():
-        secs = time_kernel(torch, lambda: sweep(v), reps) / len(wl["layers"])
-        rows.append({"variant": name, "us_per_layer": round(secs * 1e6, 2),
-                     "tbps": round(layer_bytes / secs / 1e12, 2)})
-        print(f"[probe] {name}: {secs * 1e6:.2f} us", flush=True)
-    c_avg, c_bytes = cross_kernel_timing(torch, wl, reps)
-    print(json.dumps({"gather_probe": rows, "bytes_per_layer": layer_bytes,
-                      "cross_attention_back_to_back_us": round(c_avg * 1e6, 2),
-                      "cross_attention_algorithmic_bytes": int(c_bytes)}), flush=True)
-
-
 def measured_traffic(c_bytes: int):
     """HBM bytes per cross-attention launch from the committed counter summary, if it was
     taken on this same workload (its algorithmic byte count matches); else None."""
@@ -1034,9 +965,6 @@ def main():
     wl = build_workload(torch, args.seed)
     if args.counters:
         counter_pass(torch, wl, reps=2)
-        return
-    if args.gather_probe:
-        gather_probe(torch, wl, args.kernel_reps)
         return
     print("[bench] capturing 128 decode-step graphs", flush=True)
     grouped = not args.ungrouped_self

@@ -126,7 +126,9 @@ int32_t vfl_engine_num_pending_beams(const vfl_engine *engine);
  * (their ids go to admitted[0..*n_admitted), at most admitted_cap), check that the
  * pool covers the step (VFL_HOST_E_FULL otherwise: "KV cache is full"), then make
  * every running row's next position writable in row order.  *n_rows running rows
- * and *n_pairs copy-on-write pairs result.
+ * and *n_pairs copy-on-write pairs result.  On VFL_HOST_E_FULL nothing has changed:
+ * the requests the call would have admitted are back at the head of the waiting
+ * queue in their order and *n_admitted is 0.
  */
 int vfl_engine_schedule(vfl_engine *engine, int64_t *admitted, int32_t admitted_cap,
                         int32_t *n_admitted, int32_t *n_rows, int32_t *n_pairs);

@@ -97,9 +97,9 @@ const char *vfl_get_isa(int dtype, int block_size, int head_dim);
  * key / value are [num_tokens][num_heads][head_dim] with arbitrary token and head
  * strides (in elements) and a contiguous last dimension -- the strided views a
  * fused qkv projection produces.  Negative slots are skipped (padding tokens), as
- * are slots past the end of the pool.  Bit-exact copy.  block_size must be 16, the
- * block size the attention kernels read (VFL_E_UNSUPPORTED otherwise, nothing
- * launched).
+ * are slots past the end of the pool.  Bit-exact copy.  block_size must be 16 or
+ * 32, the block sizes the attention kernels read (VFL_E_UNSUPPORTED otherwise,
+ * nothing launched).
  */
 int vfl_reshape_and_cache(const void *key, const void *value,
                           int64_t key_stride_token, int64_t key_stride_head,
@@ -276,9 +276,11 @@ int vfl_copy_blocks(void *const *caches, int num_caches, const int64_t *src,
  * No counterpart in the reference: vfl_copy_blocks for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  Same copy and semantics; with `staged` non-zero the
- * gather-then-scatter goes through a staging buffer the library holds in each GPU's
- * device memory from the first call on that GPU until the process ends, of
- * VFL_NOALLOC_STAGING_BYTES bytes: num_caches * num_pairs * block_bytes beyond that is
+ * gather-then-scatter goes through a staging buffer of VFL_NOALLOC_STAGING_BYTES
+ * bytes that is part of the library's code object: every GPU on which the library's
+ * module is loaded (at its first kernel launch of any entry point) holds it until the
+ * process ends, whether or not this entry point is ever called.
+ * num_caches * num_pairs * block_bytes beyond that size is
  * refused with VFL_E_INVALID before anything is launched.  No device memory is
  * allocated.  Calls that overlap on one GPU (other streams, other threads) share that
  * buffer and race; serialise them.  The buffer keeps the last call's contents and

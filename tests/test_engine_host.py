@@ -461,6 +461,26 @@ def test_pool_full_raises_and_abort_frees_everything():
     assert sched.is_finished() and sched.block_manager.free_block_ids == [0, 1, 2]
 
 
+def test_pool_full_leaves_the_admission_queue_as_it_was():
+    """A step the pool cannot cover raises before anything changes: the requests it was
+    about to admit are still waiting, in order, so a caller that catches the error and
+    makes room (here: aborts a request) steps on without a reset."""
+    params = SamplingParams(max_tokens=40, eos_token_id=[]).with_defaults(defaults())
+    sched = Scheduler(config(max_num_seqs=4, num_blocks=3))
+    for r in range(4):
+        sched.add(Sequence(r, [1], [3], params))
+    for _ in range(2):  # the failure repeats identically
+        with pytest.raises(RuntimeError, match="KV cache is full"):
+            sched.schedule()
+        assert sched.core.num_waiting == 4 and sched.num_running == 0
+        assert [s.request_id for s in sched.waiting] == [0, 1, 2, 3]
+        assert sched.block_manager.num_free_blocks == 3
+    assert sched.abort_request(3)
+    batch = sched.schedule()
+    assert [s.request_id for s in batch.fresh] == [0, 1, 2] and batch.num_rows == 3
+    assert sched.block_manager.num_free_blocks == 0
+
+
 def test_synthetic_checkpoint_is_deterministic_and_loads_into_transformers():
     from transformers import BartConfig, BartForConditionalGeneration
 

@@ -247,3 +247,56 @@ def test_cpu_tensors_are_rejected():
     k24 = torch.zeros(4, 2, 24, 64, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="block_size=24"):
         hip_attn.reshape_and_cache(x, x, k24, k24, torch.zeros(3, dtype=torch.int64))
+
+
+def _header_struct_layout(tmp_path):
+    """(field, offset) of the header's vfl_sched_meta and its size, as a C compiler lays
+    it out (gcc on a tiny program that includes the header)."""
+    import subprocess
+
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    body = re.search(r"typedef struct vfl_sched_meta \{(.*?)\} vfl_sched_meta;", text, re.S)
+    fields = re.findall(r"\b(\w+)\s*;", body.group(1))
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "vflorence_amd.h"\n'
+                   "int main(void) {\n"
+                   + "".join(f'  printf("{f} %zu\\n", offsetof(vfl_sched_meta, {f}));\n'
+                             for f in fields)
+                   + '  printf("sizeof %zu\\n", sizeof(vfl_sched_meta));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-x", "c", "-I", os.path.join(ROOT, "include"), str(src), "-o",
+                    str(exe)], check=True)
+    lines = subprocess.run([str(exe)], check=True, capture_output=True,
+                           text=True).stdout.split("\n")
+    pairs = [ln.split() for ln in lines if ln]
+    return [(n, int(o)) for n, o in pairs[:-1]], int(pairs[-1][1])
+
+
+def _integration_sched_meta():
+    """Execute the SchedMeta class of INTEGRATION.md's binding snippet (only that class
+    and its size assertion) and return it."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = re.search(r"```python\n(.*?)```", text, re.S).group(1)
+    start = block.index("class SchedMeta(")
+    end = block.index("\n\n", start)
+    snippet = block[start:end]
+    scope = {"ctypes": ctypes}
+    exec(snippet, scope)
+    return scope["SchedMeta"], snippet
+
+
+def test_sched_meta_bindings_match_the_header(tmp_path):
+    """The scheduler-metadata struct has one layout everywhere a caller meets it: the
+    header (compiled), the package's binding and the binding INTEGRATION.md shows a
+    maintainer -- same field names in the same order, same offsets, 64 bytes.  A short
+    copy would let vfl_get_scheduler_metadata write past the caller's struct."""
+    from vflorence_amd import _lib
+
+    c_fields, c_size = _header_struct_layout(tmp_path)
+    assert c_size == 64
+    for binding in (_lib.SchedMeta, _integration_sched_meta()[0]):
+        names = [f for f, _ in binding._fields_]
+        assert names == [f for f, _ in c_fields], binding
+        assert [getattr(binding, f).offset for f in names] == [o for _, o in c_fields]
+        assert ctypes.sizeof(binding) == c_size
+    assert "sizeof(SchedMeta) == 64" in _integration_sched_meta()[1]

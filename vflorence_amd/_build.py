@@ -67,25 +67,6 @@ def build_host_library(verbose: bool = False) -> str:
     return HOST_OUTPUT
 
 
-PROBE_SOURCES = ("probes/gather_probe.hip",)
-PROBE_OUTPUT = os.path.join(HERE, "libvfl_probes.so")
-
-
-def build_probe_library(verbose: bool = False) -> str:
-    """Compile the measurement probes (bench.py --gather-probe) into PROBE_OUTPUT."""
-    tmp = PROBE_OUTPUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, *[os.path.join(CSRC, s) for s in PROBE_SOURCES], "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "'-packed-fp32-ops' is not a recognized feature"
-    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if noise not in ln]
-    if proc.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
-    os.replace(tmp, PROBE_OUTPUT)
-    return PROBE_OUTPUT
-
-
 def build_library(verbose: bool = False) -> str:
     """Compile every HIP source into OUTPUT; always recompiles.  The sources compile to
     objects in parallel (one hipcc per file), then link into the shared library."""
@@ -128,4 +109,3 @@ def build_library(verbose: bool = False) -> str:
 if __name__ == "__main__":
     print(build_library(verbose="-v" in sys.argv))
     print(build_host_library(verbose="-v" in sys.argv))
-    print(build_probe_library(verbose="-v" in sys.argv))

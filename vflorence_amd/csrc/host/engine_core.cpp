@@ -363,8 +363,16 @@ int vfl_engine_schedule(vfl_engine *e, int64_t *admitted, int32_t admitted_cap,
     const int32_t idx = r.cached / pool.block_size;
     writes[i] = idx < (int32_t)r.table.size() ? r.table[idx] : -1;
   }
-  if (pool.blocks_needed(writes.data(), (int32_t)writes.size()) > pool.count)
+  if (pool.blocks_needed(writes.data(), (int32_t)writes.size()) > pool.count) {
+    // Nothing has touched the pool yet: put this call's admissions back at the head of
+    // the waiting queue, in order, so a failed call leaves the engine as it found it.
+    for (int32_t a = 0; a < *n_admitted; ++a) {
+      e->waiting.push_front(std::move(e->running.back()));
+      e->running.pop_back();
+    }
+    *n_admitted = 0;
     return fail(VFL_HOST_E_FULL, "KV cache is full; increase num_blocks");
+  }
   for (Row &r : e->running) {
     int32_t block = -1, src = -1;
     const int st = pool.prepare_write(r.table.data(), (int32_t)r.table.size(), r.cached, &block,
@@ -607,7 +615,10 @@ int vfl_engine_beam_update(vfl_engine *e, const float *scores, const int64_t *id
       }
     }
     if (finish) {
-      if (q.finished.empty())  // every walked candidate lived on or ranked too low
+      // Unreachable: k >= 1, so the request's best candidate (rank 0 < num_beams) became
+      // either a finished hypothesis or a live one, and a request that ends with live
+      // candidates holds num_beams finished ones.  Kept as a guard, not a code path.
+      if (q.finished.empty())
         return fail(VFL_HOST_E_STATE, "beam_update: request %lld ends with no hypothesis",
                     (long long)q.id);
       std::vector<int32_t> best = std::move(q.finished.front().tokens);

@@ -15,7 +15,9 @@ import torch
 
 @dataclass(slots=True)
 class Context:
-    """Per-step metadata shared across decoder attention layers."""
+    """What one decode step hands every decoder layer's attention ops: the self-attention
+    lengths, tables and slots, the query offsets, the self-attention launch metadata,
+    the ISA tag and one cross-attention staging tuple per layer."""
 
     context_lens: torch.Tensor | None = None
     block_tables: torch.Tensor | None = None
@@ -35,6 +37,7 @@ def get_context() -> Context | None:
 
 
 def set_context(**fields) -> None:
-    """Set the global Context for the current model forward pass (no fields: clear it)."""
+    """Publish ``fields`` as the process's Context until the next call; the runner calls
+    it with no fields after each step, which leaves an all-None Context."""
     global _CONTEXT
     _CONTEXT = Context(**fields)
