@@ -145,8 +145,8 @@ int vfl_engine_schedule(vfl_engine *engine, int64_t *admitted, int32_t admitted_
  *   row_requests    [n_rows] each row's request id
  * Row groups for the self-attention kernel: runs of rows of one request (a request's
  * beams are adjacent) cut every max_group rows.  When some group holds more than one
- * row, group_start gets the padded + 1 group starts (padding rows as groups of one,
- * then empty groups up to padded) and *grouped = 1; otherwise order gets the row
+ * row, group_start gets the padded + 1 group starts (padding rows in groups of
+ * max_group, then empty groups up to padded) and *grouped = 1; otherwise order gets the row
  * indices by descending context length, stable (longest first), and *grouped = 0.
  */
 int vfl_engine_pack(const vfl_engine *engine, int32_t padded, int32_t table_width,

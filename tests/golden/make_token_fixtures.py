@@ -22,6 +22,12 @@ suppressed (``min_length`` past ``max_tokens``), length penalty 2 and no repeate
 prompts are drawn from seeded streams; a prompt whose decisive margin at some step
 is below 1e-4 (a tie within fp32 rounding of the accumulated scores) is skipped and
 listed with its margin, and each case stores the prompts it kept.
+
+The reachable-EOS cases (``bart_large_eos``, ``florence2_base_eos``; refreshed alone by
+``python tests/golden/make_token_fixtures.py eos``) add a bias to EOS's final logit so
+that hypotheses end at different steps, with early stopping on and off; their margins
+also include the gap between the best two final hypothesis scores (which finished
+hypothesis is returned).
 """
 
 from __future__ import annotations
@@ -112,7 +118,7 @@ class _CandidateGaps:
         self.model._get_top_k_continuations = self._orig
 
 
-def hf_generate(model, ids: list[int], params: dict):
+def hf_generate(model, ids: list[int], params: dict, final_gap: bool = False):
     kw = dict(max_new_tokens=params["max_tokens"], num_beams=params["num_beams"], do_sample=False,
               repetition_penalty=params["repetition_penalty"], eos_token_id=params["eos_token_id"],
               length_penalty=params["length_penalty"],
@@ -125,6 +131,10 @@ def hf_generate(model, ids: list[int], params: dict):
               decoder_start_token_id=model.config.decoder_start_token_id,
               pad_token_id=model.config.pad_token_id, output_scores=True,
               return_dict_in_generate=True)
+    if final_gap and params["num_beams"] > 1:
+        # every kept hypothesis comes back with its final score: the gap between the best
+        # two decides which one is returned (whatever step they finished at)
+        kw["num_return_sequences"] = params["num_beams"]
     recorder = (_CandidateGaps(model, params["num_beams"], params["max_tokens"])
                 if params["num_beams"] > 1 else None)
     try:
@@ -139,7 +149,11 @@ def hf_generate(model, ids: list[int], params: dict):
         gaps = [float(s[0].topk(2).values.diff().abs()) for s in out.scores]
         return tokens, gaps
     pad = model.config.pad_token_id
-    return [t for t in tokens if t != pad], recorder.gaps
+    gaps = recorder.gaps
+    if final_gap:
+        final = out.sequences_scores
+        gaps = gaps + [float(final[0] - final[1])]
+    return [t for t in tokens if t != pad], gaps
 
 
 def min_gap(gaps):
@@ -154,9 +168,11 @@ def case_record(params, outs):
             "min_gap": [min_gap(gp) for _, gp in outs]}
 
 
-def build(config_kwargs: dict):
+def build(config_kwargs: dict, eos_bias: float = 0.0):
     config = BartConfig(**config_kwargs)
     sd = synthetic_state_dict(config, seed=0)
+    if eos_bias:
+        sd = with_eos_bias(sd, config.eos_token_id, eos_bias)
     model = BartForConditionalGeneration(config).eval()
     missing, unexpected = model.load_state_dict(sd, strict=False)
     assert not unexpected and not [k for k in missing if "embed_tokens" not in k
@@ -182,7 +198,8 @@ FLORENCE_BEAM3 = {**BASE, "max_tokens": 32, "num_beams": 3}
 BEAM_MARGIN = 1e-4
 
 
-def beam_case(model, vocab: int, params: dict, count: int, length_fn, seed: int, tag: str):
+def beam_case(model, vocab: int, params: dict, count: int, length_fn, seed: int, tag: str,
+              final_gap: bool = False):
     """``count`` prompts drawn in order from a seeded stream (lengths from ``length_fn``),
     each generated with ``params``; a prompt with a decisive margin below BEAM_MARGIN is
     skipped and recorded in ``skipped``."""
@@ -191,7 +208,7 @@ def beam_case(model, vocab: int, params: dict, count: int, length_fn, seed: int,
     while len(kept) < count:
         n = length_fn(g)
         ids = torch.randint(3, vocab, (n,), generator=g).tolist()
-        tokens, gaps = hf_generate(model, ids, params)
+        tokens, gaps = hf_generate(model, ids, params, final_gap)
         margin = min_gap(gaps)
         print(tag, n, len(tokens), margin, flush=True)
         if margin is None or margin < BEAM_MARGIN:
@@ -215,6 +232,51 @@ def florence2_base() -> dict:
     cases["beam3"] = beam_case(model, config.vocab_size, FLORENCE_BEAM3, 6, lambda g: 587,
                                seed=5, tag="florence2_base beam3")
     return {"config": FLORENCE_BASE, "checksum": checksum, "prompts": reqs, "cases": cases}
+
+
+def with_eos_bias(state_dict: dict, eos: int, bias: float) -> dict:
+    """The checkpoint with ``bias`` added to ``final_logits_bias[0, eos]`` (one fp32 add,
+    the same bits on any device)."""
+    out = dict(state_dict)
+    flb = out["final_logits_bias"].clone()
+    flb[0, eos] += bias
+    out["final_logits_bias"] = flb
+    return out
+
+
+# Reachable EOS at real depth (the reference's early-stopping check,
+# tests/test_parity.py:88-122: an EOS logit bias plus min_length so that beams finish
+# at different steps).  With random weights every token's log-probability sits near
+# -ln(vocab); the bias lifts EOS to the edge of the kept candidates, so hypotheses end
+# at different steps and the EOS rank gate, finished-hypothesis scoring and both
+# early-stopping rules decide the outputs.  Biases chosen by a sweep over the two
+# shapes (BART-large: 1.8 never ends before 24 tokens on most prompts, 1.9 ends every
+# prompt at min_length; Florence-2-base: 1.5 ends prompts at 10-13 tokens and the two
+# early-stopping rules part).
+EOS_CASES = {
+    "bart_large_eos": dict(config=LARGE, eos_bias=1.85, beams=4, max_tokens=24, count=8,
+                           lengths=lambda g: int(torch.randint(128, 1025, (1,), generator=g)),
+                           seed=8),
+    "florence2_base_eos": dict(config=FLORENCE_BASE, eos_bias=1.5, beams=3, max_tokens=32,
+                               count=6, lengths=lambda g: 587, seed=9),
+}
+
+
+def eos_fixtures() -> dict:
+    out = {}
+    for name, spec in EOS_CASES.items():
+        config, model, checksum = build(spec["config"], spec["eos_bias"])
+        cases = {}
+        for early in (False, True):
+            params = {**BASE, "max_tokens": spec["max_tokens"], "num_beams": spec["beams"],
+                      "min_length": 4, "early_stopping": early}
+            key = f"beam{spec['beams']}_eos" + ("_early" if early else "")
+            cases[key] = beam_case(model, config.vocab_size, params, spec["count"],
+                                   spec["lengths"], seed=spec["seed"], tag=f"{name} {key}",
+                                   final_gap=True)
+        out[name] = {"config": spec["config"], "eos_bias": spec["eos_bias"],
+                     "checksum": checksum, "cases": cases}
+    return out
 
 
 def main():
@@ -254,10 +316,20 @@ def main():
     fixtures["bart_large"] = {"config": LARGE, "checksum": checksum, "prompts": reqs,
                               "cases": cases}
     fixtures["florence2_base"] = florence2_base()
+    fixtures.update(eos_fixtures())
     with open(OUT, "w") as f:
         json.dump(fixtures, f)
     print("wrote", OUT)
 
 
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["eos"]:  # add or refresh only the reachable-EOS sections
+        torch.set_num_threads(min(8, os.cpu_count() or 1))
+        with open(OUT) as f:
+            fixtures = json.load(f)
+        fixtures.update(eos_fixtures())
+        with open(OUT, "w") as f:
+            json.dump(fixtures, f)
+        print("wrote", OUT)
+    else:
+        main()

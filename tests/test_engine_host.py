@@ -15,6 +15,7 @@ import torch
 
 from oracle.engine_host import HostOracle
 from vflorence_amd.engine.block_manager import BlockManager
+from vflorence_amd.engine.model_runner import launch_slots, row_buckets
 from vflorence_amd.engine.scheduler import Scheduler
 from vflorence_amd.engine.sequence import Sequence
 from vflorence_amd.layers.logits_processor import LogitsProcessor
@@ -418,6 +419,12 @@ def test_host_core_equals_the_oracle_step_by_step(beams, early, lp, seed):
                 assert starts[0] == 0 and starts[-1] == padded
                 for g in range(len(starts) - 1):  # each group: rows of one request
                     assert len({rids[r] for r in range(starts[g], min(starts[g + 1], n))}) <= 1
+                # once every request runs all its beams (a new request runs one row on
+                # its first step), the groups fit the runner's sized launches
+                groups = int(np.searchsorted(starts, padded))
+                per_request = [rids.count(q) for q in set(rids)]
+                if all(c == beams for c in per_request):
+                    assert groups <= launch_slots(padded, n - 1, beams, 8)
             else:
                 order = views["order"][:padded].tolist()
                 ctx = views["context_lens"][:padded].tolist()
@@ -445,6 +452,24 @@ def test_host_core_equals_the_oracle_step_by_step(beams, early, lp, seed):
     assert rid == 14 and step > 10
     if beams > 1:
         assert seen_pairs > 0 and seen_groups > 0
+
+
+@pytest.mark.parametrize("beams", [1, 2, 3, 4, 5, 8, 10])
+def test_launch_slots_cover_every_batch_of_a_bucket(beams):
+    """For every row bucket and every batch of whole requests that pads to it, the
+    groups the packed step forms (requests cut every 8 rows, padding rows in groups of
+    8) fit the launch's slots, and the slots are no more than the bucket's rows."""
+    buckets = row_buckets(512)
+    for i, padded in enumerate(buckets):
+        below = buckets[i - 1] if i else 0
+        slots = launch_slots(padded, below, beams, 8)
+        assert slots <= padded
+        for n in range(below + 1, padded + 1):
+            if n % beams:
+                continue
+            groups = n // beams * -(-beams // 8) + -(-(padded - n) // 8)
+            assert groups <= slots, (padded, n)
+    assert launch_slots(256, 224, 4, 8) == 64  # 64 requests x 4 beams: 64 of 256 slots
 
 
 def test_pool_full_raises_and_abort_frees_everything():

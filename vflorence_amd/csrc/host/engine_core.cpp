@@ -453,7 +453,9 @@ int vfl_engine_pack(const vfl_engine *e, int32_t padded, int32_t table_width, in
       group_start[groups++] = i;
   }
   if (groups < n) {  // some group holds several rows: beam groups
-    for (int32_t i = n; i < padded; ++i) group_start[groups++] = i;  // padding: groups of one
+    // padding rows (empty contexts) in groups of max_group, so a launch sized for the
+    // real groups plus a few covers them
+    for (int32_t i = n; i < padded; i += max_group) group_start[groups++] = i;
     for (int32_t g = groups; g <= padded; ++g) group_start[g] = padded;
     *grouped = 1;
   } else {

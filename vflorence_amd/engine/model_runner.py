@@ -71,7 +71,6 @@ class _StepBuffers:
         self.h = self._views(self.host)
         self.d = self._views(self.dev)
         self.np = {k: v.numpy() for k, v in self.h.items()}
-        self.device_plan = hip_attn.GroupPlan(self.d["plan"], self.plan_stride, rows, width)
 
     def _views(self, buf):
         r, w = self.rows, self.width
@@ -85,9 +84,10 @@ class _StepBuffers:
         out["plan"] = buf[self.plan_offset:]
         return out
 
-    def build_plan(self, padded: int, num_blocks: int, block_size: int) -> None:
+    def build_plan(self, padded: int, num_blocks: int, block_size: int) -> int:
         """The beam groups' plan for this step's ``padded`` rows, from the packed tables,
-        lengths and group starts (slots = groups in row order, then empty ones)."""
+        lengths and group starts (slots = groups in row order, then empty ones); returns
+        the number of groups."""
         gs = self.np["group_start"]
         groups = int(np.searchsorted(gs[: padded + 1], padded))
         h = self.h
@@ -96,6 +96,7 @@ class _StepBuffers:
             padded, h["group_start"].data_ptr(), None, groups, block_size, num_blocks,
             h["plan"].data_ptr(), self.rows, self.plan_stride))
         self._plan_words = 4 + groups * self.plan_stride
+        return groups
 
     def upload(self, grouped: bool = False) -> None:
         words = self.plan_offset + (self._plan_words if grouped else 0)
@@ -120,6 +121,23 @@ def _to_host(*tensors: torch.Tensor) -> list[torch.Tensor]:
     if any(t.is_cuda for t in tensors):
         torch.cuda.current_stream().synchronize()
     return out
+
+
+def launch_slots(padded: int, below: int, beams: int, max_group: int) -> int:
+    """Row-group slots an attention launch over a bucket of ``padded`` rows needs when
+    its real rows are whole requests of ``beams`` rows each (more than ``below`` rows:
+    the next smaller bucket), cut into groups of at most ``max_group`` rows, and the
+    padding rows form groups of ``max_group``: the most groups any such batch makes.
+    A launch sized this way spends no workgroups on slots no group can reach (64
+    requests x 4 beams: 64 slots instead of 256).  ``padded`` when no row count of the
+    bucket is a multiple of ``beams``.  A step whose groups exceed it (a request runs a
+    single row on its first step) launches one slot per row instead."""
+    per_request = -(-beams // max_group)
+    most = 0
+    for n in range(below + 1, padded + 1):
+        if n % beams == 0:
+            most = max(most, n // beams * per_request + -(-(padded - n) // max_group))
+    return most or padded
 
 
 def row_buckets(max_rows: int) -> list[int]:
@@ -163,10 +181,12 @@ class ModelRunner:
         self._cross_buffers = attention.CrossStagingBuffers(
             config.max_num_seqs, math.ceil(config.max_encoder_len / self.block_size), self.device)
         # decode steps captured per batch size (rows), replayed while the shapes repeat
-        self._graphs: dict[tuple[int, bool, int], tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self._graphs: dict[tuple, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self._step_grouped = False
         self._buckets = row_buckets(config.max_num_seqs)
-        self._self_metadata: dict[tuple[int, bool], hip_attn.SchedulerMetadata] = {}
+        self._self_metadata: dict[tuple[int, bool, int], hip_attn.SchedulerMetadata] = {}
+        self._slots: dict[tuple[int, int], int] = {}
+        self._step_slots = 0
         self._no_pages = torch.zeros(0, dtype=torch.int32)
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
         # the decoder step; compiled as the reference compiles it when asked
@@ -295,31 +315,39 @@ class ModelRunner:
         # self-attention runs as row groups that read each shared block once; the group
         # list is padded with empty groups so one launch shape serves every n-row batch.
         grouped = core.pack(padded, buf.width, hip_attn.MAX_GROUP_SIZE, h)
+        beams = batch.sampling_params.num_beams if batch.sampling_params else 1
+        slots = self._launch_slots(padded, beams)
         if grouped:
-            buf.build_plan(padded, self.config.num_blocks, self.block_size)
+            groups = buf.build_plan(padded, self.config.num_blocks, self.block_size)
+            self_slots = slots if groups <= slots else padded
+        else:
+            self_slots = padded
         buf.upload(grouped)
         d = buf.d
         if num_pairs:  # copy-on-write first: this step writes into the now-private blocks
             src, dst = h["copy_src"][:num_pairs], h["copy_dst"][:num_pairs]
             staged = not set(src.tolist()).isdisjoint(dst.tolist())
             self._copier(d["copy_src"][:num_pairs], d["copy_dst"][:num_pairs], staged=staged)
-        # the plan points at fixed views of the step buffers: one per (rows, grouped)
+        # the plan points at fixed views of the step buffers: one per (rows, grouped,
+        # group slots)
         bs = self.block_size
-        self_metadata = self._self_metadata.get((padded, grouped))
+        self_metadata = self._self_metadata.get((padded, grouped, self_slots))
         if self_metadata is None:
             common = dict(num_reqs=padded, num_heads=self.num_heads, num_kv_heads=self.num_heads,
                           head_dim=self.head_dim, dtype=self.dtype, block_size=bs,
                           fuse_kv_write=True)
-            if grouped:  # the groups' blocks come from the step's plan
+            if grouped:  # the groups' blocks come from the step's plan, self_slots slots
+                plan = hip_attn.GroupPlan(d["plan"], buf.plan_stride, self_slots, buf.width)
                 self_metadata = hip_attn.get_scheduler_metadata(
-                    group_start=d["group_start"][: padded + 1],
+                    group_start=d["group_start"][: self_slots + 1],
                     max_group_size=hip_attn.MAX_GROUP_SIZE, own_tables=True,
-                    group_plan=buf.device_plan, **common)
+                    group_plan=plan, **common)
             else:  # one row per workgroup, longest context first
                 self_metadata = hip_attn.get_scheduler_metadata(
                     group_order=d["order"][:padded], **common)
-            self._self_metadata[(padded, grouped)] = self_metadata
+            self._self_metadata[(padded, grouped, self_slots)] = self_metadata
         self._step_grouped = grouped
+        self._step_slots = self_slots
         rows = h["row_requests"][:n]
         key = (padded, rows.tobytes())
         if key != self._cross_key:
@@ -328,7 +356,8 @@ class ModelRunner:
             pages = pages + (self._no_pages,) * (padded - n)
             enc_lens = enc_lens + (0,) * (padded - n)
             self._cross_staged = attention.stage_cross(self.decoder_layers, pages, enc_lens, bs,
-                                                       self.isa, buffers=self._cross_buffers)
+                                                       self.isa, buffers=self._cross_buffers,
+                                                       slots=slots)
             self._cross_key = key
         set_context(
             context_lens=d["context_lens"][:padded],
@@ -340,6 +369,17 @@ class ModelRunner:
             cross_staged=self._cross_staged,
         )
         return d["input_ids"][:padded], d["positions"][:padded]
+
+    def _launch_slots(self, padded: int, beams: int) -> int:
+        """Group slots of this bucket's attention launches at this beam width."""
+        key = (padded, beams)
+        slots = self._slots.get(key)
+        if slots is None:
+            i = self._buckets.index(padded) if padded in self._buckets else -1
+            below = self._buckets[i - 1] if i > 0 else 0
+            slots = self._slots[key] = launch_slots(padded, below, beams,
+                                                    hip_attn.MAX_GROUP_SIZE)
+        return slots
 
     # -- sampling ----------------------------------------------------------------------
 
@@ -429,7 +469,7 @@ class ModelRunner:
         # the batch's number of requests (one capture per count the batches use)
         cross_meta = self._cross_staged[0][4]
         cross_waves = cross_meta.plan(n, self._cross_buffers.max_pages).waves_per_workgroup
-        key = (n, self._step_grouped, cross_waves)
+        key = (n, self._step_grouped, cross_waves, self._step_slots, cross_meta.num_groups)
         entry = self._graphs.get(key)
         if entry is None:
             side = torch.cuda.Stream()

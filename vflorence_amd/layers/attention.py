@@ -45,7 +45,8 @@ class CrossStagingBuffers:
 
     int32 words: lengths [max_rows] | group starts [max_rows + 1] | dispatch order
     [max_rows] | page table [max_rows, max_pages].  Every batch of n rows uses the
-    same addresses and launch shape (n groups, unused slots marked -1 in the order),
+    same addresses and launch shape (a group slot count fixed per row count and beam
+    width, unused slots marked -1 in the order),
     so a decode step captured in a HIP graph stays valid when the batch's requests,
     and hence its beam groups and pages, change.
     """
@@ -61,14 +62,16 @@ class CrossStagingBuffers:
         self.np = self.host.numpy()
         self.offsets = (0, m, 2 * m + 1, 3 * m + 1)
 
-    def views(self, n: int):
-        o = self.offsets
-        return (self.dev[o[0]: o[0] + n], self.dev[o[1]: o[1] + n + 1], self.dev[o[2]: o[2] + n],
+    def views(self, n: int, slots: int | None = None):
+        """Lengths and table of ``n`` rows; group starts and order of ``slots`` launch
+        slots (default ``n``)."""
+        o, g = self.offsets, n if slots is None else slots
+        return (self.dev[o[0]: o[0] + n], self.dev[o[1]: o[1] + g + 1], self.dev[o[2]: o[2] + g],
                 self.dev[o[3]: o[3] + self.max_rows * self.max_pages]
                 .view(self.max_rows, self.max_pages)[:n])
 
 
-def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts, run):
+def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts, run, slots=None):
     n = len(pages)
     if n > buffers.max_rows or max(len(p) for p in pages) > buffers.max_pages:
         raise ValueError(f"{n} rows / {max(len(p) for p in pages)} pages exceed the staging "
@@ -89,17 +92,20 @@ def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts, run):
         table[i, len(p):] = 0
     buffers.dev.copy_(buffers.host, non_blocking=True)
     buffers.copied.record()
-    return buffers.views(n)
+    return buffers.views(n, slots)
 
 
-def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=None):
+def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=None,
+                slots=None):
     """Point this step's sequences at their encoder K/V pages in each layer's pool.
 
     ``pages[i]`` (int32 tensor) and ``enc_lens[i]`` belong to running sequence i; beams
     of one request repeat its pages.  Nothing is copied: the padded block table,
     lengths and beam groups go to the device once and every layer shares them.
     With ``buffers`` (a ``CrossStagingBuffers``) they go to its fixed addresses
-    instead of a fresh allocation, with one launch slot per row.
+    instead of a fresh allocation, with ``slots`` launch slots (one per row when not
+    given, or when the rows form more groups than that), the unused ones exiting at
+    once.
     """
     attn = layers[0].encoder_attn
     device = attn.k_cache.device
@@ -111,8 +117,10 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=N
     run = hip_attn.resident_run(device, attn.num_heads) if device.type == "cuda" else 1
     active = None
     if buffers is not None:
+        if slots is None or not ng <= slots <= n:
+            slots = n
         seq_lens, group_start, group_order, block_table = _stage_into(buffers, pages, enc_lens,
-                                                                      starts, run)
+                                                                      starts, run, slots)
         # n slots, about n / (beams per request) of them working: waves per workgroup as
         # for a launch of that many groups (4 beams of 64 requests: 1024 workgroups and
         # eight waves, not the 4096 slots' four).  Slots over beam width, not the exact
