@@ -57,6 +57,9 @@ def parse_args():
     p.add_argument("--table-walk", action="store_true",
                    help="grouped self-attention walks the block tables in every launch "
                         "instead of reading the step's group plan")
+    p.add_argument("--separate-copy", action="store_true",
+                   help="copy-on-write as its own launch before each step's attention instead "
+                        "of folded into the self-attention launches")
     p.add_argument("--ungrouped-self", action="store_true",
                    help="self-attention one row per workgroup (no shared-prefix groups)")
     p.add_argument("--counters", action="store_true",
@@ -135,15 +138,24 @@ def step_bytes(plan, enc, elem=2, grouped=True, self_only=False):
     if self_only:
         return self_b
     cross_b = workloads.cross_attention_bytes(enc, rows, NUM_HEADS, HEAD_DIM, elem, BLOCK)
-    cow_b = len(plan.copies) * 2 * NUM_LAYERS * (NUM_HEADS * BLOCK * HEAD_DIM * elem) * 2
+    cow_b = cow_bytes(plan, elem)
     return NUM_LAYERS * (self_b + cross_b) + cow_b, self_b, cross_b, cow_b
 
 
-def capture_steps(torch, wl, grouped=True, keep_outputs=False, planned=True):
+def cow_bytes(plan, elem=2):
+    """Copy-on-write bytes of a step: each pair's block read and written in the K and V
+    pools of every layer."""
+    return len(plan.copies) * 2 * NUM_LAYERS * (NUM_HEADS * BLOCK * HEAD_DIM * elem) * 2
+
+
+def capture_steps(torch, wl, grouped=True, keep_outputs=False, planned=True, fold_copies=True):
     """One HIP graph per decode step of the schedule.  ``grouped``: each request's beams
     form one self-attention row group (own tables, shared blocks read once).
     ``planned``: grouped launches read the step's group plan (made on the host from the
     step's tables, uploaded before capture) instead of walking the block tables.
+    ``fold_copies`` (planned only): the step's copy-on-write pairs ride in its plan and
+    each layer's self-attention launch copies them for its pools; otherwise one
+    copy_blocks launch over all pools opens the step.
     ``keep_outputs``: also return, per step, the [(self out, cross out)] per layer that
     its graph writes (every step keeps its own output buffers)."""
     from vflorence_amd import hip_attn
@@ -173,10 +185,16 @@ def capture_steps(torch, wl, grouped=True, keep_outputs=False, planned=True):
             starts = starts_h.to(dev)
             order = None
             if planned:
-                gplan = hip_attn.build_group_plan(
+                nblocks = wl["layers"][0].self_attn.k_cache.shape[0]
+                host_plan = hip_attn.build_group_plan(
                     tables.cpu(), lens.cpu(), starts_h, max_group_size=BEAMS,
-                    block_size=BLOCK, num_blocks=wl["layers"][0].self_attn.k_cache.shape[0],
-                ).to(dev)
+                    block_size=BLOCK, num_blocks=nblocks)
+                if fold_copies and plan.copies:
+                    if not hip_attn.fold_plan_copies(host_plan, [a for a, _ in plan.copies],
+                                                     [b for _, b in plan.copies],
+                                                     num_blocks=nblocks):
+                        raise RuntimeError(f"step {t}: copy pairs cannot be folded")
+                gplan = host_plan.to(dev)
             meta = hip_attn.get_scheduler_metadata(
                 num_reqs=rows, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS, head_dim=HEAD_DIM,
                 dtype=torch.bfloat16, block_size=BLOCK, group_start=starts,
@@ -190,7 +208,7 @@ def capture_steps(torch, wl, grouped=True, keep_outputs=False, planned=True):
                 dtype=torch.bfloat16, block_size=BLOCK, group_order=order, fuse_kv_write=True)
         src = dst = None
         staged = False
-        if plan.copies:
+        if plan.copies and not (planned and grouped and fold_copies):
             src = torch.tensor([s for s, _ in plan.copies], dtype=torch.int64, device=dev)
             dst = torch.tensor([d for _, d in plan.copies], dtype=torch.int64, device=dev)
             staged = hip_attn.copy_pairs_need_staging(plan.copies)
@@ -283,10 +301,11 @@ def workloads_cross_bytes(wl) -> int:
                                            BLOCK)
 
 
-def self_in_step_table(durations, plans, grouped):
+def self_in_step_table(durations, plans, grouped, folded=False):
     """In-step self-attention launches (``durations`` in launch order, NUM_LAYERS per
     step) by the step's context length: mean duration and algorithmic GB/s per bucket
-    of decode steps."""
+    of decode steps (``folded``: each launch also copies its layer's share of the
+    step's copy-on-write bytes, which count with it)."""
     if len(durations) != len(plans) * NUM_LAYERS:
         return None
     buckets = ((0, 16), (16, 32), (32, 64), (64, 96), (96, 128))
@@ -295,6 +314,8 @@ def self_in_step_table(durations, plans, grouped):
         secs, nbytes, n = 0.0, 0, 0
         for t in range(lo, min(hi, len(plans))):
             b = step_bytes(plans[t], None, grouped=grouped, self_only=True)
+            if folded:
+                b += cow_bytes(plans[t]) // NUM_LAYERS
             for s_ in durations[t * NUM_LAYERS:(t + 1) * NUM_LAYERS]:
                 secs += s_
                 nbytes += b
@@ -969,7 +990,8 @@ def main():
     print("[bench] capturing 128 decode-step graphs", flush=True)
     grouped = not args.ungrouped_self
     planned = grouped and not args.table_walk
-    graphs, keep = capture_steps(torch, wl, grouped, planned=planned)
+    folded = planned and not args.separate_copy
+    graphs, keep = capture_steps(torch, wl, grouped, planned=planned, fold_copies=folded)
     plans = wl["plans"]
     per_step = [step_bytes(p, wl["enc"], grouped=grouped) for p in plans]
 
@@ -1022,7 +1044,7 @@ def main():
         cross_in_step = in_step["cross"]
         c_step_avg = sum(cross_in_step) / len(cross_in_step)
         self_key = ("self" if planned else "self_walk") if grouped else "self_rows"
-        self_by_ctx = self_in_step_table(in_step[self_key], wl["plans"], grouped)
+        self_by_ctx = self_in_step_table(in_step[self_key], wl["plans"], grouped, folded)
         cow = in_step["cow"]
         measured_over = (f"{len(cross_in_step)} launches inside the decode-step graphs, one "
                          f"pass over the whole {DECODE_STEPS}-step schedule (torch.profiler "
@@ -1119,6 +1141,7 @@ def main():
             },
             "self_attention_in_step_by_context": self_by_ctx,
             "copy_on_write_in_step": {
+                "folded_into_self_attention": folded,
                 "launches": len(cow),
                 "avg_us": round(sum(cow) / len(cow) * 1e6, 2) if cow else None,
                 "gbps": (round(sum(step_bytes(p, wl_enc, grouped=grouped)[3]

@@ -176,6 +176,26 @@ int vfl_build_group_plan(const int32_t *block_table, int64_t block_table_stride,
                          int32_t *plan, int64_t num_slots, int64_t stride);
 
 /*
+ * Host function (all pointers host memory; no device call).  Folds a decode step's
+ * copy-on-write pairs into its group plan -- the batched block copy that replaces the
+ * loop of vflorence/engine/model_runner.py:162-167, which the reference runs before the
+ * step's KV writes (:284-286).  For each pair the plan entry holding block dst[i]
+ * records src[i] as its copy source; vfl_self_attention_with_kv_write with that plan
+ * then reads the source block instead of dst[i], stores it whole to dst[i] with the
+ * row's new token in place (each layer's launch for its own pools), and the step needs
+ * no vfl_copy_blocks launch.  Only the fused launch acts on copy sources (the plain
+ * attention launch reads every entry's own block), and it relies on the fused write's
+ * contract: dst[i] is the block of a row's last context position, which no other row
+ * reads.  plan: the used slots of vfl_build_group_plan's output (num_slots and stride
+ * as given to it).  Refused (VFL_E_INVALID, plan unchanged) when a block is out of
+ * [0, num_blocks), a destination repeats or is also a source, or a destination is not
+ * exactly one single-row entry of the plan; the caller then copies the pairs itself.
+ */
+int vfl_fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
+                         const int64_t *src, const int64_t *dst, int64_t num_pairs,
+                         int64_t num_blocks);
+
+/*
  * Replaces vllm_cpu_attn.attention_with_kv_cache(query, k_cache, v_cache, out,
  * query_start_loc, seq_lens, scale=, causal=, block_table=, scheduler_metadata=)
  * on its decode path (vflorence/layers/attention.py:61-72 for self-attention,

@@ -462,8 +462,8 @@ def test_continuous_batching_stress_florence2_large_shape():
 def test_beam_step_uploads_the_group_plan_of_its_tables(dtype):
     """A beam-search step's beam groups run from the group plan the runner builds on the
     host: the plan in HBM (its used part) equals build_group_plan over the step's
-    uploaded tables, lengths and group starts, and the self-attention metadata points at
-    it."""
+    uploaded tables, lengths and group starts with the step's copy-on-write pairs folded
+    in, and the self-attention metadata points at it."""
     from vflorence_amd import Request, SamplingParams, hip_attn
     from vflorence_amd.utils.context import get_context, set_context
 
@@ -493,17 +493,26 @@ def test_beam_step_uploads_the_group_plan_of_its_tables(dtype):
         want = hip_attn.build_group_plan(
             ctx.block_tables.cpu(), ctx.context_lens.cpu(), gs[: groups + 1], num_slots=buf.rows,
             max_group_size=hip_attn.MAX_GROUP_SIZE, num_blocks=runner.config.num_blocks)
+        # the step's copy-on-write pairs ride in the plan (bf16/fp16: the fused launch
+        # copies them)
+        pairs = batch.num_pairs
+        src = buf.d["copy_src"][:pairs].cpu().numpy()
+        dst = buf.d["copy_dst"][:pairs].cpu().numpy()
+        assert pairs > 0
+        assert hip_attn.fold_plan_copies(want, src, dst, num_blocks=runner.config.num_blocks)
         used = 4 + groups * want.stride
         got = sm.group_plan.words[:used].cpu()
         # compare header and the entries each slot holds (the rest of a slot is unused)
         assert int(got[0]) == groups == int(want.words[0])
-        shared = 0
+        shared = copies = 0
         for s in range(groups):
             a = got[4 + s * want.stride:]
             b = want.words[4 + s * want.stride:]
             n = int(b[2])
-            assert torch.equal(a[:4 + 2 * n], b[:4 + 2 * n]), s
-            shared += sum(bin(int(b[5 + 2 * e]) & 0xFF).count("1") > 1 for e in range(n))
+            assert torch.equal(a[:12 + 2 * n], b[:12 + 2 * n]), s  # header, sources, entries
+            shared += sum(bin(int(b[13 + 2 * e]) & 0xFF).count("1") > 1 for e in range(n))
+            copies += sum(int(b[13 + 2 * e]) < 0 for e in range(n))  # flagged fork blocks
         assert shared > 0  # beams share prefix blocks
+        assert copies == pairs  # every pair rides in the plan
         set_context()
     llm.abort()

@@ -259,6 +259,100 @@ def test_planned_beam_search_tables_fused_equals_two_steps(beams):
         oracle_check(o1, fused, k1, v1, L, table)
 
 
+def beam_step(beams, step, seed):
+    from vflorence_amd.workloads import beam_decode_schedule
+
+    R = 6
+    plans = beam_decode_schedule(num_requests=R, beams=beams, steps=step + 1, cow_fraction=0.3,
+                                 seed=seed)
+    p = plans[step]
+    N = len(p.context_lens)
+    width = max(len(t) for t in p.block_tables)
+    table = torch.zeros(N, width, dtype=torch.int32)
+    for i, t in enumerate(p.block_tables):
+        table[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    NB = 1 + max(max(max(t) for t in q.block_tables) for q in plans)
+    starts = torch.arange(0, R * beams + 1, beams, dtype=torch.int32)
+    return p, table, NB, starts
+
+
+@pytest.mark.parametrize("beams", [4, 3])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("waves", [1, 2, 4])
+def test_fused_launch_with_folded_copies_equals_copy_then_fused_launch(beams, head_dim, waves):
+    """Copy-on-write folded into the plan: the fused launch reads each fork's source
+    block, stores it whole to the fork's block with the new token in place and attends
+    to it -- caches and outputs bit-identical to copy_blocks followed by the same fused
+    launch (the reference's order, model_runner.py:284-286), stale tails included."""
+    hip_attn = hip()
+    H, D = 16, head_dim
+    for step in (17, 33, 50):
+        p, table, NB, starts = beam_step(beams, step, seed=10 * beams + step)
+        assert p.copies
+        N = len(p.context_lens)
+        g = torch.Generator().manual_seed(step)
+        kc = torch.randn(NB, H, BS, D, generator=g).to(torch.bfloat16)
+        vc = torch.randn(NB, H, BS, D, generator=g).to(torch.bfloat16)
+        fused = torch.randn(N, 3 * H * D, generator=g).to(torch.bfloat16).to(DEV)
+        q, k, v = (t.reshape(N, H, D) for t in fused.chunk(3, dim=-1))
+        L = torch.tensor(p.context_lens, dtype=torch.int32)
+        slots = torch.tensor(p.slot_mapping, dtype=torch.int64).to(DEV)
+        src = [a for a, _ in p.copies]
+        dst = [b for _, b in p.copies]
+        results = []
+        for fold in (False, True):
+            kd, vd = kc.to(DEV), vc.to(DEV)
+            plan = hip_attn.build_group_plan(table, L, starts, block_size=BS, num_blocks=NB)
+            if fold:
+                assert hip_attn.fold_plan_copies(plan, src, dst, num_blocks=NB)
+            else:
+                hip_attn.copy_blocks([kd, vd], torch.tensor(src, device=DEV),
+                                     torch.tensor(dst, device=DEV), staged=False)
+            sm = planned_metadata(N, H, D, q.dtype, starts, plan.to(DEV), waves, True)
+            out = torch.empty(q.shape, dtype=q.dtype, device=DEV)
+            hip_attn.self_attention_with_kv_write(q, k, v, kd, vd, out, L.to(DEV), slots,
+                                                  scale=D**-0.5, block_table=table.to(DEV),
+                                                  scheduler_metadata=sm)
+            torch.cuda.synchronize()
+            results.append((out.cpu(), kd.cpu(), vd.cpu()))
+        (o0, k0, v0), (o1, k1, v1) = results
+        assert np.array_equal(bits(k0), bits(k1)) and np.array_equal(bits(v0), bits(v1))
+        assert np.array_equal(bits(o0), bits(o1))
+        # the copies happened: every fork's block holds its source's tokens
+        for a, b in p.copies:
+            assert not np.array_equal(bits(kc[b]), bits(k1[b]))
+
+
+def test_plain_launch_reads_entries_own_blocks_whatever_their_copy_source():
+    """Only the fused launch acts on copy sources: attention_with_kv_cache with a folded
+    plan reads every entry's own block (bit-identical to the unfolded plan) and writes
+    no cache."""
+    hip_attn = hip()
+    H, D = 16, 64
+    p, table, NB, starts = beam_step(4, 33, seed=5)
+    N = len(p.context_lens)
+    g = torch.Generator().manual_seed(3)
+    kc = torch.randn(NB, H, BS, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(NB, H, BS, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(N, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    L = torch.tensor(p.context_lens, dtype=torch.int32)
+    outs = []
+    for fold in (False, True):
+        kd, vd = kc.to(DEV), vc.to(DEV)
+        plan = hip_attn.build_group_plan(table, L, starts, block_size=BS, num_blocks=NB)
+        if fold:
+            assert hip_attn.fold_plan_copies(plan, [a for a, _ in p.copies],
+                                             [b for _, b in p.copies], num_blocks=NB)
+        sm = planned_metadata(N, H, D, q.dtype, starts, plan.to(DEV), 2, False)
+        out = torch.empty_like(q)
+        hip_attn.attention_with_kv_cache(q, kd, vd, out, None, L.to(DEV), scale=D**-0.5,
+                                         block_table=table.to(DEV), scheduler_metadata=sm)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(kd.cpu()), bits(kc)) and np.array_equal(bits(vd.cpu()), bits(vc))
+        outs.append(out.cpu())
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+
+
 def test_plan_for_another_table_width_is_refused():
     fused, kc, vc, L, table, _, starts = prefix_tree_case([4, 4], seed=1)
     N, H, D = fused.shape[0], 16, 64

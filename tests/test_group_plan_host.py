@@ -1,7 +1,9 @@
 """The group-plan builder (``vfl_build_group_plan``, host code, no device): its output
 against a plain restatement of the definition on random beam-like tables, the
 coverage property every planned launch relies on (each (row, position) a row reads
-is in exactly one entry of its position, with the row's bit), and its refusals."""
+is in exactly one entry of its position, with the row's bit), and its refusals; the
+copy-on-write fold (``vfl_fold_plan_copies``) on the block tables and copy pairs of a
+beam search through the BlockManager, and its refusals (plan unchanged)."""
 
 import math
 
@@ -54,15 +56,33 @@ def restated(table, lens, starts, order, slots, width, num_blocks):
     return out
 
 
-def decoded(plan):
+HEADER, ENTRY = 12, 2  # words of a slot's header (4 + 8 rows' copy sources), of an entry
+
+
+def decoded(plan, copies=False):
+    """(used slots, [(first row, rows, widest, entries)]); an entry is (id, position,
+    tokens, rows) -- with ``copies``, plus the copy source of a flagged entry's row or
+    -1.  Without ``copies`` no entry may be flagged nor any row have a source."""
     w = plan.words.numpy()
     out = []
     for s in range(plan.slots):
         rec = w[4 + s * plan.stride:]
         n = int(rec[2])
-        ents = [(int(rec[4 + 2 * e]), int(np.uint32(rec[5 + 2 * e]) >> 16),
-                 int((np.uint32(rec[5 + 2 * e]) >> 8) & 0xFF),
-                 int(np.uint32(rec[5 + 2 * e]) & 0xFF)) for e in range(n)]
+        sources = [int(x) for x in rec[4:HEADER]]
+        ents = []
+        for e in range(n):
+            x = rec[HEADER + ENTRY * e: HEADER + ENTRY * (e + 1)]
+            word = np.uint32(x[1])
+            flagged = bool(word >> 31)
+            ent = (int(x[0]), int((word >> 16) & 0x7FFF), int((word >> 8) & 0xFF),
+                   int(word & 0xFF))
+            if copies:
+                ent += (sources[int(word & 0xFF).bit_length() - 1] if flagged else -1,)
+            else:
+                assert not flagged
+            ents.append(ent)
+        if not copies:
+            assert sources == [-1] * 8
         out.append((int(rec[0]), int(rec[1]), int(rec[3]), ents))
     return int(w[0]), out
 
@@ -116,7 +136,7 @@ def test_plan_matches_its_definition(seed):
                                   num_slots=slots, num_blocks=nb)
     used, got = decoded(plan)
     assert used == groups and plan.slots == slots and plan.max_blocks == width
-    assert plan.stride % 4 == 0 and plan.stride >= 4 + 2 * 8 * width
+    assert plan.stride % 4 == 0 and plan.stride >= HEADER + ENTRY * 8 * width
     want = restated(table[:, :width], lens, starts, order if use_order else None, slots, width,
                     nb)
     assert got == want
@@ -163,10 +183,90 @@ def test_plan_refusals():
     # a stride too small for a group's distinct blocks (the library's own check)
     from vflorence_amd._lib import lib
 
-    words = torch.zeros(4 + 8, dtype=torch.int32)
+    words = torch.zeros(4 + HEADER + 4, dtype=torch.int32)  # room for two entries
     t2 = torch.arange(8, dtype=torch.int32).reshape(4, 2)
     starts = torch.tensor([0, 4], dtype=torch.int32)
     rc = lib.vfl_build_group_plan(t2.data_ptr(), 2, 2, lens.data_ptr(), 4, starts.data_ptr(),
-                                  None, 1, BS, 1 << 30, words.data_ptr(), 1, 8)
+                                  None, 1, BS, 1 << 30, words.data_ptr(), 1, HEADER + 4)
     assert rc != 0
     assert b"more distinct blocks" in lib.vfl_last_error()
+
+
+def beam_step_plan(step, beams=4, requests=5):
+    """A beam-search step's tables, lengths and copy pairs (BlockManager forks) and its
+    group plan, one group per request."""
+    from vflorence_amd.workloads import beam_decode_schedule
+
+    p = beam_decode_schedule(num_requests=requests, beams=beams, steps=step + 1,
+                             cow_fraction=0.3, seed=beams + step)[step]
+    n = len(p.context_lens)
+    width = max(len(t) for t in p.block_tables)
+    table = torch.zeros(n, width, dtype=torch.int32)
+    for i, t in enumerate(p.block_tables):
+        table[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    nb = 1 + int(table.max())
+    starts = torch.arange(0, n + 1, beams, dtype=torch.int32)
+    plan = hip().build_group_plan(table, torch.tensor(p.context_lens, dtype=torch.int32),
+                                  starts, num_blocks=nb)
+    return p, table, nb, plan
+
+
+@pytest.mark.parametrize("step", [17, 30, 45])
+def test_fold_marks_each_copy_destination_with_its_source(step):
+    p, table, nb, plan = beam_step_plan(step)
+    assert p.copies, "the schedule forks at this step"
+    before = decoded(plan)
+    src = [a for a, _ in p.copies]
+    dst = [b for _, b in p.copies]
+    assert hip().fold_plan_copies(plan, src, dst, num_blocks=nb)
+    used, slots = decoded(plan, copies=True)
+    want = dict(zip(dst, src))
+    found = {}
+    for (r0, n, widest, ents), (_, _, _, plain) in zip(slots, before[1]):
+        assert [e[:4] for e in ents] == plain  # nothing else changed
+        for (i, pos, toks, cols, source) in ents:
+            if i in want:
+                assert source == want[i] and cols & (cols - 1) == 0  # one row's block
+                # the fork's block is at its row's last position
+                r = r0 + cols.bit_length() - 1
+                assert pos == (p.context_lens[r] - 1) // BS
+                found[i] = source
+            else:
+                assert source == -1
+    assert found == want
+
+
+def test_fold_refusals_leave_the_plan_unchanged():
+    p, table, nb, plan = beam_step_plan(30)
+    src = [a for a, _ in p.copies]
+    dst = [b for _, b in p.copies]
+    from vflorence_amd._lib import lib
+
+    words = plan.words.clone()
+    # a block several rows of a group read at one position (a shared prefix block)
+    shared = next(i for (_, _, _, ents) in decoded(plan)[1] for (i, _, _, cols) in ents
+                  if cols & (cols - 1))
+    absent = nb + 5
+    cases = [
+        (src + [src[0]], dst + [absent], nb + 10, b"not a block of the plan"),
+        (src + [src[0]], dst + [dst[0]], nb, b"destination of two copies"),
+        (src + [dst[0]], dst + [absent], nb + 10, b"both a copy source and a destination"),
+        (src, dst[:-1] + [nb], nb, b"out of range"),
+        (src + [src[0]], dst + [shared], nb, b"listed by several rows"),
+    ]
+    for s, d, n, why in cases:
+        assert not hip().fold_plan_copies(plan, s, d, num_blocks=n), (s, d)
+        assert why in lib.vfl_last_error()
+        assert torch.equal(plan.words, words)
+    assert hip().fold_plan_copies(plan, [], [], num_blocks=nb)
+    assert torch.equal(plan.words, words)
+    # one row, two private blocks: only one of them can be its fork block
+    one = hip().build_group_plan(torch.tensor([[5, 6]], dtype=torch.int32),
+                                 torch.tensor([20], dtype=torch.int32),
+                                 torch.tensor([0, 1], dtype=torch.int32), num_blocks=10)
+    before = one.words.clone()
+    assert not hip().fold_plan_copies(one, [1, 2], [5, 6], num_blocks=10)
+    assert b"a row has two copy destinations" in lib.vfl_last_error()
+    assert torch.equal(one.words, before)
+    assert hip().fold_plan_copies(one, [2], [6], num_blocks=10)
+    assert decoded(one, copies=True)[1][0][3] == [(5, 0, 16, 1, -1), (6, 1, 4, 1, 2)]

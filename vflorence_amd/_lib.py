@@ -27,6 +27,7 @@ EXPORTED_SYMBOLS = (
     "vfl_get_scheduler_metadata",
     "vfl_group_plan_stride",
     "vfl_build_group_plan",
+    "vfl_fold_plan_copies",
     "vfl_attention_with_kv_cache",
     "vfl_self_attention_with_kv_write",
     "vfl_copy_blocks",
@@ -76,6 +77,7 @@ _SIGNATURES = {
         [_i64, _i64, _i32, _i32, _i32, _i64, _i32, _i32, _i32, _i32, ctypes.POINTER(SchedMeta)],
     ),
     "vfl_group_plan_stride": (_i64, [_i32, _i64]),
+    "vfl_fold_plan_copies": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64]),
     "vfl_build_group_plan": (
         ctypes.c_int,
         [_vp, _i64, _i32, _vp, _i64, _vp, _vp, _i64, _i32, _i64, _vp, _i64, _i64],

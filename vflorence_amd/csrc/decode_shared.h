@@ -127,16 +127,18 @@ __device__ __forceinline__ void mfma_consume_cols(const uint4 (&qop)[D / 32], Mf
 // holding it, and its V values patched into the whole 8-byte words of its 4-token group,
 // so 16 lanes cover one full 128-byte line (no partial-line read-modify-write).  The
 // other three tokens' bytes go back unchanged; no other workgroup touches this head's
-// slice of a private block.
-template <int D>
+// slice of a private block.  With STORE false only the registers are patched (the
+// caller stores the whole block).
+template <int D, bool STORE = true>
 __device__ __forceinline__ void store_new_token(const uint16_t *kc, const uint16_t *vc, int id,
                                                 int64_t block_elems, int head_off, int k_lane,
                                                 int v_lane, int col, int rg, int t_new,
                                                 const uint32_t (&newv)[D / 16],
                                                 MfmaBlock<D> &blk) {
+  constexpr bool store = STORE;
   uint16_t *tile_k = const_cast<uint16_t *>(kc) + (int64_t)id * block_elems + head_off;
   uint16_t *tile_v = const_cast<uint16_t *>(vc) + (int64_t)id * block_elems + head_off;
-  if (col == t_new) {
+  if (store && col == t_new) {
 #pragma unroll
     for (int kk = 0; kk < D / 32; ++kk)
       *reinterpret_cast<uint4 *>(tile_k + k_lane + 32 * kk) = blk.k[kk];
@@ -151,9 +153,25 @@ __device__ __forceinline__ void store_new_token(const uint16_t *kc, const uint16
       const uint32_t y = (blk.v[c].y & keep) | (newv[c] << sh);
       blk.v[c].x = upper ? blk.v[c].x : x;
       blk.v[c].y = upper ? y : blk.v[c].y;
-      *reinterpret_cast<uint2 *>(tile_v + v_lane + 64 * c) = blk.v[c];
+      if (store) *reinterpret_cast<uint2 *>(tile_v + v_lane + 64 * c) = blk.v[c];
     }
   }
+}
+
+// Store a whole loaded block (this head's slice: every lane's K row chunks and V
+// 4-token words) to block `id`: 16 tokens x D of K and of V, in the pools' layouts.
+template <int D>
+__device__ __forceinline__ void store_block(const uint16_t *kc, const uint16_t *vc, int id,
+                                            int64_t block_elems, int head_off, int k_lane,
+                                            int v_lane, const MfmaBlock<D> &blk) {
+  uint16_t *tile_k = const_cast<uint16_t *>(kc) + (int64_t)id * block_elems + head_off;
+  uint16_t *tile_v = const_cast<uint16_t *>(vc) + (int64_t)id * block_elems + head_off;
+#pragma unroll
+  for (int kk = 0; kk < D / 32; ++kk)
+    *reinterpret_cast<uint4 *>(tile_k + k_lane + 32 * kk) = blk.k[kk];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c)
+    *reinterpret_cast<uint2 *>(tile_v + v_lane + 64 * c) = blk.v[c];
 }
 
 // 16 bytes of a new-token row (K or V of one head), 16-byte aligned when `vec`.

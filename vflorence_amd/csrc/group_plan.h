@@ -7,9 +7,15 @@
 //   [1 .. 3]       zero
 //   slot s at PLAN_PREFIX + s * stride:
 //     [0] first row   [1] rows   [2] entries   [3] blocks of the group's longest row
+//     [4 + c]  copy source of row first + c (c < 8): -1, or the block this step's
+//              copy-on-write copies into that row's fork block (fold_plan_copies)
 //     entry e at PLAN_HEADER + PLAN_ENTRY * e:
 //       [0] block id
-//       [1] position << 16 | tokens << 8 | row mask (bit c: row first + c)
+//       [1] copy << 31 | position << 16 | tokens << 8 | row mask (bit c: row first + c)
+//           copy: the entry is its one row's fork block, to be filled from the row's
+//           copy source.  The fused launch then reads the source, writes the whole
+//           block to [0] with the row's new token in it, and the step needs no separate
+//           copy launch; the plain launch reads [0] as for any entry.
 // A slot's entries list, position by position, the distinct block ids the group's
 // rows hold there (ids outside [0, num_blocks) left out), each once, with the rows
 // that list it, in order of each id's first row: the blocks the shared kernel finds
@@ -21,13 +27,17 @@
 
 #include <stdint.h>
 
+#include <algorithm>
+#include <vector>
+
 namespace vfl {
 
 constexpr int PLAN_PREFIX = 4;
-constexpr int PLAN_HEADER = 4;
-constexpr int PLAN_ENTRY = 2;
 constexpr int PLAN_MAX_ROWS = 8;        // rows per group
-constexpr int PLAN_MAX_POSITION = 65535;
+constexpr int PLAN_HEADER = 4 + PLAN_MAX_ROWS;
+constexpr int PLAN_ENTRY = 2;
+constexpr int PLAN_MAX_POSITION = 32767;
+constexpr uint32_t PLAN_COPY = 1u << 31;
 
 // Words of one slot for groups of up to max_group rows and tables max_blocks wide:
 // room for every row holding a distinct block at every position, rounded up to 16
@@ -70,6 +80,7 @@ inline int build_group_plan(const int32_t *block_table, int64_t bt_stride, int m
   for (int64_t s = 0; s < num_slots; ++s) {
     int32_t *rec = plan + PLAN_PREFIX + s * stride;
     rec[0] = rec[1] = rec[2] = rec[3] = 0;
+    for (int c = 0; c < PLAN_MAX_ROWS; ++c) rec[4 + c] = -1;
     if (s >= num_groups) continue;
     const int64_t g = order ? order[s] : s;
     if (g < 0 || g >= num_groups) {
@@ -128,6 +139,105 @@ inline int build_group_plan(const int32_t *block_table, int64_t bt_stride, int m
     rec[3] = widest;
   }
   return 0;
+}
+
+// Fold a step's copy-on-write pairs (src[i] -> dst[i]) into its plan (the used slots
+// of build_group_plan's output): the entry holding block dst[i] gets the copy flag and
+// its row gets src[i] as copy source.  Each destination must be a block in
+// [0, num_blocks) that exactly one entry of the plan holds, for one row (the fresh
+// block a fork writes into), one per row; sources in [0, num_blocks); no block both a
+// destination and a source, no destination twice.  All pairs are checked before the
+// plan changes: on -1 (with *why set) the plan is as it was and the caller copies the
+// pairs itself.
+inline int fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
+                            const int64_t *src, const int64_t *dst, int64_t num_pairs,
+                            int64_t num_blocks, const char **why) {
+  *why = nullptr;
+  if (num_pairs < 0 || num_slots < 0 || stride < PLAN_HEADER || stride % 4 != 0 ||
+      (num_pairs > 0 && (!src || !dst))) {
+    *why = "bad sizes or null pairs";
+    return -1;
+  }
+  if (num_pairs == 0) return 0;
+  const int64_t used = plan[0];
+  if (used < 0 || used > num_slots) {
+    *why = "plan slot count out of range";
+    return -1;
+  }
+  // destinations sorted with their pair index, for a binary search per entry
+  std::vector<int64_t> order(num_pairs);
+  std::vector<int32_t *> where(num_pairs, nullptr);  // the destination's entry
+  std::vector<int32_t *> row_src(num_pairs, nullptr);  // its row's copy-source word
+  for (int64_t i = 0; i < num_pairs; ++i) order[i] = i;
+  std::sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return dst[a] < dst[b]; });
+  int rc = 0;
+  for (int64_t i = 0; i < num_pairs && rc == 0; ++i) {
+    const int64_t s = src[order[i]], d = dst[order[i]];
+    if (s < 0 || s >= num_blocks || d < 0 || d >= num_blocks) {
+      *why = "copy pair block out of range";
+      rc = -1;
+    } else if (i > 0 && dst[order[i - 1]] == d) {
+      *why = "a block is the destination of two copies";
+      rc = -1;
+    }
+  }
+  for (int64_t i = 0; i < num_pairs && rc == 0; ++i) {  // no source is also a destination
+    int64_t lo = 0, hi = num_pairs;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) / 2;
+      if (dst[order[mid]] < src[i]) lo = mid + 1; else hi = mid;
+    }
+    if (lo < num_pairs && dst[order[lo]] == src[i]) {
+      *why = "a block is both a copy source and a destination";
+      rc = -1;
+    }
+  }
+  for (int64_t s = 0; s < used && rc == 0; ++s) {
+    int32_t *rec = plan + PLAN_PREFIX + s * stride;
+    const int64_t ne = rec[2];
+    if (ne < 0 || PLAN_HEADER + ne * PLAN_ENTRY > stride) {
+      *why = "plan slot entry count out of range";
+      rc = -1;
+      break;
+    }
+    uint32_t taken = 0;  // rows of the slot that received a copy source
+    for (int64_t e = 0; e < ne; ++e) {
+      int32_t *ent = rec + PLAN_HEADER + PLAN_ENTRY * e;
+      int64_t lo = 0, hi = num_pairs;
+      while (lo < hi) {
+        const int64_t mid = (lo + hi) / 2;
+        if (dst[order[mid]] < ent[0]) lo = mid + 1; else hi = mid;
+      }
+      if (lo == num_pairs || dst[order[lo]] != ent[0]) continue;
+      const uint32_t rows = (uint32_t)ent[1] & 0xffu;
+      if (where[order[lo]] != nullptr || rows == 0 || (rows & (rows - 1u)) != 0) {
+        *why = "a copy destination is listed by several rows or entries";
+        rc = -1;
+        break;
+      }
+      int c = 0;
+      while (!((rows >> c) & 1u)) ++c;
+      if ((taken >> c) & 1u) {
+        *why = "a row has two copy destinations";
+        rc = -1;
+        break;
+      }
+      taken |= 1u << c;
+      where[order[lo]] = ent;
+      row_src[order[lo]] = rec + 4 + c;
+    }
+  }
+  for (int64_t i = 0; i < num_pairs && rc == 0; ++i)
+    if (where[i] == nullptr) {
+      *why = "a copy destination is not a block of the plan";
+      rc = -1;
+    }
+  if (rc == 0)
+    for (int64_t i = 0; i < num_pairs; ++i) {
+      where[i][1] = (int32_t)((uint32_t)where[i][1] | PLAN_COPY);
+      *row_src[i] = (int32_t)src[i];
+    }
+  return rc;
 }
 
 }  // namespace vfl

@@ -219,6 +219,22 @@ extern "C" int vfl_build_group_plan(const int32_t *block_table, int64_t block_ta
   return VFL_OK;
 }
 
+extern "C" int vfl_fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
+                                    const int64_t *src, const int64_t *dst, int64_t num_pairs,
+                                    int64_t num_blocks) {
+  clear_error();
+  if (!plan) {
+    set_error("fold_plan_copies: plan is NULL");
+    return VFL_E_INVALID;
+  }
+  const char *why = nullptr;
+  if (fold_plan_copies(plan, num_slots, stride, src, dst, num_pairs, num_blocks, &why) != 0) {
+    set_error("fold_plan_copies: %s", why);
+    return VFL_E_INVALID;
+  }
+  return VFL_OK;
+}
+
 // Shared argument checks and launch of both attention entry points.
 static int attention_impl(const void *query, int64_t query_stride_token,
                           int64_t query_stride_head, const void *k_cache, const void *v_cache,

@@ -98,6 +98,15 @@ class _StepBuffers:
         self._plan_words = 4 + groups * self.plan_stride
         return groups
 
+    def fold_copies(self, num_pairs: int, num_blocks: int) -> bool:
+        """Fold the packed copy-on-write pairs into the plan just built (the fused
+        self-attention launches then copy the blocks); False when they cannot be."""
+        h = self.h
+        rc = lib.vfl_fold_plan_copies(h["plan"].data_ptr(), self.rows, self.plan_stride,
+                                      h["copy_src"].data_ptr(), h["copy_dst"].data_ptr(),
+                                      num_pairs, num_blocks)
+        return rc == 0
+
     def upload(self, grouped: bool = False) -> None:
         words = self.plan_offset + (self._plan_words if grouped else 0)
         self.dev[:words].copy_(self.host[:words], non_blocking=True)
@@ -186,6 +195,8 @@ class ModelRunner:
         self._buckets = row_buckets(config.max_num_seqs)
         self._self_metadata: dict[tuple[int, bool, int], hip_attn.SchedulerMetadata] = {}
         self._slots: dict[tuple[int, int], int] = {}
+        self._fold_copies = hip_attn.plan_copies_supported(self.dtype, self.head_dim,
+                                                           self.block_size)
         self._step_slots = 0
         self._no_pages = torch.zeros(0, dtype=torch.int32)
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
@@ -317,14 +328,21 @@ class ModelRunner:
         grouped = core.pack(padded, buf.width, hip_attn.MAX_GROUP_SIZE, h)
         beams = batch.sampling_params.num_beams if batch.sampling_params else 1
         slots = self._launch_slots(padded, beams)
+        folded = False
         if grouped:
             groups = buf.build_plan(padded, self.config.num_blocks, self.block_size)
             self_slots = slots if groups <= slots else padded
+            # the copy-on-write rides in the self-attention launches: each layer's
+            # launch copies the fork's block in its own pools (model_runner.py:284-286
+            # order: the copy lands before the KV write, in the same launch)
+            if num_pairs and self._fold_copies:
+                folded = buf.fold_copies(num_pairs, self.config.num_blocks)
         else:
             self_slots = padded
         buf.upload(grouped)
         d = buf.d
-        if num_pairs:  # copy-on-write first: this step writes into the now-private blocks
+        if num_pairs and not folded:  # copy-on-write first: this step writes into the
+            # now-private blocks
             src, dst = h["copy_src"][:num_pairs], h["copy_dst"][:num_pairs]
             staged = not set(src.tolist()).isdisjoint(dst.tolist())
             self._copier(d["copy_src"][:num_pairs], d["copy_dst"][:num_pairs], staged=staged)

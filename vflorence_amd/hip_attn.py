@@ -233,6 +233,34 @@ def build_group_plan(block_table: torch.Tensor, seq_lens: torch.Tensor,
     return GroupPlan(out[:words], stride, slots, width)
 
 
+def fold_plan_copies(plan: GroupPlan, src, dst, *, num_blocks: int) -> bool:
+    """Fold a step's copy-on-write pairs ``src[i] -> dst[i]`` (host int64 sequences)
+    into a host group plan (``vfl_fold_plan_copies``): the fused self-attention launch
+    reading it then copies each pair's block for its layer's pools and the step needs no
+    ``copy_blocks``.  Returns False, leaving the plan unchanged, when the pairs cannot
+    be folded (a destination that is not one row's private block of the plan, say);
+    the caller then copies them itself."""
+    import numpy as np
+
+    if plan.words.device.type != "cpu":
+        raise ValueError("fold_plan_copies works on the host copy of a plan")
+    s = np.ascontiguousarray(src, dtype=np.int64)
+    d = np.ascontiguousarray(dst, dtype=np.int64)
+    if s.shape != d.shape or s.ndim != 1:
+        raise ValueError("src and dst must be 1-D sequences of one length")
+    rc = lib.vfl_fold_plan_copies(plan.words.data_ptr(), plan.slots, plan.stride,
+                                  s.ctypes.data, d.ctypes.data, s.size, int(num_blocks))
+    return rc == _lib.VFL_OK
+
+
+def plan_copies_supported(dtype: torch.dtype, head_dim: int, block_size: int) -> bool:
+    """Whether the fused self-attention launch acts on a plan's copy sources for pools of
+    this dtype, head size and block size (the matrix-core group kernel: 16-bit caches,
+    head size 64 or 128, 16-token blocks); elsewhere the pairs are copied by
+    ``copy_blocks``."""
+    return dtype in (torch.bfloat16, torch.float16) and head_dim in (64, 128) and block_size == 16
+
+
 @dataclass(eq=False)
 class SchedulerMetadata:
     """Launch plan for ``attention_with_kv_cache``: the GPU stand-in for the opaque
