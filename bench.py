@@ -4,10 +4,11 @@
 Workload (the metric's configuration): BART-large decoder shapes (12 layers, 16 heads
 x 64, block size 16), bf16, 64 requests x 4 beams = 256 rows, encoder lengths
 U[256, 1024], a 128-step beam search whose forks make copy-on-write pairs every step.
-A step is one decode step of the attention path: the batched CoW block copy, then per
-layer the KV slot write + paged self-attention and the beam-grouped paged
-cross-attention, through the vflorence::self_attention / vflorence::cross_attention
-custom ops.  Self-attention takes each request's beams as one row group that reads the
+A step is one decode step of the attention path: per layer the copy-on-write of the
+step's fork blocks, the KV slot write and the paged self-attention (one launch: the
+copy pairs ride in the step's group plan; ``--separate-copy``: one batched block-copy
+launch opens the step instead), then the beam-grouped paged cross-attention, through
+the vflorence::self_attention / vflorence::cross_attention custom ops.  Self-attention takes each request's beams as one row group that reads the
 prefix blocks they share once; the step's algorithmic bytes count a shared block once
 (``--ungrouped-self``: one row per workgroup, every row's blocks counted).  Each step is captured as a HIP graph; all inputs and per-step metadata
 are resident in HBM before timing.  Q/K/V values are synthetic (random), not produced
@@ -16,8 +17,11 @@ by the decoder GEMMs.
 Printed (one JSON line): whole-step algorithmic HBM GB/s (``value``), the roofline of
 the dominant kernel (cross-attention, timed live with HIP events on its stream), the
 op-level figure for 256 ragged self-attention sequences (ctx U[1, 1024], 20k-block
-pool), the decoder's projections on vfl_linear against hipBLASLt (cold weights), the
-whole engine's decode step, and the CPU restatement (oracle/) timed on the host cores.
+pool), cross-attention over a fragmented encoder pool, the decoder's projections on
+vfl_linear against hipBLASLt (cold weights), the whole engine's decode step (BART-large
+4 beams; Florence-2-base shapes with 3 beams and 587 encoder tokens; continuous
+batching at Florence-2-large shapes up to 512 rows), and the CPU restatement (oracle/)
+timed on the host cores.
 """
 
 from __future__ import annotations
@@ -399,14 +403,34 @@ def raw_fused_launcher(torch, case, out, sm):
     return launch
 
 
-def cross_kernel_timing(torch, wl, reps: int):
+def fragmented_staging(torch, wl, seed: int):
+    """The workload's cross-attention staged over a churned encoder pool: each request's
+    pages drawn from a random permutation of the whole pool instead of one contiguous run.
+    In the reference, pages return to the free list in finish order
+    (vflorence/engine/model_runner.py:169-177,261-265), so after some traffic a request's
+    pages scatter over the pool like this."""
+    from vflorence_amd.layers import attention
+
+    g = torch.Generator().manual_seed(seed + 101)
+    perm = torch.randperm(wl["num_cross"], generator=g).to(torch.int32)
+    pages, at = [], 0
+    for E in wl["enc"]:
+        n = math.ceil(E / BLOCK)
+        mine = perm[at: at + n].clone()
+        at += n
+        pages += [mine] * BEAMS
+    return attention.stage_cross(wl["layers"], pages, wl["enc_rows"], BLOCK, "gfx950")
+
+
+def cross_kernel_timing(torch, wl, reps: int, staged=None):
     """Dominant kernel of the workload: beam-grouped cross-attention, over all 12 layers'
-    pools in rotation (12 x 168 MB, so the 256 MB last-level cache cannot serve it)."""
+    pools in rotation (12 x 168 MB, so the 256 MB last-level cache cannot serve it).
+    ``staged``: another staging of the same requests (a fragmented pool)."""
     from vflorence_amd import workloads
 
     launches = []
     for i, L in enumerate(wl["layers"]):
-        k, v, table, lens, sm = wl["staged"][i]
+        k, v, table, lens, sm = (staged or wl["staged"])[i]
         out = torch.empty_like(wl["qc"][i])
         launches.append(raw_attention_launcher(torch, wl["qc"][i], k, v, out, lens, table, sm))
     seq = []
@@ -513,7 +537,8 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_cross_attention_ba
 
 def counter_pass(torch, wl, reps: int):
     """What a byte-counter pass measures: the cross-attention launches over the 12 layers'
-    pools (``reps`` rounds); the last decode step's fused self-attention over the 12 layers,
+    pools (``reps`` rounds), then the same over a fragmented encoder pool; the last decode
+    step's fused self-attention over the 12 layers,
     with beam groups read from the step's group plan, with beam groups walking the block
     tables, and with one row per workgroup; then two plain copies of COPY_BYTES
     each (a device-to-device memcpy and an elementwise negation), whose counter readings
@@ -529,6 +554,18 @@ def counter_pass(torch, wl, reps: int):
     cross_waves = sm.plan(REQUESTS * BEAMS, table.shape[1]).waves_per_workgroup
     for _ in range(reps):
         for f in launches:
+            f()
+    torch.cuda.synchronize()
+    # the same launches over a fragmented encoder pool (pages from a random permutation)
+    frag = fragmented_staging(torch, wl, 0)
+    frag_launches = []
+    for i in range(NUM_LAYERS):
+        k2, v2, table2, lens2, sm2 = frag[i]
+        out2 = torch.empty_like(wl["qc"][i])
+        frag_launches.append(raw_attention_launcher(torch, wl["qc"][i], k2, v2, out2, lens2,
+                                                    table2, sm2))
+    for _ in range(reps):
+        for f in frag_launches:
             f()
     torch.cuda.synchronize()
     # the last decode step's self-attention with its KV write over the 12 layers: beam
@@ -581,6 +618,7 @@ def counter_pass(torch, wl, reps: int):
     c_bytes = workloads.cross_attention_bytes(wl["enc"], REQUESTS * BEAMS, NUM_HEADS, HEAD_DIM,
                                               2, BLOCK)
     print(json.dumps({"counter_pass": True, "cross_launches": NUM_LAYERS * (reps + 1),
+                      "then_fragmented_pool_cross_launches": NUM_LAYERS * (reps + 1),
                       "cross_grid_threads": REQUESTS * NUM_HEADS * 64 * cross_waves,
                       "cross_algorithmic_bytes": int(c_bytes),
                       "self_step": len(wl["plans"]) - 1,
@@ -786,6 +824,170 @@ def engine_decode(torch, seed: int):
         "request_tokens_per_s": round(REQUESTS * steps / el, 1),
         "first_two_steps_s": round(first, 3),
         "hip_graphs": True,
+    }
+
+
+FLORENCE_BASE = dict(vocab_size=51289, d_model=768, encoder_layers=6, decoder_layers=6,
+                     encoder_attention_heads=12, decoder_attention_heads=12,
+                     encoder_ffn_dim=3072, decoder_ffn_dim=3072, max_position_embeddings=1024,
+                     forced_eos_token_id=None, tie_word_embeddings=False)
+
+
+def engine_decode_florence_base(torch, seed: int, steps: int = 64):
+    """Florence-2-base-shaped text decoder (6+6 layers, d_model 768, 12 heads, vocab
+    51289, synthetic weights), bf16, 128 requests x 3 beams, each reading 587 encoder
+    tokens (577 visual + 10 prompt positions, stood in for by token ids), ``steps``
+    beam-search steps with EOS suppressed (every step runs 384 rows), HIP graphs.
+    Returns decoder tokens/s and the cross-attention kernel's duration and algorithmic
+    GB/s inside the engine's steps (torch.profiler device timestamps over 8 steps)."""
+    from torch.profiler import ProfilerActivity, profile
+    from transformers import BartConfig
+
+    from vflorence_amd import LLM, Request, SamplingParams, workloads
+
+    requests, beams, enc = 128, 3, 587
+    cfg = BartConfig(**FLORENCE_BASE)
+    llm = LLM(cfg, max_num_seqs=requests * beams, dtype=torch.bfloat16, max_decoder_len=256,
+              max_encoder_len=enc, cuda_graphs=True)
+    g = torch.Generator().manual_seed(seed + 202)
+    params = SamplingParams(max_tokens=steps, num_beams=beams, min_length=steps + 2,
+                            eos_token_id=[cfg.eos_token_id])
+    for _ in range(requests):
+        llm.add_request(Request(torch.randint(3, cfg.vocab_size, (enc,), generator=g).tolist()),
+                        params)
+    torch.cuda.synchronize()
+    gc.disable()
+    try:
+        llm.step()
+        llm.step()
+        torch.cuda.synchronize()
+        rows_done = n = 0
+        t0 = time.perf_counter()
+        while n < steps - 12:  # timed steps, leaving 8 for the kernel pass below
+            rows_done += llm.scheduler.num_running
+            llm.step()
+            n += 1
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            for _ in range(8):
+                llm.step()
+            torch.cuda.synchronize()
+        while not llm.is_finished():
+            llm.step()
+    finally:
+        gc.enable()
+    cross = [e.device_time * 1e-6 for e in prof.events()
+             if e.device_type == torch.autograd.DeviceType.CUDA
+             and e.name.startswith("void vfl::paged_decode_mfma_kernel<1, 64,")
+             and ", false, 0>" in e.name]
+    nbytes = workloads.cross_attention_bytes([enc] * requests, requests * beams, 12, 64, 2, BLOCK)
+    del llm
+    torch.cuda.empty_cache()
+    out = {
+        "model": "Florence-2-base text decoder shapes (6 layers, d_model 768, 12 heads), "
+                 "synthetic weights, bf16",
+        "requests": requests, "beams": beams, "enc_len": enc,
+        "timed_steps": n,
+        "ms_per_step": round(el * 1e3 / n, 3),
+        "decoded_rows_per_s": round(rows_done / el, 1),
+        "request_tokens_per_s": round(requests * n / el, 1),
+        "hip_graphs": True,
+    }
+    if cross and sum(cross) > 0:
+        avg = sum(cross) / len(cross)
+        out["cross_attention"] = {
+            "launches": len(cross), "avg_us": round(avg * 1e6, 2),
+            "algorithmic_bytes": int(nbytes), "gbps": round(nbytes / avg / 1e9, 1),
+            "frac": round(nbytes / avg / 1e9 / HBM_PEAK_GBPS, 4)}
+    return out
+
+
+def engine_continuous_batching(torch, seed: int, n_req: int = 2000, rate: float = 6.0):
+    """Continuous batching at the stress shape: Florence-2-large text decoder (12+12
+    layers, d_model 1024, 16 heads, vocab 51289, synthetic weights), bf16, max_num_seqs
+    512; ``n_req`` requests arriving as a seeded Poisson process (``rate`` per step),
+    encoder lengths a 50/50 mix of 587 and U[64, 1024], greedy, output lengths geometric
+    with mean 96 capped at 256.  Active requests share one SamplingParams (the reference
+    requires it, vflorence/engine/llm_engine.py:147), so a request is retired at its
+    drawn length by cancelling it.  A first, shorter pass of the same process (untimed)
+    captures the row buckets' graphs; the second pass is timed end to end, encoders
+    included, with the time spent encoding admitted requests (each encode synchronised)
+    reported beside it."""
+    import numpy as np
+    from transformers import BartConfig
+
+    from vflorence_amd import LLM, Request, SamplingParams
+
+    cfg = BartConfig(vocab_size=51289, max_position_embeddings=1024, forced_eos_token_id=None,
+                     tie_word_embeddings=False)
+    llm = LLM(cfg, max_num_seqs=512, dtype=torch.bfloat16, max_decoder_len=256,
+              max_encoder_len=1024, cuda_graphs=True)
+    sp = SamplingParams(max_tokens=256, eos_token_id=[cfg.eos_token_id],
+                        suppress_tokens=[cfg.eos_token_id])
+
+    def one_pass(rng, count):
+        arrive = np.cumsum(rng.poisson(1.0 / rate, size=count)).tolist()
+        enc = np.where(rng.random(count) < 0.5, 587, rng.integers(64, 1025, size=count)).tolist()
+        out_len = np.minimum(rng.geometric(1 / 96, size=count), 256)
+        first = llm._next_request_id  # request ids run on from here, one per add
+        tokens = rows = steps = 0
+        pending = list(range(count))
+        while pending or not llm.is_finished():
+            while pending and arrive[pending[0]] <= steps:
+                i = pending.pop(0)
+                ids = rng.integers(3, cfg.vocab_size, size=enc[i]).tolist()
+                llm.add_request(Request(ids), sp)
+            if not llm.is_finished():
+                llm.step()
+                # the step's rows as the runner packed them: request ids and token counts
+                # before the step (start token included) = generated counts after it
+                runner = llm.runner
+                n = runner.step_rows
+                rid = runner._buffers.np["row_requests"][:n].copy()
+                gen = runner._buffers.np["lengths"][:n].copy()
+                rows += n
+                tokens += n
+                for r in rid[gen >= out_len[rid - first]]:
+                    llm.abort_request(int(r))
+            steps += 1
+        return tokens, rows, steps
+
+    encode = llm.runner._encode
+    encode_s = [0.0]
+
+    def timed_encode(seqs):
+        t = time.perf_counter()
+        encode(seqs)
+        torch.cuda.synchronize()
+        encode_s[0] += time.perf_counter() - t
+
+    gc.disable()
+    try:
+        one_pass(np.random.default_rng(seed + 303), 400)
+        torch.cuda.synchronize()
+        llm.runner._encode = timed_encode
+        t0 = time.perf_counter()
+        tokens, rows, steps = one_pass(np.random.default_rng(seed + 304), n_req)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+    finally:
+        gc.enable()
+        llm.runner._encode = encode
+    graphs = len(llm.runner._graphs)
+    del llm
+    torch.cuda.empty_cache()
+    return {
+        "model": "Florence-2-large text decoder shapes (12 layers, d_model 1024, 16 heads), "
+                 "synthetic weights, bf16, greedy",
+        "requests": n_req, "arrivals_per_step": rate, "max_num_seqs": 512,
+        "enc_len": "50/50 587 | U[64,1024]", "out_len": "geometric mean 96, cap 256",
+        "steps": steps, "mean_running_rows": round(rows / steps, 1),
+        "wall_s": round(el, 3),
+        "request_tokens_per_s": round(tokens / el, 1),
+        "encoder_s": round(encode_s[0], 3),
+        "decode_request_tokens_per_s": round(tokens / (el - encode_s[0]), 1),
+        "hip_graphs_captured": graphs,
     }
 
 
@@ -1033,6 +1235,10 @@ def main():
     print("[bench] timing the cross-attention kernel back to back", flush=True)
     c_avg, _ = cross_kernel_timing(torch, wl, args.kernel_reps)
     c_gbps = c_bytes / c_avg / 1e9
+    print("[bench] cross-attention over a fragmented encoder pool", flush=True)
+    f_avg, _ = cross_kernel_timing(torch, wl, args.kernel_reps,
+                                   staged=fragmented_staging(torch, wl, args.seed))
+    c_avg2, _ = cross_kernel_timing(torch, wl, args.kernel_reps)  # contiguous again, beside it
     print("[bench] copy-on-write at 115 pairs per step", flush=True)
     cow_avg, cow_bytes = cow_planned_volume_timing(torch, wl, args.kernel_reps, args.seed)
     if in_step is not None and sum(in_step["cross"]) / len(in_step["cross"]) < 0.5 * c_avg:
@@ -1067,10 +1273,16 @@ def main():
     torch.cuda.empty_cache()
     print("[bench] decoder projections: vfl_linear against hipBLASLt, cold weights", flush=True)
     linear = decoder_linear_timing(torch)
-    decoder = None
+    decoder = florence = batching = None
     if not args.no_engine:
         print("[bench] engine decode: BART-large bf16, 64 requests x 4 beams", flush=True)
         decoder = engine_decode(torch, args.seed)
+        print("[bench] engine decode: Florence-2-base shapes bf16, 128 requests x 3 beams",
+              flush=True)
+        florence = engine_decode_florence_base(torch, args.seed)
+        print("[bench] continuous batching: Florence-2-large shapes bf16, 512 rows max",
+              flush=True)
+        batching = engine_continuous_batching(torch, args.seed)
 
     rows = REQUESTS * BEAMS
     result = {
@@ -1088,6 +1300,11 @@ def main():
         "data": "synthetic (random Q/K/V, seeded beam-search block tables)",
         "config": {
             "workload": ("BART-large decoder attention path, 64 requests x 4 beams bf16, "
+                         "enc U[256,1024], 128-step beam search with CoW forks; one step = "
+                         "12 x (CoW of the layer's pools + KV write + paged self-attn, one "
+                         "launch; grouped cross-attn), HIP-graph replay"
+                         if folded else
+                         "BART-large decoder attention path, 64 requests x 4 beams bf16, "
                          "enc U[256,1024], 128-step beam search with CoW forks; one step = "
                          "CoW copy + 12 x (KV write + paged self-attn + grouped cross-attn), "
                          "HIP-graph replay"),
@@ -1139,6 +1356,13 @@ def main():
                 "back_to_back_gbps": round(c_gbps, 1),
                 "kernel_bytes": int(c_bytes),
             },
+            "cross_attention_64x4_fragmented_pool": {
+                "pages": "each request's pages from a random permutation of the pool",
+                "back_to_back_us": round(f_avg * 1e6, 2),
+                "back_to_back_frac": round(c_bytes / f_avg / 1e9 / HBM_PEAK_GBPS, 4),
+                "contiguous_back_to_back_us": round(c_avg2 * 1e6, 2),
+                "contiguous_back_to_back_frac": round(c_bytes / c_avg2 / 1e9 / HBM_PEAK_GBPS, 4),
+            },
             "self_attention_in_step_by_context": self_by_ctx,
             "copy_on_write_in_step": {
                 "folded_into_self_attention": folded,
@@ -1159,6 +1383,8 @@ def main():
             "decoder_linear_256_rows_cold_weights": linear,
         },
         "decoder_tokens": decoder,
+        "florence2_base_3beam": florence,
+        "continuous_batching_florence2_large": batching,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
