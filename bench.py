@@ -539,7 +539,8 @@ def counter_pass(torch, wl, reps: int):
     """What a byte-counter pass measures: the cross-attention launches over the 12 layers'
     pools (``reps`` rounds), then the same over a fragmented encoder pool; the last decode
     step's fused self-attention over the 12 layers,
-    with beam groups read from the step's group plan, with beam groups walking the block
+    with beam groups read from the step's group plan, the same with the step's
+    copy-on-write pairs folded into the plan, with beam groups walking the block
     tables, and with one row per workgroup; then two plain copies of COPY_BYTES
     each (a device-to-device memcpy and an elementwise negation), whose counter readings
     calibrate the counters against a known byte count."""
@@ -582,13 +583,21 @@ def counter_pass(torch, wl, reps: int):
     common = dict(num_reqs=rows, num_heads=NUM_HEADS, num_kv_heads=NUM_HEADS,
                   head_dim=HEAD_DIM, dtype=torch.bfloat16, block_size=BLOCK, fuse_kv_write=True)
     starts_h = torch.arange(0, rows + 1, BEAMS, dtype=torch.int32)
-    gplan = hip_attn.build_group_plan(
+    nblocks = wl["layers"][0].self_attn.k_cache.shape[0]
+    host_plan = hip_attn.build_group_plan(
         tables.cpu(), lens.cpu(), starts_h, max_group_size=BEAMS, block_size=BLOCK,
-        num_blocks=wl["layers"][0].self_attn.k_cache.shape[0]).to(dev)
+        num_blocks=nblocks)
+    gplan = host_plan.to(dev)
+    if not hip_attn.fold_plan_copies(host_plan, [a for a, _ in plan.copies],
+                                     [b for _, b in plan.copies], num_blocks=nblocks):
+        raise RuntimeError("the last step's copy pairs cannot be folded")
     plans = {
         "planned": hip_attn.get_scheduler_metadata(
             group_start=starts_h.to(dev), max_group_size=BEAMS, own_tables=True,
             group_plan=gplan, **common),
+        "planned_copies": hip_attn.get_scheduler_metadata(
+            group_start=starts_h.to(dev), max_group_size=BEAMS, own_tables=True,
+            group_plan=host_plan.to(dev), **common),
         "grouped": hip_attn.get_scheduler_metadata(
             group_start=starts_h.to(dev), max_group_size=BEAMS, own_tables=True, **common),
         "rows": hip_attn.get_scheduler_metadata(
@@ -605,7 +614,9 @@ def counter_pass(torch, wl, reps: int):
                 scale=HEAD_DIM**-0.5, block_table=tables, scheduler_metadata=sm)
         torch.cuda.synchronize()
     grouped_bytes = step_bytes(plan, wl["enc"], grouped=True)[1]
-    self_bytes = {"planned": grouped_bytes, "grouped": grouped_bytes,
+    self_bytes = {"planned": grouped_bytes,
+                  "planned_copies": grouped_bytes + cow_bytes(plan) // NUM_LAYERS,
+                  "grouped": grouped_bytes,
                   "rows": step_bytes(plan, wl["enc"], grouped=False)[1]}
     subjects = extra_counter_subjects(torch, wl)
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")

@@ -179,15 +179,16 @@ int vfl_build_group_plan(const int32_t *block_table, int64_t block_table_stride,
  * Host function (all pointers host memory; no device call).  Folds a decode step's
  * copy-on-write pairs into its group plan -- the batched block copy that replaces the
  * loop of vflorence/engine/model_runner.py:162-167, which the reference runs before the
- * step's KV writes (:284-286).  For each pair the plan entry holding block dst[i]
- * records src[i] as its copy source; vfl_self_attention_with_kv_write with that plan
- * then reads the source block instead of dst[i], stores it whole to dst[i] with the
- * row's new token in place (each layer's launch for its own pools), and the step needs
- * no vfl_copy_blocks launch.  Only the fused launch acts on copy sources (the plain
- * attention launch reads every entry's own block), and it relies on the fused write's
- * contract: dst[i] is the block of a row's last context position, which no other row
- * reads.  plan: the used slots of vfl_build_group_plan's output (num_slots and stride
- * as given to it).  Refused (VFL_E_INVALID, plan unchanged) when a block is out of
+ * step's KV writes (:284-286).  For each pair the plan entry holding block dst[i] gets
+ * a copy flag and src[i] in place of dst[i]; vfl_self_attention_with_kv_write with that
+ * plan then reads the source block, stores it whole with the row's new token in place
+ * to the block of the row's slot -- dst[i], by the fused write's contract (a row's slot
+ * is at its last context position, in a block no other row reads) -- in each layer's
+ * launch for its own pools, and the step needs no vfl_copy_blocks launch.  Only the
+ * fused launch may read a folded plan (the plain attention launch would read the
+ * sources as the rows' blocks).  plan: the used slots of vfl_build_group_plan's output
+ * (num_slots and stride as given to it).  Refused (VFL_E_INVALID, plan unchanged) when
+ * a block is out of
  * [0, num_blocks), a destination repeats or is also a source, or a destination is not
  * exactly one single-row entry of the plan; the caller then copies the pairs itself.
  */

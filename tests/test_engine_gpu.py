@@ -509,9 +509,9 @@ def test_beam_step_uploads_the_group_plan_of_its_tables(dtype):
             a = got[4 + s * want.stride:]
             b = want.words[4 + s * want.stride:]
             n = int(b[2])
-            assert torch.equal(a[:12 + 2 * n], b[:12 + 2 * n]), s  # header, sources, entries
-            shared += sum(bin(int(b[13 + 2 * e]) & 0xFF).count("1") > 1 for e in range(n))
-            copies += sum(int(b[13 + 2 * e]) < 0 for e in range(n))  # flagged fork blocks
+            assert torch.equal(a[:4 + 2 * n], b[:4 + 2 * n]), s  # header, entries
+            shared += sum(bin(int(b[5 + 2 * e]) & 0xFF).count("1") > 1 for e in range(n))
+            copies += sum(int(b[5 + 2 * e]) < 0 for e in range(n))  # flagged fork blocks
         assert shared > 0  # beams share prefix blocks
         assert copies == pairs  # every pair rides in the plan
         set_context()

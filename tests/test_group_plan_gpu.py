@@ -323,34 +323,24 @@ def test_fused_launch_with_folded_copies_equals_copy_then_fused_launch(beams, he
             assert not np.array_equal(bits(kc[b]), bits(k1[b]))
 
 
-def test_plain_launch_reads_entries_own_blocks_whatever_their_copy_source():
-    """Only the fused launch acts on copy sources: attention_with_kv_cache with a folded
-    plan reads every entry's own block (bit-identical to the unfolded plan) and writes
-    no cache."""
+def test_plain_launch_refuses_a_plan_with_copies_folded_in():
+    """A folded plan names each fork block's copy source in its place, which only the
+    fused launch acts on: the plain attention launch refuses it."""
     hip_attn = hip()
     H, D = 16, 64
     p, table, NB, starts = beam_step(4, 33, seed=5)
     N = len(p.context_lens)
-    g = torch.Generator().manual_seed(3)
-    kc = torch.randn(NB, H, BS, D, generator=g).to(torch.bfloat16)
-    vc = torch.randn(NB, H, BS, D, generator=g).to(torch.bfloat16)
-    q = torch.randn(N, H, D, generator=g).to(torch.bfloat16).to(DEV)
     L = torch.tensor(p.context_lens, dtype=torch.int32)
-    outs = []
-    for fold in (False, True):
-        kd, vd = kc.to(DEV), vc.to(DEV)
-        plan = hip_attn.build_group_plan(table, L, starts, block_size=BS, num_blocks=NB)
-        if fold:
-            assert hip_attn.fold_plan_copies(plan, [a for a, _ in p.copies],
-                                             [b for _, b in p.copies], num_blocks=NB)
-        sm = planned_metadata(N, H, D, q.dtype, starts, plan.to(DEV), 2, False)
-        out = torch.empty_like(q)
-        hip_attn.attention_with_kv_cache(q, kd, vd, out, None, L.to(DEV), scale=D**-0.5,
-                                         block_table=table.to(DEV), scheduler_metadata=sm)
-        torch.cuda.synchronize()
-        assert np.array_equal(bits(kd.cpu()), bits(kc)) and np.array_equal(bits(vd.cpu()), bits(vc))
-        outs.append(out.cpu())
-    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    plan = hip_attn.build_group_plan(table, L, starts, block_size=BS, num_blocks=NB)
+    assert hip_attn.fold_plan_copies(plan, [a for a, _ in p.copies], [b for _, b in p.copies],
+                                     num_blocks=NB)
+    sm = planned_metadata(N, H, D, torch.bfloat16, starts, plan.to(DEV), 2, False)
+    q = torch.zeros(N, H, D, dtype=torch.bfloat16, device=DEV)
+    kv = torch.zeros(NB, H, BS, D, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="only self_attention_with_kv_write"):
+        hip_attn.attention_with_kv_cache(q, kv, kv, torch.empty_like(q), None, L.to(DEV),
+                                         scale=D**-0.5, block_table=table.to(DEV),
+                                         scheduler_metadata=sm)
 
 
 def test_plan_for_another_table_width_is_refused():

@@ -56,19 +56,18 @@ def restated(table, lens, starts, order, slots, width, num_blocks):
     return out
 
 
-HEADER, ENTRY = 12, 2  # words of a slot's header (4 + 8 rows' copy sources), of an entry
+HEADER, ENTRY = 4, 2  # words of a slot's header, of an entry
 
 
 def decoded(plan, copies=False):
     """(used slots, [(first row, rows, widest, entries)]); an entry is (id, position,
-    tokens, rows) -- with ``copies``, plus the copy source of a flagged entry's row or
-    -1.  Without ``copies`` no entry may be flagged nor any row have a source."""
+    tokens, rows) -- with ``copies``, plus whether it is flagged as a fork block whose id
+    is its copy source.  Without ``copies`` no entry may be flagged."""
     w = plan.words.numpy()
     out = []
     for s in range(plan.slots):
         rec = w[4 + s * plan.stride:]
         n = int(rec[2])
-        sources = [int(x) for x in rec[4:HEADER]]
         ents = []
         for e in range(n):
             x = rec[HEADER + ENTRY * e: HEADER + ENTRY * (e + 1)]
@@ -77,12 +76,10 @@ def decoded(plan, copies=False):
             ent = (int(x[0]), int((word >> 16) & 0x7FFF), int((word >> 8) & 0xFF),
                    int(word & 0xFF))
             if copies:
-                ent += (sources[int(word & 0xFF).bit_length() - 1] if flagged else -1,)
+                ent += (flagged,)
             else:
                 assert not flagged
             ents.append(ent)
-        if not copies:
-            assert sources == [-1] * 8
         out.append((int(rec[0]), int(rec[1]), int(rec[3]), ents))
     return int(w[0]), out
 
@@ -223,16 +220,17 @@ def test_fold_marks_each_copy_destination_with_its_source(step):
     want = dict(zip(dst, src))
     found = {}
     for (r0, n, widest, ents), (_, _, _, plain) in zip(slots, before[1]):
-        assert [e[:4] for e in ents] == plain  # nothing else changed
-        for (i, pos, toks, cols, source) in ents:
-            if i in want:
-                assert source == want[i] and cols & (cols - 1) == 0  # one row's block
-                # the fork's block is at its row's last position
+        for (i, pos, toks, cols, flagged), (i0, pos0, toks0, cols0) in zip(ents, plain):
+            assert (pos, toks, cols) == (pos0, toks0, cols0)  # only ids and flags change
+            if i0 in want:
+                # the fork's block (one row's, at its last position) names its source
+                assert flagged and i == want[i0] and cols & (cols - 1) == 0
                 r = r0 + cols.bit_length() - 1
                 assert pos == (p.context_lens[r] - 1) // BS
-                found[i] = source
+                assert table[r, pos] == i0
+                found[i0] = i
             else:
-                assert source == -1
+                assert not flagged and i == i0
     assert found == want
 
 
@@ -269,4 +267,4 @@ def test_fold_refusals_leave_the_plan_unchanged():
     assert b"a row has two copy destinations" in lib.vfl_last_error()
     assert torch.equal(one.words, before)
     assert hip().fold_plan_copies(one, [2], [6], num_blocks=10)
-    assert decoded(one, copies=True)[1][0][3] == [(5, 0, 16, 1, -1), (6, 1, 4, 1, 2)]
+    assert decoded(one, copies=True)[1][0][3] == [(5, 0, 16, 1, False), (2, 1, 4, 1, True)]

@@ -100,8 +100,6 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
   const int cap = (int)min<int64_t>((plan_stride - PLAN_HEADER) / PLAN_ENTRY, 1 << 24);
   PlanEntries ents;
   ents.init(rec + PLAN_HEADER, max(0, min(hdr.z, cap)));
-  // copy source of row first + lane (lanes < 8), for fork blocks flagged in the entries
-  const int row_src = FUSE && lane < PLAN_MAX_ROWS ? rec[4 + lane] : -1;
   if (slot >= used) return;
   const int row0 = hdr.x;
   if (row0 < 0 || row0 >= num_rows || hdr.y <= 0) return;
@@ -152,8 +150,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
 
   // Wave w takes entries w, w + NW, w + 2 NW, ...; a stage is U of them.  The first
   // stage's block loads go out before anything waits for the level-2 loads above.
-  // A copy entry (fused launch only) reads its copy source, all of it, and the block
-  // goes to the entry's own id with the new token in it before it is consumed.
+  // A copy entry (fused launch only) names its copy source: all of it is read, and the
+  // block goes whole, with the row's new token in it, to the row's slot block before it
+  // is consumed.
   int e_id[U], e_pos[U];
   uint32_t e_cols[U];
   bool e_ok[U], e_copy[U];
@@ -167,7 +166,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
       e_cols[u] = 0;
       e_ok[u] = false;
       e_copy[u] = false;
-      int tokens = 0, from = 0;
+      int tokens = 0;
       if (e < n_e) {
         const int2 en = ents.get(e);
         e_pos[u] = (int)(((uint32_t)en.y >> 16) & 0x7fffu);
@@ -175,19 +174,14 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
         e_cols[u] = (uint32_t)en.y & 0xffu & row_bits;
         e_ok[u] = en.x >= 0 && en.x < num_blocks && e_pos[u] < max_blocks && e_cols[u] != 0;
         e_id[u] = e_ok[u] ? en.x : 0;
-        // selects, not branches: the stage's loads stay one straight run
-        const int source =
-            __builtin_amdgcn_readlane(row_src, __builtin_ctz(e_cols[u] | 0x100u) & 63);
-        e_copy[u] = FUSE && e_ok[u] && ((uint32_t)en.y & PLAN_COPY) && source >= 0 &&
-                    source < num_blocks;
-        from = e_copy[u] ? source : e_id[u];
+        e_copy[u] = FUSE && e_ok[u] && ((uint32_t)en.y & PLAN_COPY);
         tokens = e_copy[u] ? BS : tokens;
       }
       // Only the K rows and V 4-token groups of tokens some listing row attends to
       // (masked tokens are never read, so the rest may stay zero); a copy reads all.
       const bool k_ok = e_ok[u] && col < tokens;
       const bool v_ok = e_ok[u] && 4 * rg < tokens;
-      const int64_t base = (int64_t)from * block_elems + head_off;
+      const int64_t base = (int64_t)e_id[u] * block_elems + head_off;
 #pragma unroll
       for (int kk = 0; kk < D / 32; ++kk) {
         blk[u].k[kk] = make_uint4(0, 0, 0, 0);
@@ -202,6 +196,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
   };
   int e0 = wave;
   if (e0 < n_e) load_stage(e0);
+  // the block of the row's slot, where a copy entry's block goes (after the first
+  // stage's loads are out: it waits for the slot)
+  const int wblk = wslot >= 0 ? (int)(wslot / BS) : 0;
 
   const int my_nblk = L > 0 ? min((L + BS - 1) / BS, max_blocks) : 0;
   const int Lc = min(L, my_nblk * BS);
@@ -230,8 +227,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool mine = (e_cols[u] >> col) & 1u;
+        // a copy entry names the source: its row's new token goes to the slot's block
         sub[u] = column_mask(e_ok[u] && mine && last == e_pos[u] &&
-                             (int64_t)e_id[u] * BS + t_new == wslot);
+                             (e_copy[u] ? wslot >= 0 : (int64_t)e_id[u] * BS + t_new == wslot));
         written |= sub[u];
       }
     }
@@ -253,17 +251,19 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_planned_kernel(
             uint32_t newv[VCH];
 #pragma unroll
             for (int cc = 0; cc < VCH; ++cc) newv[cc] = s_new[wave][c][1][16 * cc + col];
-            if (e_copy[u])
-              store_new_token<D, false>(kc, vc, e_id[u], block_elems, head_off, k_lane, v_lane,
+            if (e_copy[u]) {
+              // The copy-on-write of a fork's block, folded in: the source's tokens with
+              // the row's new token, stored whole to the row's slot block before the
+              // consume masks V past the context.
+              store_new_token<D, false>(kc, vc, 0, block_elems, head_off, k_lane, v_lane,
                                         col, rg, tn, newv, blk[u]);
-            else
+              store_block<D>(kc, vc, __builtin_amdgcn_readlane(wblk, c), block_elems, head_off,
+                             k_lane, v_lane, blk[u]);
+            } else {
               store_new_token<D>(kc, vc, e_id[u], block_elems, head_off, k_lane, v_lane, col,
                                  rg, tn, newv, blk[u]);
+            }
           }
-          // The copy-on-write of a fork's block, folded in: the source's tokens with the
-          // row's new token, stored whole before the consume masks V past the context.
-          if (e_copy[u])
-            store_block<D>(kc, vc, e_id[u], block_elems, head_off, k_lane, v_lane, blk[u]);
         }
         const bool mine = (e_cols[u] >> col) & 1u;
         const int ext = row_max16(mine ? Lc : 0);

@@ -7,15 +7,15 @@
 //   [1 .. 3]       zero
 //   slot s at PLAN_PREFIX + s * stride:
 //     [0] first row   [1] rows   [2] entries   [3] blocks of the group's longest row
-//     [4 + c]  copy source of row first + c (c < 8): -1, or the block this step's
-//              copy-on-write copies into that row's fork block (fold_plan_copies)
 //     entry e at PLAN_HEADER + PLAN_ENTRY * e:
 //       [0] block id
 //       [1] copy << 31 | position << 16 | tokens << 8 | row mask (bit c: row first + c)
-//           copy: the entry is its one row's fork block, to be filled from the row's
-//           copy source.  The fused launch then reads the source, writes the whole
-//           block to [0] with the row's new token in it, and the step needs no separate
-//           copy launch; the plain launch reads [0] as for any entry.
+//           copy (set by fold_plan_copies): the entry is its one row's fork block, and
+//           [0] holds the block copy-on-write fills it from.  The fused launch reads
+//           that source, writes the whole block with the row's new token in it to the
+//           row's slot block (its fork block, by the fused write's contract), and the
+//           step needs no separate copy launch.  Only the fused launch can read such a
+//           plan: the plain launch would read the source as the row's block.
 // A slot's entries list, position by position, the distinct block ids the group's
 // rows hold there (ids outside [0, num_blocks) left out), each once, with the rows
 // that list it, in order of each id's first row: the blocks the shared kernel finds
@@ -34,7 +34,7 @@ namespace vfl {
 
 constexpr int PLAN_PREFIX = 4;
 constexpr int PLAN_MAX_ROWS = 8;        // rows per group
-constexpr int PLAN_HEADER = 4 + PLAN_MAX_ROWS;
+constexpr int PLAN_HEADER = 4;
 constexpr int PLAN_ENTRY = 2;
 constexpr int PLAN_MAX_POSITION = 32767;
 constexpr uint32_t PLAN_COPY = 1u << 31;
@@ -80,7 +80,6 @@ inline int build_group_plan(const int32_t *block_table, int64_t bt_stride, int m
   for (int64_t s = 0; s < num_slots; ++s) {
     int32_t *rec = plan + PLAN_PREFIX + s * stride;
     rec[0] = rec[1] = rec[2] = rec[3] = 0;
-    for (int c = 0; c < PLAN_MAX_ROWS; ++c) rec[4 + c] = -1;
     if (s >= num_groups) continue;
     const int64_t g = order ? order[s] : s;
     if (g < 0 || g >= num_groups) {
@@ -143,7 +142,7 @@ inline int build_group_plan(const int32_t *block_table, int64_t bt_stride, int m
 
 // Fold a step's copy-on-write pairs (src[i] -> dst[i]) into its plan (the used slots
 // of build_group_plan's output): the entry holding block dst[i] gets the copy flag and
-// its row gets src[i] as copy source.  Each destination must be a block in
+// src[i] in place of dst[i].  Each destination must be a block in
 // [0, num_blocks) that exactly one entry of the plan holds, for one row (the fresh
 // block a fork writes into), one per row; sources in [0, num_blocks); no block both a
 // destination and a source, no destination twice.  All pairs are checked before the
@@ -167,7 +166,6 @@ inline int fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
   // destinations sorted with their pair index, for a binary search per entry
   std::vector<int64_t> order(num_pairs);
   std::vector<int32_t *> where(num_pairs, nullptr);  // the destination's entry
-  std::vector<int32_t *> row_src(num_pairs, nullptr);  // its row's copy-source word
   for (int64_t i = 0; i < num_pairs; ++i) order[i] = i;
   std::sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return dst[a] < dst[b]; });
   int rc = 0;
@@ -224,7 +222,6 @@ inline int fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
       }
       taken |= 1u << c;
       where[order[lo]] = ent;
-      row_src[order[lo]] = rec + 4 + c;
     }
   }
   for (int64_t i = 0; i < num_pairs && rc == 0; ++i)
@@ -234,8 +231,8 @@ inline int fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
     }
   if (rc == 0)
     for (int64_t i = 0; i < num_pairs; ++i) {
+      where[i][0] = (int32_t)src[i];
       where[i][1] = (int32_t)((uint32_t)where[i][1] | PLAN_COPY);
-      *row_src[i] = (int32_t)src[i];
     }
   return rc;
 }

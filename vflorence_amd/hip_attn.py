@@ -181,10 +181,12 @@ class GroupPlan:
     stride: int
     slots: int
     max_blocks: int
+    # copy-on-write pairs folded in (fold_plan_copies): for the fused launch only
+    folded: bool = False
 
     def to(self, device, non_blocking: bool = False) -> "GroupPlan":
         return GroupPlan(self.words.to(device, non_blocking=non_blocking), self.stride,
-                         self.slots, self.max_blocks)
+                         self.slots, self.max_blocks, self.folded)
 
 
 def group_plan_stride(max_group_size: int, max_blocks: int) -> int:
@@ -239,7 +241,8 @@ def fold_plan_copies(plan: GroupPlan, src, dst, *, num_blocks: int) -> bool:
     reading it then copies each pair's block for its layer's pools and the step needs no
     ``copy_blocks``.  Returns False, leaving the plan unchanged, when the pairs cannot
     be folded (a destination that is not one row's private block of the plan, say);
-    the caller then copies them itself."""
+    the caller then copies them itself.  A folded plan names the sources in place of
+    the fork blocks, so only ``self_attention_with_kv_write`` may read it."""
     import numpy as np
 
     if plan.words.device.type != "cpu":
@@ -250,6 +253,8 @@ def fold_plan_copies(plan: GroupPlan, src, dst, *, num_blocks: int) -> bool:
         raise ValueError("src and dst must be 1-D sequences of one length")
     rc = lib.vfl_fold_plan_copies(plan.words.data_ptr(), plan.slots, plan.stride,
                                   s.ctypes.data, d.ctypes.data, s.size, int(num_blocks))
+    if rc == _lib.VFL_OK and s.size:
+        plan.folded = True
     return rc == _lib.VFL_OK
 
 
@@ -523,6 +528,9 @@ def attention_with_kv_cache(
         _require_gpu(query, sm.group_start)
     if sm.group_order is not None:
         _require_gpu(query, sm.group_order)
+    if sm.group_plan is not None and sm.group_plan.folded:
+        raise ValueError("a group plan with copy-on-write folded in names the copy sources in "
+                         "place of the fork blocks: only self_attention_with_kv_write reads it")
     num_groups = num_rows if sm.group_start is None else sm.num_groups
     meta = sm.plan(num_rows, block_table.shape[1])
     check(
