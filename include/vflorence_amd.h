@@ -128,7 +128,8 @@ typedef struct vfl_sched_meta {
    * vfl_get_scheduler_metadata, which leaves it NULL.  A device copy of what
    * vfl_build_group_plan wrote for this call's tables, lengths and groups; the launch
    * then reads each group's distinct blocks from it instead of walking the tables,
-   * and runs group_plan_slots x num_heads workgroups. */
+   * and runs group_plan_slots x num_heads workgroups.  For shared-table groups the same
+   * fields carry slot descriptors (vfl_build_slot_descriptors). */
   const int32_t *group_plan;
   int64_t group_plan_stride;   /* words per slot (vfl_group_plan_stride)            */
   int64_t group_plan_slots;    /* slots the plan holds (>= its groups)              */
@@ -174,6 +175,28 @@ int vfl_build_group_plan(const int32_t *block_table, int64_t block_table_stride,
                          const int32_t *group_start, const int32_t *group_order,
                          int64_t num_groups, int block_size, int64_t num_blocks,
                          int32_t *plan, int64_t num_slots, int64_t stride);
+
+/*
+ * Slot descriptors for shared-table row groups (the beams of a request reading its
+ * encoder pages, vflorence/layers/attention.py:9-39 stage_cross): the per-batch part of
+ * the reference's scheduler metadata for cross-attention, made on the host once per
+ * batch composition.  Words of one slot for tables max_blocks_per_seq wide (0 when out
+ * of range).  vfl_build_slot_descriptors (host memory, no device call) writes desc, of
+ * num_slots * stride int32: slot s < num_groups holds group group_order[s] (s when
+ * group_order is NULL) as [first row, rows, seq_lens[first row], 0, block_table[first
+ * row][0 .. max_blocks_per_seq)], later slots [0, 0, 0, 0].  Passed (device copy) as
+ * vfl_sched_meta.group_plan with VFL_GROUP_SHARED_TABLE groups and group_plan_stride /
+ * group_plan_slots set, vfl_attention_with_kv_cache's 16-bit head-size-64/128 launch
+ * reads each workgroup's group from its slot in one dependent load instead of three
+ * (dispatch order, group start, then length and table); the call's group_start,
+ * group_order, seq_lens and block_table must describe the same groups.
+ */
+int64_t vfl_slot_descriptor_stride(int64_t max_blocks_per_seq);
+int vfl_build_slot_descriptors(const int32_t *block_table, int64_t block_table_stride,
+                               int max_blocks_per_seq, const int32_t *seq_lens,
+                               int64_t num_rows, const int32_t *group_start,
+                               const int32_t *group_order, int64_t num_groups, int32_t *desc,
+                               int64_t num_slots, int64_t stride);
 
 /*
  * Host function (all pointers host memory; no device call).  Folds a decode step's

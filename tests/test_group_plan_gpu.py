@@ -356,3 +356,57 @@ def test_plan_for_another_table_width_is_refused():
         hip().attention_with_kv_cache(q, kc.to(DEV), vc.to(DEV), out, None, L.to(DEV),
                                       scale=D**-0.5, block_table=wider.to(DEV),
                                       scheduler_metadata=sm)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("waves", [1, 2, 4, 8])
+def test_slot_descriptors_equal_the_group_start_path(dtype, head_dim, waves):
+    """Shared-table groups (cross-attention beams) read through slot descriptors --
+    each slot's group, length and page row in one load level -- give outputs
+    bit-identical to the dispatch-order / group-start path, with a random dispatch
+    order, empty groups and padded slots, and match the oracle."""
+    from oracle import oracle as orc
+
+    hip_attn = hip()
+    rnd = np.random.default_rng(waves + head_dim)
+    H, D, NB = 12, head_dim, 900
+    sizes = [int(x) for x in rnd.integers(0, 9, size=14)]
+    starts = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]), dtype=torch.int32)
+    N = int(starts[-1])
+    width = 40
+    table = torch.zeros(N, width, dtype=torch.int32)
+    lens = torch.zeros(N, dtype=torch.int32)
+    for g, n in enumerate(sizes):  # a group's rows share one page row and length
+        E = int(rnd.integers(0, width * BS + 1))
+        pages = rnd.permutation(NB)[: -(-E // BS)]
+        for r in range(int(starts[g]), int(starts[g + 1])):
+            table[r, : len(pages)] = torch.from_numpy(pages.astype(np.int32))
+            lens[r] = E
+    order = torch.from_numpy(rnd.permutation(len(sizes)).astype(np.int32))
+    slots = len(sizes) + 3
+    g = torch.Generator().manual_seed(waves)
+    kc = torch.randn(NB, H, BS, D, generator=g).to(dtype)
+    vc = torch.randn(NB, H, BS, D, generator=g).to(dtype)
+    q = torch.randn(N, H, D, generator=g).to(dtype)
+    gs = torch.cat([starts, torch.full((slots - len(sizes),), N, dtype=torch.int32)])
+    order_p = torch.cat([order, torch.full((slots - len(sizes),), -1, dtype=torch.int32)])
+    desc = hip_attn.build_slot_descriptors(table, lens, starts, group_order=order,
+                                           num_slots=slots).to(DEV)
+    outs = []
+    for use in (False, True):
+        sm = hip_attn.get_scheduler_metadata(
+            num_reqs=N, num_heads=H, num_kv_heads=H, head_dim=D, dtype=dtype, block_size=BS,
+            group_start=gs.to(DEV), group_order=order_p.to(DEV), max_group_size=8,
+            waves_per_workgroup=waves, slot_descriptors=desc if use else None)
+        out = torch.full((N, H, D), float("nan"), dtype=dtype, device=DEV)
+        hip_attn.attention_with_kv_cache(q.to(DEV), kc.to(DEV), vc.to(DEV), out, None,
+                                         lens.to(DEV), scale=D**-0.5, block_table=table.to(DEV),
+                                         scheduler_metadata=sm)
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    want = orc.paged_attention(q.double().numpy(), kc.double().numpy(),
+                               hip_attn.v_cache_logical(vc).double().numpy(), lens.numpy(),
+                               table.numpy(), D**-0.5)
+    np.testing.assert_allclose(outs[1].double().numpy(), want, rtol=0, atol=2e-2)

@@ -268,3 +268,60 @@ def test_fold_refusals_leave_the_plan_unchanged():
     assert torch.equal(one.words, before)
     assert hip().fold_plan_copies(one, [2], [6], num_blocks=10)
     assert decoded(one, copies=True)[1][0][3] == [(5, 0, 16, 1, False), (2, 1, 4, 1, True)]
+
+
+def restated_descriptors(table, lens, starts, order, slots, width):
+    out = []
+    groups = len(starts) - 1
+    for s in range(slots):
+        if s >= groups:
+            out.append([0, 0, 0, 0])
+            continue
+        g = order[s] if order is not None else s
+        r0, r1 = int(starts[g]), int(starts[g + 1])
+        if r1 == r0:
+            out.append([0, 0, 0, 0])
+            continue
+        out.append([r0, r1 - r0, int(lens[r0]), 0] + [int(x) for x in table[r0, :width]])
+    return out
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_slot_descriptors_match_their_definition(seed):
+    """Slot descriptors of shared-table groups (cross-attention beams): per dispatch slot,
+    the group's first row, rows, length and the first row's table row; empty slots and
+    empty groups zero."""
+    rnd = np.random.default_rng(seed)
+    sizes = [int(x) for x in rnd.integers(0, 9, size=10)]
+    starts = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    rows = int(starts[-1])
+    width = int(rnd.integers(1, 70))
+    table = rnd.integers(0, 5000, size=(rows, width)).astype(np.int32)
+    lens = rnd.integers(0, width * BS + 1, size=rows).astype(np.int32)
+    order = rnd.permutation(len(sizes)).astype(np.int32) if seed % 2 else None
+    slots = len(sizes) + seed
+    d = hip().build_slot_descriptors(
+        torch.from_numpy(table), torch.from_numpy(lens), torch.from_numpy(starts),
+        group_order=None if order is None else torch.from_numpy(order), num_slots=slots)
+    assert d.stride % 4 == 0 and d.stride >= 4 + width and d.slots == slots
+    w = d.words.numpy()
+    got = []
+    for s in range(slots):
+        rec = w[s * d.stride: (s + 1) * d.stride]
+        got.append([int(x) for x in rec[:4]] + ([int(x) for x in rec[4: 4 + width]]
+                                                if rec[1] else []))
+    assert got == restated_descriptors(table, lens, starts, order, slots, width)
+
+
+def test_slot_descriptor_refusals():
+    ha = hip()
+    t = torch.zeros(4, 2, dtype=torch.int32)
+    lens = torch.full((4,), 20, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="group order entry out of range"):
+        ha.build_slot_descriptors(t, lens, torch.tensor([0, 2, 4], dtype=torch.int32),
+                                  group_order=torch.tensor([0, 5], dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="group rows out of range"):
+        ha.build_slot_descriptors(t, lens, torch.tensor([0, 2, 9], dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="bad sizes"):  # fewer slots than groups
+        ha.build_slot_descriptors(t, lens, torch.tensor([0, 2, 4], dtype=torch.int32),
+                                  num_slots=1)

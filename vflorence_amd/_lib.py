@@ -28,6 +28,8 @@ EXPORTED_SYMBOLS = (
     "vfl_group_plan_stride",
     "vfl_build_group_plan",
     "vfl_fold_plan_copies",
+    "vfl_slot_descriptor_stride",
+    "vfl_build_slot_descriptors",
     "vfl_attention_with_kv_cache",
     "vfl_self_attention_with_kv_write",
     "vfl_copy_blocks",
@@ -78,6 +80,9 @@ _SIGNATURES = {
     ),
     "vfl_group_plan_stride": (_i64, [_i32, _i64]),
     "vfl_fold_plan_copies": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64]),
+    "vfl_slot_descriptor_stride": (_i64, [_i64]),
+    "vfl_build_slot_descriptors": (
+        ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64]),
     "vfl_build_group_plan": (
         ctypes.c_int,
         [_vp, _i64, _i32, _vp, _i64, _vp, _vp, _i64, _i32, _i64, _vp, _i64, _i64],

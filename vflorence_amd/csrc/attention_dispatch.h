@@ -26,6 +26,8 @@ struct AttnArgs {
   bool own_tables;  // groups whose rows keep their own tables (paged_decode_shared_kernel)
   const int32_t *plan;  // group plan (paged_decode_planned_kernel), or nullptr
   int64_t plan_stride, plan_slots;
+  const int32_t *desc;  // slot descriptors of shared-table groups (decode_mfma.h), or nullptr
+  int64_t desc_stride;
   bool q_vec;  // query rows 16-byte aligned
   int bs_shift;  // pool blocks of 16 << bs_shift tokens
 };
@@ -88,7 +90,8 @@ int launch_mfma_rows(const AttnArgs &a) {
   paged_decode_mfma_kernel<DT, D, NW, U, false, SHIFT><<<grid, dim3(NW * 64), 0, a.stream>>>(
       (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
       (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
-      a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw);
+      a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw, a.desc,
+      a.desc_stride);
   return launch_status("attention_with_kv_cache");
 }
 

@@ -196,6 +196,11 @@ __device__ __forceinline__ void write_new_token(const uint16_t *kc, const uint16
 // blocks); the kernel walks 16-token chunks, chunk b being part b & mask of table entry
 // b >> SHIFT (the same offset, 16 * D elements per part, in K and in the
 // 4-token-interleaved V).
+// desc (shared-table groups, no fused write): one descriptor per launch slot, at
+// desc + slot * desc_stride: first row, rows, length, 0, then the group's table row.
+// The workgroup then reads its group -- rows, length and first 64 block ids -- in one
+// dependent load level instead of three (dispatch order, group start, then length and
+// table); group_order, group_start, seq_lens and bt are not read.
 template <int DT, int D, int NW, int U, bool FUSE, int SHIFT>
 __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
     const uint16_t *__restrict__ q, int64_t q_st, int64_t q_sh, const uint16_t *kc,
@@ -203,7 +208,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
     const int32_t *__restrict__ bt, int64_t bt_stride, int max_blocks,
     const int32_t *__restrict__ group_start, const int32_t *__restrict__ group_order,
     int64_t num_rows, int64_t num_groups, int H, int64_t num_blocks, float scale_log2,
-    KvWrite kvw) {
+    KvWrite kvw, const int32_t *__restrict__ desc = nullptr, int64_t desc_stride = 0) {
   constexpr int BS = 16;
   constexpr int bs_shift = SHIFT;
   static_assert(!FUSE || SHIFT == 0, "the fused KV write is built for 16-token blocks");
@@ -220,21 +225,35 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(
   int64_t pos;
   int h;
   xcd_position(blockIdx.x, (unsigned)H, pos, h);
-  if (pos >= num_groups) return;  // workgroup-uniform
-  int g = (int)pos;
-  if (group_order) g = group_order[g];
-  if (g < 0 || g >= num_groups || h >= H) return;
-  int row0 = g, nrows = 1;
-  if (group_start) {
-    row0 = group_start[g];
-    nrows = min(group_start[g + 1] - row0, MAXG);
-  }
-  if (row0 < 0 || row0 >= num_rows) return;
-  nrows = (int)min((int64_t)nrows, num_rows - row0);
-  if (nrows <= 0) return;
+  if (pos >= num_groups || h >= H) return;  // workgroup-uniform
+  int row0, nrows, L;
   WaveBlockIds ids;
-  ids.prefetch(bt + (int64_t)row0 * bt_stride, max_blocks);
-  const int L = seq_lens[row0];
+  if (!FUSE && desc) {
+    const int32_t *rec = desc + pos * desc_stride;
+    const int4 hdr = *reinterpret_cast<const int4 *>(rec);
+    ids.prefetch(rec + 4, max_blocks);
+    row0 = hdr.x;
+    nrows = min(hdr.y, MAXG);
+    L = hdr.z;
+    if (row0 < 0 || row0 >= num_rows) return;
+    nrows = (int)min((int64_t)nrows, num_rows - row0);
+    if (nrows <= 0) return;
+  } else {
+    int g = (int)pos;
+    if (group_order) g = group_order[g];
+    if (g < 0 || g >= num_groups) return;
+    row0 = g;
+    nrows = 1;
+    if (group_start) {
+      row0 = group_start[g];
+      nrows = min(group_start[g + 1] - row0, MAXG);
+    }
+    if (row0 < 0 || row0 >= num_rows) return;
+    nrows = (int)min((int64_t)nrows, num_rows - row0);
+    if (nrows <= 0) return;
+    ids.prefetch(bt + (int64_t)row0 * bt_stride, max_blocks);
+    L = seq_lens[row0];
+  }
   int nblk = L > 0 ? (L + BS - 1) / BS : 0;  // 16-token chunks
   nblk = min(nblk, max_blocks << bs_shift);
   const int Lc = min(L, nblk * BS);

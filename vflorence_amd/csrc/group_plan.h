@@ -140,6 +140,54 @@ inline int build_group_plan(const int32_t *block_table, int64_t bt_stride, int m
   return 0;
 }
 
+// Slot descriptors of shared-table row groups (the beams of a request reading its
+// encoder pages in cross-attention): slot s at s * stride, for s < num_groups the group
+// group_order[s] (s when order is null): [first row, rows, length of the first row, 0,
+// the first row's table row (max_blocks ids)]; later slots [0, 0, 0, 0].  The
+// attention launch reads its group from its slot in one load level.
+inline int64_t slot_descriptor_stride(int64_t max_blocks) {
+  if (max_blocks < 0 || max_blocks > (int64_t)1 << 24) return 0;
+  return (4 + max_blocks + 3) / 4 * 4;
+}
+
+inline int build_slot_descriptors(const int32_t *block_table, int64_t bt_stride, int max_blocks,
+                                  const int32_t *seq_lens, int64_t num_rows,
+                                  const int32_t *group_start, const int32_t *order,
+                                  int64_t num_groups, int32_t *desc, int64_t num_slots,
+                                  int64_t stride, const char **why) {
+  *why = nullptr;
+  if (num_groups < 0 || num_groups > num_slots || num_rows < 0 || max_blocks < 0 ||
+      stride < slot_descriptor_stride(max_blocks) || stride % 4 != 0 || bt_stride < max_blocks) {
+    *why = "bad sizes";
+    return -1;
+  }
+  if (num_groups > 0 && (!block_table || !seq_lens || !group_start)) {
+    *why = "null table, lengths or group starts";
+    return -1;
+  }
+  for (int64_t s = 0; s < num_slots; ++s) {
+    int32_t *rec = desc + s * stride;
+    rec[0] = rec[1] = rec[2] = rec[3] = 0;
+    if (s >= num_groups) continue;
+    const int64_t g = order ? order[s] : s;
+    if (g < 0 || g >= num_groups) {
+      *why = "group order entry out of range";
+      return -1;
+    }
+    const int64_t r0 = group_start[g], r1 = group_start[g + 1];
+    if (r0 < 0 || r1 < r0 || r1 > num_rows) {
+      *why = "group rows out of range";
+      return -1;
+    }
+    if (r1 == r0) continue;
+    rec[0] = (int32_t)r0;
+    rec[1] = (int32_t)(r1 - r0);
+    rec[2] = seq_lens[r0];
+    for (int b = 0; b < max_blocks; ++b) rec[4 + b] = block_table[r0 * bt_stride + b];
+  }
+  return 0;
+}
+
 // Fold a step's copy-on-write pairs (src[i] -> dst[i]) into its plan (the used slots
 // of build_group_plan's output): the entry holding block dst[i] gets the copy flag and
 // src[i] in place of dst[i].  Each destination must be a block in

@@ -76,7 +76,8 @@ static int launch_mfma(const AttnArgs &a) {
         <<<grid, dim3(NW * 64), 0, a.stream>>>(
         (const uint16_t *)a.q, a.q_st, a.q_sh, (const uint16_t *)a.kc, (const uint16_t *)a.vc,
         (uint16_t *)a.out, a.seq_lens, a.bt, a.bt_stride, a.max_blocks, a.group_start,
-        a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw);
+        a.group_order, a.num_rows, a.num_groups, a.H, a.num_blocks, a.scale_log2, a.kvw, a.desc,
+        a.desc_stride);
   return launch_status("attention_with_kv_cache");
 }
 
@@ -219,6 +220,30 @@ extern "C" int vfl_build_group_plan(const int32_t *block_table, int64_t block_ta
   return VFL_OK;
 }
 
+extern "C" int64_t vfl_slot_descriptor_stride(int64_t max_blocks_per_seq) {
+  return slot_descriptor_stride(max_blocks_per_seq);
+}
+
+extern "C" int vfl_build_slot_descriptors(const int32_t *block_table, int64_t block_table_stride,
+                                          int max_blocks_per_seq, const int32_t *seq_lens,
+                                          int64_t num_rows, const int32_t *group_start,
+                                          const int32_t *group_order, int64_t num_groups,
+                                          int32_t *desc, int64_t num_slots, int64_t stride) {
+  clear_error();
+  if (!desc) {
+    set_error("build_slot_descriptors: desc is NULL");
+    return VFL_E_INVALID;
+  }
+  const char *why = nullptr;
+  if (build_slot_descriptors(block_table, block_table_stride, max_blocks_per_seq, seq_lens,
+                             num_rows, group_start, group_order, num_groups, desc, num_slots,
+                             stride, &why) != 0) {
+    set_error("build_slot_descriptors: %s", why);
+    return VFL_E_INVALID;
+  }
+  return VFL_OK;
+}
+
 extern "C" int vfl_fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
                                     const int64_t *src, const int64_t *dst, int64_t num_pairs,
                                     int64_t num_blocks) {
@@ -341,6 +366,24 @@ static int attention_impl(const void *query, int64_t query_stride_token,
     a.plan = meta->group_plan;
     a.plan_stride = meta->group_plan_stride;
     a.plan_slots = meta->group_plan_slots;
+  }
+  // Shared-table groups (cross-attention beams) with slot descriptors in group_plan.
+  a.desc = nullptr;
+  a.desc_stride = 0;
+  if (meta->group_plan != nullptr && !a.own_tables && group_start != nullptr && full_set &&
+      kvw.slots == nullptr) {
+    if ((uintptr_t)meta->group_plan % 16 != 0 ||
+        meta->group_plan_stride < slot_descriptor_stride(meta->max_blocks_per_seq) ||
+        meta->group_plan_stride % 4 != 0 || meta->group_plan_slots < num_groups) {
+      set_error("%s: slot descriptors of %lld slots x %lld words (16-byte aligned, stride at "
+                "least %lld, at least num_groups %lld slots)",
+                who, (long long)meta->group_plan_slots, (long long)meta->group_plan_stride,
+                (long long)slot_descriptor_stride(meta->max_blocks_per_seq),
+                (long long)num_groups);
+      return VFL_E_INVALID;
+    }
+    a.desc = meta->group_plan;
+    a.desc_stride = meta->group_plan_stride;
   }
   if (a.own_tables && !full_set) {
     // The VALU kernel and the one-row matrix-core kernel read one table per group; with

@@ -235,6 +235,51 @@ def build_group_plan(block_table: torch.Tensor, seq_lens: torch.Tensor,
     return GroupPlan(out[:words], stride, slots, width)
 
 
+def slot_descriptor_stride(max_blocks: int) -> int:
+    """int32 words of one slot descriptor over block tables ``max_blocks`` wide."""
+    stride = int(lib.vfl_slot_descriptor_stride(int(max_blocks)))
+    if stride <= 0:
+        raise ValueError(f"no slot descriptors for tables {max_blocks} wide")
+    return stride
+
+
+def build_slot_descriptors(block_table: torch.Tensor, seq_lens: torch.Tensor,
+                           group_start: torch.Tensor, *, group_order: torch.Tensor | None = None,
+                           num_slots: int | None = None,
+                           out: torch.Tensor | None = None) -> GroupPlan:
+    """Slot descriptors of shared-table groups (``vfl_build_slot_descriptors``) from host
+    CPU int32 tensors: per dispatch slot, the group's first row, rows, length and table
+    row, so a cross-attention workgroup reads its group in one load level.  Pass the
+    device copy as ``get_scheduler_metadata(slot_descriptors=...)``.  ``num_slots``
+    (default: the group count) sizes it for a launch padded to more groups; ``out``
+    reuses a CPU int32 buffer of at least the size."""
+    for name, t in (("block_table", block_table), ("seq_lens", seq_lens),
+                    ("group_start", group_start)):
+        if t.device.type != "cpu" or t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous CPU int32 tensor")
+    if block_table.dim() != 2 or seq_lens.shape != (block_table.shape[0],):
+        raise ValueError("block_table must be [rows, width] and seq_lens [rows]")
+    num_groups = group_start.numel() - 1
+    if group_order is not None and (group_order.device.type != "cpu" or
+                                    group_order.dtype != torch.int32 or
+                                    group_order.shape != (num_groups,)):
+        raise ValueError(f"group_order must be a CPU int32 tensor [{num_groups}]")
+    slots = num_groups if num_slots is None else int(num_slots)
+    width = block_table.shape[1]
+    stride = slot_descriptor_stride(width)
+    words = slots * stride
+    if out is None:
+        out = torch.empty(max(words, 4), dtype=torch.int32)
+    elif out.device.type != "cpu" or out.dtype != torch.int32 or out.numel() < words:
+        raise ValueError(f"out must be a CPU int32 tensor of at least {words} words")
+    check(lib.vfl_build_slot_descriptors(
+        block_table.data_ptr(), block_table.stride(0), width, seq_lens.data_ptr(),
+        block_table.shape[0], group_start.data_ptr(),
+        None if group_order is None else group_order.data_ptr(), num_groups, out.data_ptr(),
+        slots, stride))
+    return GroupPlan(out[:max(words, 4)], stride, slots, width)
+
+
 def fold_plan_copies(plan: GroupPlan, src, dst, *, num_blocks: int) -> bool:
     """Fold a step's copy-on-write pairs ``src[i] -> dst[i]`` (host int64 sequences)
     into a host group plan (``vfl_fold_plan_copies``): the fused self-attention launch
@@ -303,6 +348,9 @@ class SchedulerMetadata:
     # Device copy of the step's group plan (own-table groups, 16-bit caches): the
     # launch reads the groups' blocks from it instead of walking the tables.
     group_plan: GroupPlan | None = None
+    # Device copy of slot descriptors (shared-table groups, build_slot_descriptors): the
+    # launch reads each slot's group, length and table row from it in one load level.
+    slot_descriptors: GroupPlan | None = None
     _plans: dict = field(default_factory=dict, repr=False)
 
     def plan(self, num_rows: int, max_blocks: int) -> SchedMeta:
@@ -343,7 +391,7 @@ class SchedulerMetadata:
                     ctypes.byref(meta),
                 )
             )
-            gp = self.group_plan
+            gp = self.group_plan if self.group_plan is not None else self.slot_descriptors
             if gp is not None:
                 if gp.max_blocks != max_blocks:
                     raise ValueError(f"the group plan was made for block tables {gp.max_blocks} "
@@ -413,6 +461,7 @@ def get_scheduler_metadata(
     own_tables: bool = False,
     group_plan: GroupPlan | None = None,
     active_groups: int | None = None,
+    slot_descriptors: GroupPlan | None = None,
 ) -> SchedulerMetadata:
     """Counterpart of ``vllm_cpu_attn.get_scheduler_metadata`` (keyword names from
     vflorence/layers/attention.py:18-29 and vflorence/engine/model_runner.py:308-319).
@@ -449,6 +498,16 @@ def get_scheduler_metadata(
                 or group_plan.slots < num_groups):
             raise ValueError("group_plan must be a device copy of build_group_plan's output "
                              f"with at least {num_groups} slots")
+    if slot_descriptors is not None:
+        if own_tables or group_start is None:
+            raise ValueError("slot descriptors describe shared-table row groups (group_start, "
+                             "own_tables=False)")
+        w = slot_descriptors.words
+        if (w.device.type != "cuda" or w.dtype != torch.int32 or not w.is_contiguous()
+                or w.numel() < slot_descriptors.slots * slot_descriptors.stride
+                or slot_descriptors.slots < num_groups):
+            raise ValueError("slot_descriptors must be a device copy of build_slot_descriptors' "
+                             f"output with at least {num_groups} slots")
     return SchedulerMetadata(
         num_heads=num_heads,
         head_dim=head_dim,
@@ -463,6 +522,7 @@ def get_scheduler_metadata(
         own_tables=own_tables,
         group_plan=group_plan,
         active_groups=active_groups,
+        slot_descriptors=slot_descriptors,
     )
 
 

@@ -14,6 +14,7 @@ from __future__ import annotations
 import torch
 
 from .. import hip_attn
+from .._lib import check, lib
 from ..utils.context import get_context
 
 # Head sizes with a gfx950 kernel (the reference lists its CPU ISAs' sizes at :6).
@@ -44,7 +45,10 @@ class CrossStagingBuffers:
     twin laid out for up to ``max_rows`` rows and ``max_pages`` pages per row.
 
     int32 words: lengths [max_rows] | group starts [max_rows + 1] | dispatch order
-    [max_rows] | page table [max_rows, max_pages].  Every batch of n rows uses the
+    [max_rows] | page table [max_rows, max_pages] | (16-byte aligned) one slot
+    descriptor per launch slot (``hip_attn.build_slot_descriptors``: the slot's group,
+    length and page row, which the launch reads in one load level).  Every batch of n
+    rows uses the
     same addresses and launch shape (a group slot count fixed per row count and beam
     width, unused slots marked -1 in the order),
     so a decode step captured in a HIP graph stays valid when the batch's requests,
@@ -54,21 +58,25 @@ class CrossStagingBuffers:
     def __init__(self, max_rows: int, max_pages: int, device):
         self.max_rows, self.max_pages = max_rows, max_pages
         m = max_rows
-        words = 3 * m + 1 + m * max_pages
+        self.desc_stride = hip_attn.slot_descriptor_stride(max_pages)
+        desc_at = (3 * m + 1 + m * max_pages + 3) // 4 * 4
+        words = desc_at + m * self.desc_stride
         self.host = torch.zeros(words, dtype=torch.int32, pin_memory=True)
         self.dev = torch.zeros(words, dtype=torch.int32, device=device)
         self.copied = torch.cuda.Event()
         self.copied.record()
         self.np = self.host.numpy()
-        self.offsets = (0, m, 2 * m + 1, 3 * m + 1)
+        self.offsets = (0, m, 2 * m + 1, 3 * m + 1, desc_at)
 
     def views(self, n: int, slots: int | None = None):
-        """Lengths and table of ``n`` rows; group starts and order of ``slots`` launch
-        slots (default ``n``)."""
+        """Lengths and table of ``n`` rows; group starts, order and slot descriptors of
+        ``slots`` launch slots (default ``n``)."""
         o, g = self.offsets, n if slots is None else slots
+        desc = hip_attn.GroupPlan(self.dev[o[4]: o[4] + g * self.desc_stride], self.desc_stride,
+                                  g, self.max_pages)
         return (self.dev[o[0]: o[0] + n], self.dev[o[1]: o[1] + g + 1], self.dev[o[2]: o[2] + g],
                 self.dev[o[3]: o[3] + self.max_rows * self.max_pages]
-                .view(self.max_rows, self.max_pages)[:n])
+                .view(self.max_rows, self.max_pages)[:n], desc)
 
 
 def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts, run, slots=None):
@@ -90,6 +98,11 @@ def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts, run, slot
     for i, p in enumerate(pages):
         table[i, : len(p)] = p.numpy() if isinstance(p, torch.Tensor) else p
         table[i, len(p):] = 0
+    base = buffers.host.data_ptr()
+    check(lib.vfl_build_slot_descriptors(
+        base + 4 * o[3], buffers.max_pages, buffers.max_pages, base + 4 * o[0], n,
+        base + 4 * o[1], base + 4 * o[2], ng, base + 4 * o[4], n if slots is None else slots,
+        buffers.desc_stride))
     buffers.dev.copy_(buffers.host, non_blocking=True)
     buffers.copied.record()
     return buffers.views(n, slots)
@@ -119,8 +132,8 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=N
     if buffers is not None:
         if slots is None or not ng <= slots <= n:
             slots = n
-        seq_lens, group_start, group_order, block_table = _stage_into(buffers, pages, enc_lens,
-                                                                      starts, run, slots)
+        seq_lens, group_start, group_order, block_table, desc = _stage_into(
+            buffers, pages, enc_lens, starts, run, slots)
         # n slots, about n / (beams per request) of them working: waves per workgroup as
         # for a launch of that many groups (4 beams of 64 requests: 1024 workgroups and
         # eight waves, not the 4096 slots' four).  Slots over beam width, not the exact
@@ -135,21 +148,27 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=N
         )
         width = block_table.shape[1]
         order = hip_attn.balanced_order([enc_lens[a] for a in starts[:-1]], run)
-        # One host->device copy:
-        # [seq_lens (n) | group starts (ng + 1) | group order (ng) | block table (n * width)].
-        host = torch.cat(
-            [
-                torch.tensor(enc_lens, dtype=torch.int32),
-                torch.tensor(starts, dtype=torch.int32),
-                torch.tensor(order, dtype=torch.int32),
-                block_table.flatten(),
-            ]
-        )
-        dev = host.to(device)
+        lens_h = torch.tensor(enc_lens, dtype=torch.int32)
+        starts_h = torch.tensor(starts, dtype=torch.int32)
+        order_h = torch.tensor(order, dtype=torch.int32)
+        parts = [lens_h, starts_h, order_h, block_table.flatten()]
+        fixed = sum(t.numel() for t in parts)
+        if max_group > 1:  # slot descriptors, 16-byte aligned after the rest
+            desc_h = hip_attn.build_slot_descriptors(block_table, lens_h, starts_h,
+                                                     group_order=order_h)
+            parts += [torch.zeros(-fixed % 4, dtype=torch.int32), desc_h.words]
+        # One host->device copy: [seq_lens (n) | group starts (ng + 1) | group order (ng) |
+        # block table (n * width) | slot descriptors].
+        dev = torch.cat(parts).to(device)
         seq_lens = dev[:n]
         group_start = dev[n : n + ng + 1] if max_group > 1 else None
         group_order = dev[n + ng + 1 : n + 2 * ng + 1]
-        block_table = dev[n + 2 * ng + 1 :].view(n, width)
+        block_table = dev[n + 2 * ng + 1 : fixed].view(n, width)
+        desc = None
+        if max_group > 1:
+            at = fixed + (-fixed % 4)
+            desc = hip_attn.GroupPlan(dev[at: at + desc_h.words.numel()], desc_h.stride,
+                                      desc_h.slots, desc_h.max_blocks)
     metadata = hip_attn.get_scheduler_metadata(
         num_reqs=n,
         num_heads=attn.num_heads,
@@ -164,6 +183,7 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=N
         group_order=group_order,
         max_group_size=max_group,
         active_groups=active,
+        slot_descriptors=desc,
     )
     return [
         (
