@@ -198,7 +198,7 @@ class ModelRunner:
         self._fold_copies = hip_attn.plan_copies_supported(self.dtype, self.head_dim,
                                                            self.block_size)
         self._step_slots = 0
-        self.step_rows = 0
+        self.step_rows = self.step_pairs = 0
         self._no_pages = torch.zeros(0, dtype=torch.int32)
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
         # the decoder step; compiled as the reference compiles it when asked
@@ -460,6 +460,7 @@ class ModelRunner:
         """Encode the step's newly admitted requests, run one decoder step over the
         scheduled rows, return ``_sample``'s result (None for an empty step)."""
         self.step_rows = batch.num_rows  # rows of the latest step (packed in _buffers)
+        self.step_pairs = batch.num_pairs  # its copy-on-write pairs
         if batch.num_rows == 0:
             return None
         if batch.fresh:
