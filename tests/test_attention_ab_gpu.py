@@ -44,9 +44,10 @@ GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "token_fixtures.json"
 # logit, in rounding steps of the row's largest candidate logit (bf16).  The two
 # attention paths agree to within bf16's rounding of their outputs (relative 2^-8);
 # carried through the decoder's post-LayerNorm layers that moves the row's logits by
-# less than one such step before the LM head rounds them, so a rounded logit lands at
-# most one step away -- two allows for a pre-rounding change just over one step.
-STEP_ULPS = 2
+# about one such step before the LM head rounds them (measured: at most 2 steps at
+# BART-large depth, 1 at Florence-2-base).  A wrong kernel -- a dropped token, a wrong
+# scale, a mixed-up beam group -- moves them by many.
+STEP_ULPS = 4
 # Two candidates can swap when their margin is below the sum of their perturbations:
 # each accumulated score moves by at most the sum of the one-step changes so far.
 FLIP_FACTOR = 2.0
