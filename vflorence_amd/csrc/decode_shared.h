@@ -141,7 +141,7 @@ __device__ __forceinline__ void store_new_token(const uint16_t *kc, const uint16
   if (store && col == t_new) {
 #pragma unroll
     for (int kk = 0; kk < D / 32; ++kk)
-      *reinterpret_cast<uint4 *>(tile_k + k_lane + 32 * kk) = blk.k[kk];
+      store_stream16(tile_k + k_lane + 32 * kk, blk.k[kk]);
   }
   if (rg == t_new / 4) {
     const bool upper = (t_new & 2) != 0;
@@ -153,7 +153,7 @@ __device__ __forceinline__ void store_new_token(const uint16_t *kc, const uint16
       const uint32_t y = (blk.v[c].y & keep) | (newv[c] << sh);
       blk.v[c].x = upper ? blk.v[c].x : x;
       blk.v[c].y = upper ? y : blk.v[c].y;
-      if (store) *reinterpret_cast<uint2 *>(tile_v + v_lane + 64 * c) = blk.v[c];
+      if (store) store_stream8(tile_v + v_lane + 64 * c, blk.v[c]);
     }
   }
 }
@@ -168,10 +168,10 @@ __device__ __forceinline__ void store_block(const uint16_t *kc, const uint16_t *
   uint16_t *tile_v = const_cast<uint16_t *>(vc) + (int64_t)id * block_elems + head_off;
 #pragma unroll
   for (int kk = 0; kk < D / 32; ++kk)
-    *reinterpret_cast<uint4 *>(tile_k + k_lane + 32 * kk) = blk.k[kk];
+    store_stream16(tile_k + k_lane + 32 * kk, blk.k[kk]);
 #pragma unroll
   for (int c = 0; c < D / 16; ++c)
-    *reinterpret_cast<uint2 *>(tile_v + v_lane + 64 * c) = blk.v[c];
+    store_stream8(tile_v + v_lane + 64 * c, blk.v[c]);
 }
 
 // 16 bytes of a new-token row (K or V of one head), 16-byte aligned when `vec`.
