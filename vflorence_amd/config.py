@@ -11,7 +11,6 @@ kernels' block.
 
 from __future__ import annotations
 
-import math
 import os
 from dataclasses import dataclass, field
 
@@ -44,46 +43,63 @@ class Config:
     generation_config: object = field(init=False)
 
     def __post_init__(self) -> None:
-        from transformers import AutoConfig, GenerationConfig, PretrainedConfig
-
         self.block_size = BLOCK_SIZE
-        if self.max_num_seqs <= 0:
-            raise ValueError("max_num_seqs must be positive")
+        self._check_options()
+        self.hf_config, self.generation_config = _model_configs(self.model)
+        self.text_config = self.hf_config.get_text_config()
+        limit = self.text_config.max_position_embeddings
+        if self.max_decoder_len is None:
+            # the generation config's token budget, padded to the block it ends in
+            budget = SamplingParams.from_generation_config(self.generation_config).max_tokens
+            self.max_decoder_len = min(_blocks(min(budget, limit)) * BLOCK_SIZE, limit)
+        if self.max_encoder_len is None:
+            self.max_encoder_len = limit
+        for name, value in (("max_decoder_len", self.max_decoder_len),
+                            ("max_encoder_len", self.max_encoder_len)):
+            if value < 1 or value > limit:
+                raise ValueError(f"{name}={value} is outside 1..{limit}, the model's "
+                                 "max_position_embeddings")
+        # one pool of decoder blocks and one of encoder blocks, each for max_num_seqs
+        # requests at their longest
+        if self.num_blocks is None:
+            self.num_blocks = self.max_num_seqs * _blocks(self.max_decoder_len)
+        self.num_cross_blocks = self.max_num_seqs * _blocks(self.max_encoder_len)
+        if self.num_blocks <= 0:
+            raise ValueError(f"num_blocks={self.num_blocks}: the decoder pool needs a block")
+
+    def _check_options(self) -> None:
+        if self.max_num_seqs < 1:
+            raise ValueError(f"max_num_seqs={self.max_num_seqs}: at least one request "
+                             "must fit a step")
         if self.compile and self.cuda_graphs:
             raise ValueError("compile and cuda_graphs are alternatives; choose one")
-        if self.dtype not in (torch.float32, torch.bfloat16, torch.float16):
-            raise ValueError("dtype must be torch.float32, torch.bfloat16 or torch.float16")
-        if isinstance(self.model, PretrainedConfig):
-            self.hf_config = self.model
-            self.generation_config = GenerationConfig()
-        else:
-            path = os.fspath(self.model)
-            if not os.path.isdir(path):
-                raise ValueError(f"model must be a local checkpoint directory, got {path!r}")
-            self.hf_config = AutoConfig.from_pretrained(path, local_files_only=True)
-            try:
-                self.generation_config = GenerationConfig.from_pretrained(
-                    path, local_files_only=True)
-            except OSError:
-                self.generation_config = GenerationConfig()
-        self.text_config = self.hf_config.get_text_config()
-        max_positions = self.text_config.max_position_embeddings
-        bs = self.block_size
+        if self.dtype not in _DTYPES:
+            raise ValueError(f"dtype {self.dtype} is not one of the caches' types "
+                             "(torch.float32, torch.bfloat16, torch.float16)")
 
-        def whole_blocks(n):
-            return min(math.ceil(min(n, max_positions) / bs) * bs, max_positions)
 
-        if self.max_decoder_len is None:
-            self.max_decoder_len = whole_blocks(
-                SamplingParams.from_generation_config(self.generation_config).max_tokens)
-        if self.max_encoder_len is None:
-            self.max_encoder_len = whole_blocks(math.inf)
-        for name in ("max_decoder_len", "max_encoder_len"):
-            if not 0 < getattr(self, name) <= max_positions:
-                raise ValueError(
-                    f"{name} must be in [1, max_position_embeddings={max_positions}]")
-        if self.num_blocks is None:
-            self.num_blocks = self.max_num_seqs * math.ceil(self.max_decoder_len / bs)
-        self.num_cross_blocks = self.max_num_seqs * math.ceil(self.max_encoder_len / bs)
-        if self.num_blocks <= 0:
-            raise ValueError("num_blocks must be positive")
+_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _blocks(tokens: int) -> int:
+    """Blocks of BLOCK_SIZE tokens that hold ``tokens`` tokens."""
+    return -(-tokens // BLOCK_SIZE)
+
+
+def _model_configs(model):
+    """(model config, generation config) of an in-memory transformers config or of a
+    local checkpoint directory; a directory without generation_config.json gets the
+    library's defaults."""
+    from transformers import AutoConfig, GenerationConfig, PretrainedConfig
+
+    if isinstance(model, PretrainedConfig):
+        return model, GenerationConfig()
+    path = os.fspath(model)
+    if not os.path.isdir(path):
+        raise ValueError(f"model must be a local checkpoint directory, got {path!r}")
+    hf = AutoConfig.from_pretrained(path, local_files_only=True)
+    try:
+        gen = GenerationConfig.from_pretrained(path, local_files_only=True)
+    except OSError:
+        gen = GenerationConfig()
+    return hf, gen
