@@ -67,11 +67,13 @@ __device__ __forceinline__ uint2 load_stream8(const uint16_t *p) {
   const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(p));
   return make_uint2(v.x, v.y);
 }
-// The fused KV write's stores are non-temporal too.  Nothing in the launch reads them
-// back, and a streamed line does not stay dirty in the XCD's L2, which the end of
-// every launch writes back before the next one starts: on the 64 x 4-beam decode step
-// the step ran 0.5113 -> 0.4924 ms with these stores streamed (write-through stores,
-// sc0 sc1, ran it at 0.853 ms).
+// The beam-group kernels' fused KV write stores non-temporally too.  Nothing in the
+// launch reads them back, and a streamed line does not stay dirty in the XCD's L2, which
+// the end of every launch writes back before the next one starts: on the 64 x 4-beam
+// decode step the step ran 0.5113 -> 0.4924 ms with these stores streamed (write-through
+// stores, sc0 sc1, ran it at 0.853 ms).  The one-row kernel below keeps ordinary stores:
+// its write goes out after the first stage of a long launch, and streamed there the
+// 256-sequence op ran 105.9 against 102.2 us.
 __device__ __forceinline__ void store_stream16(uint16_t *p, uint4 v) {
   __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t *>(p));
 }
@@ -180,7 +182,7 @@ __device__ __forceinline__ void write_new_token(const uint16_t *kc, const uint16
     for (int kk = 0; kk < k_chunks<D>(); ++kk) {
       if (!k_chunk_ok<D>(kk, rg)) continue;
       blk.k[kk] = newk[kk];
-      store_stream16(tile_k + k_lane + 32 * kk, newk[kk]);
+      *reinterpret_cast<uint4 *>(tile_k + k_lane + 32 * kk) = newk[kk];
     }
   }
   if (rg == t_new / 4) {
@@ -194,7 +196,7 @@ __device__ __forceinline__ void write_new_token(const uint16_t *kc, const uint16
       const uint32_t y = (blk.v[c].y & keep) | (newv[c] << sh);
       blk.v[c].x = upper ? blk.v[c].x : x;
       blk.v[c].y = upper ? y : blk.v[c].y;
-      store_stream8(tile_v + v_lane + 64 * c, blk.v[c]);
+      *reinterpret_cast<uint2 *>(tile_v + v_lane + 64 * c) = blk.v[c];
     }
   }
 }
