@@ -29,14 +29,16 @@ logger = logging.getLogger(__name__)
 
 class LLMEngine:
     def __init__(self, model, state_dict: dict | None = None, **kwargs):
-        self.config = Config(model, **kwargs)
-        self.runner = ModelRunner(self.config, state_dict)
-        self.scheduler = Scheduler(self.config)
-        text = self.config.text_config
+        config = Config(model, **kwargs)
+        text = config.text_config
+        self.config = config
         self.decoder_start_token_id = text.decoder_start_token_id
         self.eos_token_id = text.eos_token_id
+        # the checkpoint's generation config fills whatever a request leaves unset
         self._sampling_params = SamplingParams.from_generation_config(
-            self.config.generation_config, self.eos_token_id)
+            config.generation_config, self.eos_token_id)
+        self.scheduler = Scheduler(config)
+        self.runner = ModelRunner(config, state_dict)
         self._next_request_id = 0
 
     # -- requests ------------------------------------------------------------------------
@@ -109,28 +111,48 @@ class LLMEngine:
     def generate(self, requests, sampling_params: SamplingParams | None = None,
                  use_tqdm: bool = False) -> list[RequestOut]:
         """Run ``requests`` (one or a list) to completion; one RequestOut each, in order.
-        A request the engine rejects gets an empty completion."""
-        if isinstance(requests, Request):
-            requests = [requests]
-        results: list = []
-        for request in requests:
-            try:
-                results.append(self.add_request(request, sampling_params))
-            except ValueError as exc:
-                logger.error("request rejected: %s", exc)
-                results.append(RequestOut(request.input_ids, [], request.pixel_values))
-        done: dict[int, RequestOut] = {}
-        # the step loop allocates no reference cycles; the cyclic collector would only
-        # add pauses to it
-        collecting = gc.isenabled()
+        A request the engine rejects gets an empty completion.  ``use_tqdm`` shows a
+        progress bar over the accepted requests."""
+        batch = [requests] if isinstance(requests, Request) else list(requests)
+        ids = [self._admit(r, sampling_params) for r in batch]
+        bar = None
+        if use_tqdm:
+            from tqdm.auto import tqdm
+
+            bar = tqdm(total=sum(i is not None for i in ids), desc="Generating", unit="req")
+        try:
+            finished = self._drain(bar)
+        finally:
+            if bar is not None:
+                bar.close()
+        return [finished[i] if i is not None else RequestOut(r.input_ids, [], r.pixel_values)
+                for r, i in zip(batch, ids)]
+
+    def _admit(self, request: Request, params: SamplingParams | None) -> int | None:
+        """Queue one request of a ``generate`` call; None (logged) when it is rejected."""
+        try:
+            return self.add_request(request, params)
+        except ValueError as exc:
+            logger.error("request rejected: %s", exc)
+            return None
+
+    def _drain(self, bar=None) -> dict[int, RequestOut]:
+        """Step until no request is left; on any exception every request is dropped and
+        its blocks and pages freed before the exception propagates.  The step loop makes
+        no reference cycles, so the cyclic collector is paused around it."""
+        finished: dict[int, RequestOut] = {}
+        paused = gc.isenabled()
         gc.disable()
         try:
             while not self.is_finished():
-                done.update(self.step())
+                done = self.step()
+                finished.update(done)
+                if bar is not None and done:
+                    bar.update(len(done))
         except BaseException:
             self.abort()
             raise
         finally:
-            if collecting:
+            if paused:
                 gc.enable()
-        return [done[r] if isinstance(r, int) else r for r in results]
+        return finished
