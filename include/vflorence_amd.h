@@ -213,7 +213,8 @@ int vfl_build_slot_descriptors(const int32_t *block_table, int64_t block_table_s
  * (num_slots and stride as given to it).  Refused (VFL_E_INVALID, plan unchanged) when
  * a block is out of
  * [0, num_blocks), a destination repeats or is also a source, or a destination is not
- * exactly one single-row entry of the plan; the caller then copies the pairs itself.
+ * exactly one single-row entry of the plan at that row's last position; the caller then
+ * copies the pairs itself.
  */
 int vfl_fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
                          const int64_t *src, const int64_t *dst, int64_t num_pairs,

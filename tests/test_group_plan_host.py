@@ -258,14 +258,16 @@ def test_fold_refusals_leave_the_plan_unchanged():
         assert torch.equal(plan.words, words)
     assert hip().fold_plan_copies(plan, [], [], num_blocks=nb)
     assert torch.equal(plan.words, words)
-    # one row, two private blocks: only one of them can be its fork block
+    # one row, two private blocks: only the last one, where the new token goes, can be
+    # its fork block (the fused launch stores the copy to the block of the row's slot)
     one = hip().build_group_plan(torch.tensor([[5, 6]], dtype=torch.int32),
                                  torch.tensor([20], dtype=torch.int32),
                                  torch.tensor([0, 1], dtype=torch.int32), num_blocks=10)
     before = one.words.clone()
-    assert not hip().fold_plan_copies(one, [1, 2], [5, 6], num_blocks=10)
-    assert b"a row has two copy destinations" in lib.vfl_last_error()
-    assert torch.equal(one.words, before)
+    for s_, d_ in (([1, 2], [5, 6]), ([1], [5])):
+        assert not hip().fold_plan_copies(one, s_, d_, num_blocks=10)
+        assert b"not its row's last block" in lib.vfl_last_error()
+        assert torch.equal(one.words, before)
     assert hip().fold_plan_copies(one, [2], [6], num_blocks=10)
     assert decoded(one, copies=True)[1][0][3] == [(5, 0, 16, 1, False), (2, 1, 4, 1, True)]
 

@@ -191,9 +191,9 @@ inline int build_slot_descriptors(const int32_t *block_table, int64_t bt_stride,
 // Fold a step's copy-on-write pairs (src[i] -> dst[i]) into its plan (the used slots
 // of build_group_plan's output): the entry holding block dst[i] gets the copy flag and
 // src[i] in place of dst[i].  Each destination must be a block in
-// [0, num_blocks) that exactly one entry of the plan holds, for one row (the fresh
-// block a fork writes into), one per row; sources in [0, num_blocks); no block both a
-// destination and a source, no destination twice.  All pairs are checked before the
+// [0, num_blocks) that exactly one entry of the plan holds, for one row, at that row's
+// last position (the fresh block a fork writes into), one per row; sources in
+// [0, num_blocks); no block both a destination and a source, no destination twice.  All pairs are checked before the
 // plan changes: on -1 (with *why set) the plan is as it was and the caller copies the
 // pairs itself.
 inline int fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
@@ -246,6 +246,16 @@ inline int fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
       rc = -1;
       break;
     }
+    // each row's last position in the slot: a destination must be there (it is the block
+    // the row's new token goes to, where the fused launch stores the copy)
+    int32_t last_pos[PLAN_MAX_ROWS];
+    for (int c = 0; c < PLAN_MAX_ROWS; ++c) last_pos[c] = -1;
+    for (int64_t e = 0; e < ne; ++e) {
+      const uint32_t meta = (uint32_t)rec[PLAN_HEADER + PLAN_ENTRY * e + 1];
+      const int32_t pos = (int32_t)((meta >> 16) & 0x7fffu);
+      for (int c = 0; c < PLAN_MAX_ROWS; ++c)
+        if ((meta >> c) & 1u) last_pos[c] = std::max(last_pos[c], pos);
+    }
     uint32_t taken = 0;  // rows of the slot that received a copy source
     for (int64_t e = 0; e < ne; ++e) {
       int32_t *ent = rec + PLAN_HEADER + PLAN_ENTRY * e;
@@ -265,6 +275,11 @@ inline int fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
       while (!((rows >> c) & 1u)) ++c;
       if ((taken >> c) & 1u) {
         *why = "a row has two copy destinations";
+        rc = -1;
+        break;
+      }
+      if ((int32_t)(((uint32_t)ent[1] >> 16) & 0x7fffu) != last_pos[c]) {
+        *why = "a copy destination is not its row's last block";
         rc = -1;
         break;
       }
