@@ -361,20 +361,21 @@ def test_plan_for_another_table_width_is_refused():
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim", [64, 128])
 @pytest.mark.parametrize("waves", [1, 2, 4, 8])
-def test_slot_descriptors_equal_the_group_start_path(dtype, head_dim, waves):
+@pytest.mark.parametrize("width", [40, 100])
+def test_slot_descriptors_equal_the_group_start_path(dtype, head_dim, waves, width):
     """Shared-table groups (cross-attention beams) read through slot descriptors --
     each slot's group, length and page row in one load level -- give outputs
     bit-identical to the dispatch-order / group-start path, with a random dispatch
-    order, empty groups and padded slots, and match the oracle."""
+    order, empty groups and padded slots, and match the oracle.  Width 100: page rows
+    past the 64 ids a wave holds at a time, read on from the descriptor."""
     from oracle import oracle as orc
 
     hip_attn = hip()
-    rnd = np.random.default_rng(waves + head_dim)
+    rnd = np.random.default_rng(waves + head_dim + width)
     H, D, NB = 12, head_dim, 900
     sizes = [int(x) for x in rnd.integers(0, 9, size=14)]
     starts = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]), dtype=torch.int32)
     N = int(starts[-1])
-    width = 40
     table = torch.zeros(N, width, dtype=torch.int32)
     lens = torch.zeros(N, dtype=torch.int32)
     for g, n in enumerate(sizes):  # a group's rows share one page row and length
