@@ -288,6 +288,60 @@ def test_prepare_and_encode_follow_the_reference_formulas(small_engine):
     assert_clean(llm)
 
 
+def test_packed_encode_pages_every_prompt(small_engine):
+    """Prompts of several lengths admitted in one step are encoded in one forward
+    (equal lengths as one attention batch): every prompt's paged K/V equals its own
+    encoder forward's kv_proj, and its pages come from the end of the free list group by
+    group in first-seen length order (model_runner.py:169-177, 208-259)."""
+    from vflorence_amd import SamplingParams, hip_attn
+    from vflorence_amd.engine.sequence import Sequence
+
+    llm = small_engine
+    runner, sched = llm.runner, llm.scheduler
+    params = SamplingParams(max_tokens=4).with_defaults(llm._sampling_params)
+    p = fixtures()["small"]["prompts"]
+    prompts = [p[1], p[3], p[0], p[1], p[5], p[3], p[4], p[1]]  # 17, 33, 5, 17, 100, ...
+    free_before = list(runner._cross_free)
+    with torch.inference_mode():
+        seqs = [Sequence(i, [2], q, params) for i, q in enumerate(prompts)]
+        for seq in seqs:
+            sched.add(seq)
+        batch = sched.schedule()
+        assert len(batch.fresh) == len(prompts)
+        runner._encode(batch.fresh)
+        torch.cuda.synchronize()
+        # pages: the groups (17 x3, 33 x2, 5, 100, 64) take the free list's tail in turn
+        free, want_pages = list(free_before), {}
+        for length in (17, 33, 5, 100, 64):
+            group = [s for s in seqs if len(s.encoder_token_ids) == length]
+            n = math.ceil(length / 16)
+            taken = free[-n * len(group):]
+            del free[-n * len(group):]
+            for j, seq in enumerate(group):
+                want_pages[seq.request_id] = taken[j * n: (j + 1) * n]
+        assert runner._cross_free == free
+        for layer in (runner.decoder_layers[0], runner.decoder_layers[-1]):
+            attn = layer.encoder_attn
+            for seq in seqs:
+                pages, enc_len = runner._cross_pages[seq.request_id]
+                assert pages.tolist() == want_pages[seq.request_id]
+                hidden = runner.model.encode(torch.tensor([seq.encoder_token_ids],
+                                                          device="cuda"))
+                k, v = attn.kv_proj(hidden)[0].chunk(2, dim=-1)
+                t = torch.arange(enc_len)
+                blk, off = pages[t // 16].long().cuda(), (t % 16).cuda()
+                kc = attn.k_cache[blk, :, off, :]
+                vc = hip_attn.v_cache_logical(attn.v_cache)[blk, :, off, :]
+                # one forward over 248 tokens against 17..100 at a time: the GEMMs'
+                # row counts differ, so fp32 rounding may too
+                torch.testing.assert_close(kc, k.view(enc_len, attn.num_heads, -1),
+                                           rtol=1e-5, atol=1e-5)
+                torch.testing.assert_close(vc, v.view(enc_len, attn.num_heads, -1),
+                                           rtol=1e-5, atol=1e-5)
+    llm.abort()
+    assert_clean(llm)
+
+
 def test_failed_step_releases_everything(small_engine):
     from vflorence_amd import Request, SamplingParams
 

@@ -546,3 +546,45 @@ def test_encoder_matches_transformers():
         want = hf.model.encoder(input_ids=ids).last_hidden_state
         got = mine.encode(ids)
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_packed_encoder_matches_transformers_per_prompt():
+    """Prompts of several lengths stored back to back and encoded in one forward
+    (attention per run of equal-length prompts) give each prompt transformers' encoder
+    output on its own; segments that leave a gap or miss tokens are refused."""
+    from transformers import BartConfig, BartForConditionalGeneration as HF
+
+    from vflorence_amd.layers.bart import BartForConditionalGeneration, fuse_projections
+    from vflorence_amd.utils.loader import synthetic_state_dict
+
+    cfg = BartConfig(vocab_size=60, d_model=128, encoder_layers=2, decoder_layers=1,
+                     encoder_attention_heads=2, decoder_attention_heads=2, encoder_ffn_dim=96,
+                     decoder_ffn_dim=96, max_position_embeddings=80, tie_word_embeddings=False)
+    sd = synthetic_state_dict(cfg, seed=5)
+    hf = HF(cfg).eval()
+    hf.load_state_dict(sd, strict=True)
+    mine = BartForConditionalGeneration(cfg).eval()
+    fused = dict(sd)
+    fuse_projections(mine, fused)
+    mine.load_state_dict(fused, strict=True)
+    g = torch.Generator().manual_seed(1)
+    # runs as the runner stores them: equal lengths adjacent, in first-seen order
+    runs = [(37, 2), (12, 2), (5, 1), (64, 1)]
+    prompts, segments, start = [], [], 0
+    for length, count in runs:
+        prompts += [torch.randint(3, 60, (length,), generator=g) for _ in range(count)]
+        segments.append((start, count, length))
+        start += count * length
+    ids = torch.cat(prompts)
+    positions = torch.cat([torch.arange(len(p)) for p in prompts])
+    with torch.no_grad():
+        got = mine.encode_packed(ids, positions, segments)
+        at = 0
+        for p in prompts:
+            want = hf.model.encoder(input_ids=p[None]).last_hidden_state[0]
+            torch.testing.assert_close(got[at: at + len(p)], want, rtol=1e-5, atol=1e-5)
+            at += len(p)
+        with pytest.raises(ValueError, match="does not start"):
+            mine.encode_packed(ids, positions, [(0, 2, 37), (80, 2, 12)])
+        with pytest.raises(ValueError, match="segments cover"):
+            mine.encode_packed(ids, positions, segments[:-1])

@@ -259,33 +259,46 @@ class ModelRunner:
         return pages
 
     def _encode(self, seqs) -> None:
-        """Encoder forward per group of equal prompt length, then page each layer's
-        cross-attention K/V (model_runner.py:208-259)."""
+        """Encode the step's admitted prompts and page each layer's cross-attention K/V
+        (model_runner.py:208-259).  The reference runs one encoder forward per group of
+        equal prompt length; here the groups' prompts are stored back to back and run as
+        one forward (projections, LayerNorms and feed-forward over all of the step's
+        tokens at once, attention per group), then one K/V scatter per layer covers every
+        token.  Pages are taken per group, in the reference's order."""
         groups = defaultdict(list)
         for seq in seqs:
             if seq.pixel_values is not None:
                 raise ValueError("pixel_values are only supported for Florence-2 checkpoints")
             groups[len(seq.encoder_token_ids)].append(seq)
+        if not groups:
+            return
         bs = self.block_size
+        ids, positions, slots, segments = [], [], [], []
+        start = 0
         for enc_len, group in groups.items():
-            ids = torch.tensor([s.encoder_token_ids for s in group], dtype=torch.long)
-            hidden = self.model.encode(ids.to(self.device, non_blocking=True))
             per_seq = math.ceil(enc_len / bs)
             pages = torch.tensor(self._allocate_cross_pages(len(group) * per_seq),
                                  dtype=torch.int32).view(len(group), per_seq)
-            token = torch.arange(enc_len)
-            slots = (pages[:, token // bs].long() * bs + token % bs).flatten()
             for seq, seq_pages in zip(group, pages):
                 self._cross_pages[seq.request_id] = (seq_pages, enc_len)
-            slots = slots.to(self.device, non_blocking=True)
-            rows = len(group) * enc_len
-            for layer in self.decoder_layers:
-                attn = layer.encoder_attn
-                kv = attn.kv_proj(hidden).view(rows, 2 * attn.embed_dim)
-                key, value = (t.view(rows, attn.num_heads, attn.head_dim)
-                              for t in kv.chunk(2, dim=-1))
-                attention.reshape_and_cache(key, value, attn.k_cache, attn.v_cache, slots,
-                                            isa=self.isa)
+            token = np.arange(enc_len)
+            slots.append((pages.numpy()[:, token // bs].astype(np.int64) * bs
+                          + token % bs).ravel())
+            ids.extend(np.asarray(s.encoder_token_ids, dtype=np.int64) for s in group)
+            positions.append(np.tile(token, len(group)))
+            segments.append((start, len(group), enc_len))
+            start += len(group) * enc_len
+        host = torch.from_numpy(np.concatenate([*ids, *positions, *slots]))
+        dev = host.to(self.device, non_blocking=True)
+        ids_d, pos_d, slots_d = dev[:start], dev[start: 2 * start], dev[2 * start:]
+        hidden = self.model.encode_packed(ids_d, pos_d, segments)
+        for layer in self.decoder_layers:
+            attn = layer.encoder_attn
+            kv = attn.kv_proj(hidden)
+            key, value = (t.view(start, attn.num_heads, attn.head_dim)
+                          for t in kv.chunk(2, dim=-1))
+            attention.reshape_and_cache(key, value, attn.k_cache, attn.v_cache, slots_d,
+                                        isa=self.isa)
 
     def clear_request(self, request_id: int) -> None:
         """Return a finished request's encoder pages; drop the staged cross state."""

@@ -262,12 +262,25 @@ class BartEncoderSelfAttention(_Heads):
         self.qkv_proj = nn.Linear(embed_dim, 3 * embed_dim)
         self.out_proj = nn.Linear(embed_dim, embed_dim)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        b, s, _ = x.shape
-        q, k, v = (t.view(b, s, self.num_heads, self.head_dim).transpose(1, 2)
-                   for t in self.qkv_proj(x).chunk(3, dim=-1))
-        out = F.scaled_dot_product_attention(q, k, v, scale=self.scaling)
-        return self.out_proj(out.transpose(1, 2).reshape(b, s, self.embed_dim))
+    def forward(self, x: torch.Tensor, segments=None) -> torch.Tensor:
+        """``x``: [B, S, d] equal-length prompts, or with ``segments`` the [T, d] tokens of
+        prompts stored back to back, where each ``(start, count, length)`` names ``count``
+        prompts of ``length`` tokens from token ``start`` on: the projections run over
+        all T tokens at once and attention per run of equal-length prompts."""
+        if segments is None:
+            b, s, _ = x.shape
+            q, k, v = (t.view(b, s, self.num_heads, self.head_dim).transpose(1, 2)
+                       for t in self.qkv_proj(x).chunk(3, dim=-1))
+            out = F.scaled_dot_product_attention(q, k, v, scale=self.scaling)
+            return self.out_proj(out.transpose(1, 2).reshape(b, s, self.embed_dim))
+        qkv = self.qkv_proj(x)
+        parts = []
+        for start, count, length in segments:
+            q, k, v = (t.view(count, length, self.num_heads, self.head_dim).transpose(1, 2)
+                       for t in qkv[start: start + count * length].chunk(3, dim=-1))
+            out = F.scaled_dot_product_attention(q, k, v, scale=self.scaling)
+            parts.append(out.transpose(1, 2).reshape(count * length, self.embed_dim))
+        return self.out_proj(parts[0] if len(parts) == 1 else torch.cat(parts))
 
 
 class BartDecoderSelfAttention(_Heads):
@@ -335,8 +348,8 @@ class BartEncoderLayer(nn.Module):
         self.fc2 = nn.Linear(config.encoder_ffn_dim, d)
         self.final_layer_norm = nn.LayerNorm(d)
 
-    def forward(self, h: torch.Tensor) -> torch.Tensor:
-        h = _residual_norm(h, self.self_attn(h), self.self_attn_layer_norm)
+    def forward(self, h: torch.Tensor, segments=None) -> torch.Tensor:
+        h = _residual_norm(h, self.self_attn(h, segments), self.self_attn_layer_norm)
         return _residual_norm(h, self.fc2(self.activation_fn(self.fc1(h))), self.final_layer_norm)
 
 
@@ -423,10 +436,10 @@ class BartEncoder(nn.Module):
         self.layers = nn.ModuleList(BartEncoderLayer(config) for _ in range(config.encoder_layers))
         self.layernorm_embedding = nn.LayerNorm(d)
 
-    def forward(self, input_ids, positions):
+    def forward(self, input_ids, positions, segments=None):
         h = self.layernorm_embedding(self.embed_tokens(input_ids) + self.embed_positions(positions))
         for layer in self.layers:
-            h = layer(h)
+            h = layer(h, segments)
         return h
 
 
@@ -500,6 +513,22 @@ class BartForConditionalGeneration(nn.Module):
         b, s = encoder_token_ids.shape
         positions = torch.arange(s, device=encoder_token_ids.device).expand(b, s)
         return self.model.encoder(encoder_token_ids, positions)
+
+    @torch.no_grad()
+    def encode_packed(self, token_ids: torch.Tensor, positions: torch.Tensor,
+                      segments) -> torch.Tensor:
+        """Encoder hidden states [T, d_model] of prompts of any lengths stored back to back
+        in ``token_ids`` / ``positions`` [T]; ``segments`` lists ``(start, count,
+        length)`` runs of equal-length prompts covering the T tokens in order."""
+        at = 0
+        for start, count, length in segments:
+            if start != at or count <= 0 or length <= 0:
+                raise ValueError(f"segment ({start}, {count}, {length}) does not start at "
+                                 f"token {at} or is empty")
+            at += count * length
+        if at != token_ids.shape[0] or positions.shape != token_ids.shape:
+            raise ValueError(f"segments cover {at} tokens of {token_ids.shape[0]}")
+        return self.model.encoder(token_ids, positions, segments)
 
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         """One decode step: logits [N, vocab] for one token per running sequence (the
