@@ -366,16 +366,20 @@ def random_candidates(rng, rows, k, vocab, eos_rate):
     return scores.astype(np.float32), ids.astype(np.int64)
 
 
-@pytest.mark.parametrize("beams,early,lp,seed", [
-    (1, False, 1.0, 0), (1, False, 1.0, 1), (4, False, 1.0, 2), (4, True, 1.0, 3),
-    (3, False, 2.0, 4), (4, False, -0.5, 5), (2, False, 1.0, 6), (8, False, 1.0, 7)])
-def test_host_core_equals_the_oracle_step_by_step(beams, early, lp, seed):
+@pytest.mark.parametrize("beams,early,lp,seed,shuffled", [
+    (1, False, 1.0, 0, False), (1, False, 1.0, 1, False), (4, False, 1.0, 2, False),
+    (4, True, 1.0, 3, False), (3, False, 2.0, 4, False), (4, False, -0.5, 5, False),
+    (2, False, 1.0, 6, False), (8, False, 1.0, 7, False), (4, False, 1.0, 8, True),
+    (3, True, 2.0, 9, True)])
+def test_host_core_equals_the_oracle_step_by_step(beams, early, lp, seed, shuffled):
     """Continuous batching with seeded arrivals, greedy or beam search with random
     candidates: every step the core admits the same requests, packs the reference's
     metadata formulas, makes the same copy-on-write pairs, leaves the same holder
     counts and free list (order included), the same running rows (tokens, tables,
     cumulative scores) and finishes the same requests with the same tokens as the
-    oracle's literal restatement."""
+    oracle's literal restatement.  ``shuffled``: each row's candidates come in a random
+    order on half the rows (the core's sorting path instead of its merge of best-first
+    rows)."""
     rng = np.random.default_rng(seed)
     bs, max_seqs, num_blocks = 16, 24, 200
     max_tokens = 40
@@ -441,6 +445,10 @@ def test_host_core_equals_the_oracle_step_by_step(beams, early, lp, seed):
             got, want = sched.postprocess(batch, toks), orc.greedy(toks)
         else:
             scores, ids = random_candidates(rng, n, keep, 60, 0.04)
+            if shuffled:
+                for r in np.flatnonzero(rng.random(n) < 0.5):
+                    perm = rng.permutation(keep)
+                    scores[r], ids[r] = scores[r][perm], ids[r][perm]
             got, want = sched.postprocess(batch, (scores, ids)), orc.beam(scores, ids)
         assert [(r, o.completion_token_ids) for r, o in got] == want
         rows = sched.running

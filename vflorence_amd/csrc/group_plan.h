@@ -188,14 +188,51 @@ inline int build_slot_descriptors(const int32_t *block_table, int64_t bt_stride,
   return 0;
 }
 
+// Destination block -> copy pair index, for fold_plan_copies: open addressing over a
+// power-of-two table at least twice the pairs, kept per thread so that a call
+// allocates only when a step brings more pairs than any before it.
+struct CopyDestinations {
+  std::vector<int64_t> key, pair;
+  int64_t mask = 0;
+
+  void reset(int64_t num_pairs) {
+    int64_t cap = 16;
+    while (cap < 2 * num_pairs) cap *= 2;
+    if ((int64_t)key.size() < cap) {
+      key.resize(cap);
+      pair.resize(cap);
+    }
+    mask = cap - 1;
+    std::fill(key.begin(), key.begin() + cap, -1);
+  }
+  int64_t slot_of(int64_t block) const {
+    int64_t h = (int64_t)(((uint64_t)block * 0x9E3779B97F4A7C15ull) >> 20) & mask;
+    while (key[h] != -1 && key[h] != block) h = (h + 1) & mask;
+    return h;
+  }
+  // false when block is a destination already
+  bool insert(int64_t block, int64_t i) {
+    const int64_t h = slot_of(block);
+    if (key[h] == block) return false;
+    key[h] = block;
+    pair[h] = i;
+    return true;
+  }
+  int64_t find(int64_t block) const {  // the pair index, or -1
+    if (block < 0) return -1;  // -1 marks a free table slot
+    const int64_t h = slot_of(block);
+    return key[h] == block ? pair[h] : -1;
+  }
+};
+
 // Fold a step's copy-on-write pairs (src[i] -> dst[i]) into its plan (the used slots
 // of build_group_plan's output): the entry holding block dst[i] gets the copy flag and
 // src[i] in place of dst[i].  Each destination must be a block in
 // [0, num_blocks) that exactly one entry of the plan holds, for one row, at that row's
 // last position (the fresh block a fork writes into), one per row; sources in
-// [0, num_blocks); no block both a destination and a source, no destination twice.  All pairs are checked before the
-// plan changes: on -1 (with *why set) the plan is as it was and the caller copies the
-// pairs itself.
+// [0, num_blocks); no block both a destination and a source, no destination twice.  All
+// pairs are checked before the plan changes: on -1 (with *why set) the plan is as it
+// was and the caller copies the pairs itself.
 inline int fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
                             const int64_t *src, const int64_t *dst, int64_t num_pairs,
                             int64_t num_blocks, const char **why) {
@@ -211,93 +248,82 @@ inline int fold_plan_copies(int32_t *plan, int64_t num_slots, int64_t stride,
     *why = "plan slot count out of range";
     return -1;
   }
-  // destinations sorted with their pair index, for a binary search per entry
-  std::vector<int64_t> order(num_pairs);
-  std::vector<int32_t *> where(num_pairs, nullptr);  // the destination's entry
-  for (int64_t i = 0; i < num_pairs; ++i) order[i] = i;
-  std::sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return dst[a] < dst[b]; });
-  int rc = 0;
-  for (int64_t i = 0; i < num_pairs && rc == 0; ++i) {
-    const int64_t s = src[order[i]], d = dst[order[i]];
-    if (s < 0 || s >= num_blocks || d < 0 || d >= num_blocks) {
+  for (int64_t i = 0; i < num_pairs; ++i)
+    if (src[i] < 0 || src[i] >= num_blocks || dst[i] < 0 || dst[i] >= num_blocks) {
       *why = "copy pair block out of range";
-      rc = -1;
-    } else if (i > 0 && dst[order[i - 1]] == d) {
+      return -1;
+    }
+  static thread_local CopyDestinations dests;
+  dests.reset(num_pairs);
+  for (int64_t i = 0; i < num_pairs; ++i)
+    if (!dests.insert(dst[i], i)) {
       *why = "a block is the destination of two copies";
-      rc = -1;
+      return -1;
     }
-  }
-  for (int64_t i = 0; i < num_pairs && rc == 0; ++i) {  // no source is also a destination
-    int64_t lo = 0, hi = num_pairs;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) / 2;
-      if (dst[order[mid]] < src[i]) lo = mid + 1; else hi = mid;
-    }
-    if (lo < num_pairs && dst[order[lo]] == src[i]) {
+  for (int64_t i = 0; i < num_pairs; ++i)
+    if (dests.find(src[i]) >= 0) {
       *why = "a block is both a copy source and a destination";
-      rc = -1;
+      return -1;
     }
-  }
-  for (int64_t s = 0; s < used && rc == 0; ++s) {
+  static thread_local std::vector<int32_t *> where;  // each pair's destination entry
+  where.assign(num_pairs, nullptr);
+  for (int64_t s = 0; s < used; ++s) {
     int32_t *rec = plan + PLAN_PREFIX + s * stride;
     const int64_t ne = rec[2];
     if (ne < 0 || PLAN_HEADER + ne * PLAN_ENTRY > stride) {
       *why = "plan slot entry count out of range";
-      rc = -1;
-      break;
+      return -1;
     }
-    // each row's last position in the slot: a destination must be there (it is the block
-    // the row's new token goes to, where the fused launch stores the copy)
+    // each row's last position in the slot (a destination must be there: it is the block
+    // the row's new token goes to, where the fused launch stores the copy), found once a
+    // slot holds a destination
     int32_t last_pos[PLAN_MAX_ROWS];
-    for (int c = 0; c < PLAN_MAX_ROWS; ++c) last_pos[c] = -1;
-    for (int64_t e = 0; e < ne; ++e) {
-      const uint32_t meta = (uint32_t)rec[PLAN_HEADER + PLAN_ENTRY * e + 1];
-      const int32_t pos = (int32_t)((meta >> 16) & 0x7fffu);
-      for (int c = 0; c < PLAN_MAX_ROWS; ++c)
-        if ((meta >> c) & 1u) last_pos[c] = std::max(last_pos[c], pos);
-    }
+    bool have_last = false;
     uint32_t taken = 0;  // rows of the slot that received a copy source
     for (int64_t e = 0; e < ne; ++e) {
       int32_t *ent = rec + PLAN_HEADER + PLAN_ENTRY * e;
-      int64_t lo = 0, hi = num_pairs;
-      while (lo < hi) {
-        const int64_t mid = (lo + hi) / 2;
-        if (dst[order[mid]] < ent[0]) lo = mid + 1; else hi = mid;
-      }
-      if (lo == num_pairs || dst[order[lo]] != ent[0]) continue;
+      const int64_t i = dests.find(ent[0]);
+      if (i < 0) continue;
       const uint32_t rows = (uint32_t)ent[1] & 0xffu;
-      if (where[order[lo]] != nullptr || rows == 0 || (rows & (rows - 1u)) != 0) {
+      if (where[i] != nullptr || rows == 0 || (rows & (rows - 1u)) != 0) {
         *why = "a copy destination is listed by several rows or entries";
-        rc = -1;
-        break;
+        return -1;
       }
-      int c = 0;
-      while (!((rows >> c) & 1u)) ++c;
+      const int c = __builtin_ctz(rows);
       if ((taken >> c) & 1u) {
         *why = "a row has two copy destinations";
-        rc = -1;
-        break;
+        return -1;
+      }
+      if (!have_last) {
+        for (int r = 0; r < PLAN_MAX_ROWS; ++r) last_pos[r] = -1;
+        for (int64_t f = 0; f < ne; ++f) {
+          const uint32_t meta = (uint32_t)rec[PLAN_HEADER + PLAN_ENTRY * f + 1];
+          const int32_t pos = (int32_t)((meta >> 16) & 0x7fffu);
+          for (uint32_t m = meta & 0xffu; m; m &= m - 1u) {
+            const int r = __builtin_ctz(m);
+            last_pos[r] = std::max(last_pos[r], pos);
+          }
+        }
+        have_last = true;
       }
       if ((int32_t)(((uint32_t)ent[1] >> 16) & 0x7fffu) != last_pos[c]) {
         *why = "a copy destination is not its row's last block";
-        rc = -1;
-        break;
+        return -1;
       }
       taken |= 1u << c;
-      where[order[lo]] = ent;
+      where[i] = ent;
     }
   }
-  for (int64_t i = 0; i < num_pairs && rc == 0; ++i)
+  for (int64_t i = 0; i < num_pairs; ++i)
     if (where[i] == nullptr) {
       *why = "a copy destination is not a block of the plan";
-      rc = -1;
+      return -1;
     }
-  if (rc == 0)
-    for (int64_t i = 0; i < num_pairs; ++i) {
-      where[i][0] = (int32_t)src[i];
-      where[i][1] = (int32_t)((uint32_t)where[i][1] | PLAN_COPY);
-    }
-  return rc;
+  for (int64_t i = 0; i < num_pairs; ++i) {
+    where[i][0] = (int32_t)src[i];
+    where[i][1] = (int32_t)((uint32_t)where[i][1] | PLAN_COPY);
+  }
+  return 0;
 }
 
 }  // namespace vfl

@@ -152,6 +152,12 @@ struct Finished {
   std::vector<int32_t> completion;
 };
 
+struct BeamCand {  // a continuation: cumulative log-prob, parent row, token
+  float value;
+  int32_t row;
+  int32_t token;
+};
+
 }  // namespace
 
 struct vfl_engine {
@@ -166,6 +172,34 @@ struct vfl_engine {
   bool scheduled = false;
   std::vector<uint32_t> req_stamp;
   uint32_t req_epoch = 0;
+  // beam_update's working storage, kept across steps so that a step allocates nothing
+  // once the batch has reached its size: candidates, the rows being built, and token
+  // and table vectors (emptied, capacity kept) that the last step's parents left
+  std::vector<BeamCand> cands;
+  std::vector<std::pair<int32_t, BeamCand>> live;  // (parent row, candidate)
+  std::vector<Row> next_rows;
+  std::vector<std::vector<int32_t>> spare_tokens, spare_tables;
+  std::vector<int32_t> handed;      // parent row -> index in next_rows of its first child
+  std::vector<uint8_t> has_child;   // parent row -> a live child takes it
+
+  // An emptied vector from `spares` (capacity kept), or a new one.
+  static std::vector<int32_t> take_spare(std::vector<std::vector<int32_t>> &spares) {
+    if (spares.empty()) return {};
+    std::vector<int32_t> v = std::move(spares.back());
+    spares.pop_back();
+    return v;
+  }
+  // A row's storage back to the spares (at most one spare per row a batch can hold).
+  void recycle(Row &r) {
+    if (r.tokens.capacity() && (int32_t)spare_tokens.size() < max_num_seqs) {
+      r.tokens.clear();
+      spare_tokens.push_back(std::move(r.tokens));
+    }
+    if (r.table.capacity() && (int32_t)spare_tables.size() < max_num_seqs) {
+      r.table.clear();
+      spare_tables.push_back(std::move(r.table));
+    }
+  }
 
   vfl_engine(int32_t nb, int32_t bs, int32_t mns) : pool(nb, bs), max_num_seqs(mns) {}
 
@@ -518,18 +552,16 @@ int vfl_engine_beam_update(vfl_engine *e, const float *scores, const int64_t *id
   e->scheduled = false;
   for (Row &r : e->running) r.cached += 1;
 
-  struct Cand {
-    float value;
-    int32_t row;
-    int32_t token;
-  };
-  std::vector<Cand> cands, merged;
-  std::vector<Row> next;
+  using Cand = BeamCand;
+  std::vector<Cand> &cands = e->cands;
+  std::vector<Row> &next = e->next_rows;
+  next.clear();
   next.reserve(e->running.size());
-  std::vector<std::pair<int32_t, Cand>> live;  // (parent row, candidate)
-  std::vector<int32_t> handed;                 // parent row -> index in next of its owner
+  std::vector<std::pair<int32_t, Cand>> &live = e->live;
+  std::vector<int32_t> &handed = e->handed;
   handed.assign(rows, -1);
-  std::vector<uint8_t> has_child(rows, 0);     // parent row -> a live child takes it
+  std::vector<uint8_t> &has_child = e->has_child;
+  has_child.assign(rows, 0);
 
   int32_t i = 0;
   while (i < rows) {  // a request's rows are adjacent
@@ -539,33 +571,45 @@ int vfl_engine_beam_update(vfl_engine *e, const float *scores, const int64_t *id
     Request &q = e->requests[slot];
     const int32_t nb = q.num_beams;
     const int32_t keep = std::max<int32_t>(2, 1 + (int32_t)q.eos.size()) * nb;
-    cands.clear();
-    bool rows_sorted = true;
-    for (int32_t r = i; r < j; ++r) {
+    // Best first, ties in row-major order (a stable sort).  When each row's list is best
+    // first (the device top-k's order), the best `keep` come from merging the rows'
+    // lists head by head, reading the scores in place (on a tie the lower row first);
+    // otherwise every candidate goes through an insertion sort, with no temporary buffer.
+    const int32_t nr = j - i;
+    bool rows_sorted = nr <= 16;
+    for (int32_t r = i; r < j && rows_sorted; ++r) {
       const float cum = (float)e->running[r].cum;
-      for (int32_t c = 0; c < k; ++c) {
-        const float v = scores[(int64_t)r * k + c] + cum;
-        if (c > 0 && !(cands.back().value >= v)) rows_sorted = false;
-        cands.push_back({v, r, (int32_t)ids[(int64_t)r * k + c]});
-      }
+      const float *sr = scores + (int64_t)r * k;
+      for (int32_t c = 1; c < k; ++c)
+        if (!(sr[c - 1] + cum >= sr[c] + cum)) {
+          rows_sorted = false;
+          break;
+        }
     }
-    // Best first, ties in row-major order (a stable sort).  Each row's list is best
-    // first already, so the best `keep` come from merging the rows' lists (on a tie the
-    // lower row first); otherwise an insertion sort, with no temporary buffer.
-    const int32_t nr = j - i, take = std::min<int32_t>(keep, (int32_t)cands.size());
-    if (rows_sorted && nr <= 16) {
-      int32_t at[16] = {0};
-      merged.clear();
+    cands.clear();
+    if (rows_sorted) {
+      const int32_t take = (int32_t)std::min<int64_t>(keep, (int64_t)nr * k);
+      int32_t at[16];
+      float head[16], cumf[16];
+      for (int32_t r = 0; r < nr; ++r) {
+        at[r] = 0;
+        cumf[r] = (float)e->running[i + r].cum;
+        head[r] = scores[(int64_t)(i + r) * k] + cumf[r];
+      }
       for (int32_t t = 0; t < take; ++t) {
         int32_t best = -1;
         for (int32_t r = 0; r < nr; ++r)
-          if (at[r] < k && (best < 0 || cands[r * k + at[r]].value > cands[best * k + at[best]].value))
-            best = r;
-        merged.push_back(cands[best * k + at[best]]);
-        ++at[best];
+          if (at[r] < k && (best < 0 || head[r] > head[best])) best = r;
+        const int64_t c = (int64_t)(i + best) * k + at[best];
+        cands.push_back({head[best], i + best, (int32_t)ids[c]});
+        if (++at[best] < k) head[best] = scores[c + 1] + cumf[best];
       }
-      cands.swap(merged);
     } else {
+      for (int32_t r = i; r < j; ++r) {
+        const float cum = (float)e->running[r].cum;
+        for (int32_t c = 0; c < k; ++c)
+          cands.push_back({scores[(int64_t)r * k + c] + cum, r, (int32_t)ids[(int64_t)r * k + c]});
+      }
       for (size_t a = 1; a < cands.size(); ++a) {
         const Cand c = cands[a];
         size_t b = a;
@@ -652,11 +696,14 @@ int vfl_engine_beam_update(vfl_engine *e, const float *scores, const int64_t *id
             child.tokens = std::move(e->running[spare].tokens);
             e->running[spare].tokens.clear();
             ++spare;
+          } else {
+            child.tokens = vfl_engine::take_spare(e->spare_tokens);
           }
           const Row &first = next[handed[p]];
           child.tokens.assign(first.tokens.begin(), first.tokens.end());
           child.tokens.back() = l.second.token;
-          child.table = first.table;
+          child.table = vfl_engine::take_spare(e->spare_tables);
+          child.table.assign(first.table.begin(), first.table.end());
           e->pool.share(child.table.data(), (int32_t)child.table.size());
         }
         next.push_back(std::move(child));
@@ -664,9 +711,12 @@ int vfl_engine_beam_update(vfl_engine *e, const float *scores, const int64_t *id
     }
     i = j;
   }
-  // every parent leaves, in row order (tables handed to a child are empty by now)
+  // every parent leaves, in row order (tables handed to a child are empty by now), and
+  // leaves its storage for the next step's children
   for (Row &r : e->running) e->pool.release(r.table.data(), (int32_t)r.table.size());
   e->running.swap(next);
+  for (Row &r : next) e->recycle(r);
+  next.clear();
   return VFL_HOST_OK;
 }
 
