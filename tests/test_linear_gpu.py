@@ -244,3 +244,53 @@ def test_linear_rejects_bad_flags_and_packed_shapes():
     w_odd = torch.zeros(100, 256, device=DEV, dtype=torch.bfloat16)
     with pytest.raises(HipAttnError, match="packed output"):
         o.linear(x, o.pack_linear_weight(w_odd), None, 100, flags=o.LINEAR_Y_PACKED)
+
+
+@pytest.mark.parametrize("vocab,tied", [(50265, False), (1000, True), (1024, False)])
+def test_lm_head_runs_on_padded_operands(vocab, tied):
+    """The LM head multiplies copies of its weight and the final logits bias padded with
+    zero rows to a multiple of 256 outputs: the logits are the first ``vocab`` columns
+    (row stride the padded width), within one rounding of the float64 product; the
+    copies follow an in-place update on the next eager call, a tied head follows the
+    shared embedding, and an inference-mode weight follows after ``repack_lm_head``."""
+    from transformers import BartConfig
+
+    from vflorence_amd.layers.bart import LM_HEAD_MULTIPLE, BartForConditionalGeneration
+
+    cfg = BartConfig(vocab_size=vocab, d_model=256, encoder_layers=1, decoder_layers=1,
+                     encoder_attention_heads=4, decoder_attention_heads=4, encoder_ffn_dim=256,
+                     decoder_ffn_dim=256, max_position_embeddings=64, tie_word_embeddings=tied)
+    with torch.device(DEV):
+        model = BartForConditionalGeneration(cfg).to(torch.bfloat16)
+    torch.manual_seed(3)
+    with torch.no_grad():
+        model.lm_head.weight.normal_(0, 0.05)
+        model.final_logits_bias.normal_()
+    model.repack_lm_head()
+    padded = -(-vocab // LM_HEAD_MULTIPLE) * LM_HEAD_MULTIPLE
+    h = torch.randn(37, 256, device=DEV).to(torch.bfloat16)
+    got = model.logits(h)
+    assert got.shape == (37, vocab) and got.stride(1) == 1
+    if padded != vocab:
+        assert got.stride(0) == padded and model._lm_padded[0].shape == (padded, 256)
+        assert not model._lm_padded[0][vocab:].any() and not model._lm_padded[1][vocab:].any()
+    else:
+        assert model._lm_padded is None
+    w, b = model.lm_head.weight, model.final_logits_bias[0]
+    assert_one_rounding(got, reference(h, w, b), torch.bfloat16)
+    with torch.no_grad():
+        (model.model.shared.weight if tied else model.lm_head.weight).mul_(-1)
+    assert_one_rounding(model.logits(h), reference(h, w, b), torch.bfloat16)
+    with torch.inference_mode():
+        with torch.device(DEV):
+            inf = BartForConditionalGeneration(cfg).to(torch.bfloat16)
+        inf.lm_head.weight.copy_(w)
+        inf.final_logits_bias.copy_(model.final_logits_bias)
+        inf.repack_lm_head()
+        before = inf.logits(h).clone()
+        inf.lm_head.weight.mul_(0.5)
+        inf.repack_lm_head()
+        after = inf.logits(h)
+        assert not torch.equal(before, after)
+        assert_one_rounding(after, reference(h, inf.lm_head.weight, inf.final_logits_bias[0]),
+                            torch.bfloat16)

@@ -207,9 +207,9 @@ class ModelRunner:
                           else self.model)
 
     def repack_weights(self) -> None:
-        """Make the decoder's packed projection weights follow the current weights, after
-        an in-place weight update (the copies are rewritten in place, so captured decode
-        steps stay valid)."""
+        """Make the decoder's packed projection weights and the LM head's padded operands
+        follow the current weights, after an in-place weight update (the copies are
+        rewritten in place, so captured decode steps stay valid)."""
         from ..utils.loader import repack_decode_weights
 
         repack_decode_weights(self.model)

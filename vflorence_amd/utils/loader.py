@@ -149,10 +149,13 @@ def load_model(config, state_dict: dict | None = None):
 
 
 def repack_decode_weights(model) -> None:
-    """Refresh every decode-step projection's packed weight copy in place (after loading
-    or updating weights; captured HIP graphs read the refreshed copies)."""
+    """Refresh every decode-step projection's packed weight copy and the LM head's
+    padded operands in place (after loading or updating weights; captured HIP graphs
+    read the refreshed copies)."""
     from ..layers.bart import DecodeLinear
 
     for module in model.modules():
         if isinstance(module, DecodeLinear):
             module.repack()
+    if hasattr(model, "repack_lm_head"):
+        model.repack_lm_head()
