@@ -111,8 +111,10 @@ def test_decoder_projections_use_the_kernel_where_it_fits():
     with torch.no_grad():
         lin.weight.mul_(-1)
     assert torch.equal(lin(x), run(x, lin.weight, lin.bias))
-    assert ops().linear_fits(256, lin.weight) and not ops().linear_fits(257, lin.weight)
-    xl = torch.randn(300, 1024, device=DEV).to(torch.bfloat16)
+    assert ops().linear_fits(512, lin.weight) and not ops().linear_fits(513, lin.weight)
+    xm = torch.randn(300, 1024, device=DEV).to(torch.bfloat16)
+    assert torch.equal(lin(xm), run(xm, lin.weight, lin.bias))
+    xl = torch.randn(600, 1024, device=DEV).to(torch.bfloat16)
     assert torch.equal(lin(xl), F.linear(xl, lin.weight, lin.bias))
     wide = DecodeLinear(1024, 4096).to(DEV, torch.bfloat16)
     assert not ops().linear_fits(8, wide.weight)
@@ -223,8 +225,8 @@ def test_decoder_feed_forward_matches_the_torch_ops():
     want = F.linear(F.gelu(F.linear(h, layer.fc1.weight, layer.fc1.bias)), layer.fc2.weight,
                     layer.fc2.bias)
     torch.testing.assert_close(got.float(), want.float(), rtol=2e-2, atol=2e-2)
-    # more rows than a decode step: the torch ops themselves
-    hl = torch.randn(300, 1024, device=DEV).to(torch.bfloat16)
+    # more rows than a decode step (over 512): the torch ops themselves
+    hl = torch.randn(600, 1024, device=DEV).to(torch.bfloat16)
     wantl = F.linear(F.gelu(F.linear(hl, layer.fc1.weight, layer.fc1.bias)), layer.fc2.weight,
                      layer.fc2.bias)
     assert torch.equal(layer._feed_forward(hl), wantl)

@@ -32,7 +32,14 @@ MAX_K = 16
 LINEAR_K_MULTIPLE = 256
 LINEAR_MAX_IN = 4096
 LINEAR_MAX_OUT = 3072
-LINEAR_MAX_ROWS = 256
+# Up to 512 rows (continuous batching's larger steps, Florence-2 beam batches), timed the
+# same way: at 320 / 384 / 448 / 512 rows a 1024 x 1024 projection 6.3-6.9 against
+# 10.8-11.1 us, fc2's shape 12.7-14.9 against 15.3-15.9 us; q|k|v 11.0 / 12.2 / 14.1 /
+# 14.7 against 11.9 / 12.9 / 12.9 / 12.9 us and fc1 + GELU 14.7-20.1 against 12.7-13.2
+# us plus the separate GELU.  With every projection of a layer on the kernel its
+# LayerNorms stay deferred (three launches fewer per layer), which outweighs the q|k|v
+# and fc1 shortfall at 448-512 rows.
+LINEAR_MAX_ROWS = 512
 
 
 @torch.library.custom_op("vflorence_amd::add_layer_norm", mutates_args=())
@@ -67,7 +74,7 @@ def _(x, residual, weight, bias, eps):
 def linear_fits(rows: int, weight: torch.Tensor, *, max_in: int | None = LINEAR_MAX_IN,
                 max_out: int | None = LINEAR_MAX_OUT) -> bool:
     """Whether ``linear`` serves ``rows`` rows times ``weight``: a contiguous, 16-byte
-    aligned 16-bit device weight, in_features a multiple of 256, at most 256 rows, and
+    aligned 16-bit device weight, in_features a multiple of 256, at most 512 rows, and
     in / out features within ``max_in`` / ``max_out`` (None: no bound; the defaults are
     where a lone projection beats hipBLASLt -- the feed-forward pair, which fuses its
     activation, lifts them)."""

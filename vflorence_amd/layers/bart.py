@@ -63,7 +63,7 @@ def apply_pre_norm(h: "PreNorm | torch.Tensor") -> torch.Tensor:
 
 
 class DecodeLinear(nn.Linear):
-    """nn.Linear whose decode-step calls -- at most 256 rows on the GPU times a 16-bit
+    """nn.Linear whose decode-step calls -- at most 512 rows on the GPU times a 16-bit
     weight of up to 3072 outputs and 4096 inputs -- run on the split-K kernel
     (vflorence_amd::linear) with a copy of the weight re-laid out for it; other shapes,
     fp32 and host tensors go through F.linear (hipBLASLt on the GPU).
