@@ -596,3 +596,48 @@ def test_packed_encoder_matches_transformers_per_prompt():
             mine.encode_packed(ids, positions, [(0, 2, 37), (80, 2, 12)])
         with pytest.raises(ValueError, match="segments cover"):
             mine.encode_packed(ids, positions, segments[:-1])
+
+
+def test_request_runs_are_the_page_comparison_groups():
+    """The runner's cross-attention groups from the rows' request ids equal
+    ``beam_groups``' runs of rows sharing encoder pages (cut at 8 rows), padding rows
+    included, over random batches of 1-12 beams per request."""
+    from vflorence_amd.engine.model_runner import request_runs
+    from vflorence_amd.layers.attention import beam_groups
+
+    rng = np.random.default_rng(7)
+    empty = torch.zeros(0, dtype=torch.int32)
+    for _ in range(200):
+        rows, pages, lens, page = [], [], [], 0
+        for rid in rng.permutation(40)[: int(rng.integers(1, 12))]:
+            beams, length = int(rng.integers(1, 13)), int(rng.integers(1, 300))
+            mine = torch.arange(page, page + -(-length // 16), dtype=torch.int32)
+            page += len(mine)
+            rows += [int(rid)] * beams
+            pages += [mine] * beams
+            lens += [length] * beams
+        n = len(rows)
+        padded = n + int(rng.integers(0, 20))
+        want = beam_groups(pages + [empty] * (padded - n), lens + [0] * (padded - n))
+        assert request_runs(np.asarray(rows, np.int64), padded, 8) == want
+
+
+def test_page_table_fill_matches_row_by_row():
+    """The staging's one-scatter page table equals filling it row by row, zero-padded,
+    for tensors, numpy arrays and rows repeating one object; rows past the batch keep
+    what they held."""
+    from vflorence_amd.layers.attention import _fill_page_table
+
+    rng = np.random.default_rng(3)
+    table = rng.integers(1, 9, (40, 12)).astype(np.int32)
+    before = table.copy()
+    shared = torch.tensor([5, 6, 7], dtype=torch.int32)
+    pages = [shared, shared, np.array([1, 2], np.int32), torch.zeros(0, dtype=torch.int32),
+             np.arange(12, dtype=np.int32), [3, 4, 9]]
+    _fill_page_table(table, pages)
+    for i, p in enumerate(pages):
+        p = np.asarray(p.numpy() if isinstance(p, torch.Tensor) else p)
+        assert table[i, : len(p)].tolist() == p.tolist() and not table[i, len(p):].any()
+    assert (table[len(pages):] == before[len(pages):]).all()
+    _fill_page_table(table, [torch.zeros(0, dtype=torch.int32)] * 3)
+    assert not table[:3].any()

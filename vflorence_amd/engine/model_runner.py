@@ -149,6 +149,24 @@ def launch_slots(padded: int, below: int, beams: int, max_group: int) -> int:
     return most or padded
 
 
+def request_runs(row_requests: np.ndarray, padded: int, max_group: int) -> list[int]:
+    """Group starts of a step's rows for the cross-attention staging: each run of rows
+    of one request (beams are adjacent, scheduler.py:121-126; they read the same encoder
+    pages) cut every ``max_group`` rows, then the padding rows up to ``padded`` in
+    groups of ``max_group`` -- what ``attention.beam_groups`` finds by comparing the
+    rows' pages.  Returns ``[0, ..., padded]``."""
+    n = len(row_requests)
+    starts = []
+    if n:
+        cuts = np.flatnonzero(row_requests[1:] != row_requests[:-1]) + 1
+        bounds = [0, *cuts.tolist(), n]
+        for a, b in zip(bounds, bounds[1:]):
+            starts.extend(range(a, b, max_group))
+    starts.extend(range(n, padded, max_group))
+    starts.append(padded)
+    return starts
+
+
 def row_buckets(max_rows: int) -> list[int]:
     """Row counts a decode step is padded to: 1, 2, 4, 8, then steps of 8 up to 64, of 16
     up to 128, of 32 beyond, and ``max_rows`` itself.  A HIP graph is captured once per
@@ -177,6 +195,7 @@ class ModelRunner:
         self.isa = hip_attn.get_isa(self.dtype, self.block_size, self.head_dim)
         self.vocab_size = self.model.lm_head.out_features
         self._cross_pages: dict[int, tuple[torch.Tensor, int]] = {}
+        self._cross_np: dict[int, np.ndarray] = {}  # the same pages as int32 numpy arrays
         self._cross_free = list(range(config.num_cross_blocks))
         self._cross_key = None
         self._cross_staged = None
@@ -200,6 +219,7 @@ class ModelRunner:
         self._step_slots = 0
         self.step_rows = self.step_pairs = 0
         self._no_pages = torch.zeros(0, dtype=torch.int32)
+        self._no_pages_np = self._no_pages.numpy()
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
         # the decoder step; compiled as the reference compiles it when asked
         # (vflorence/engine/model_runner.py:121-123)
@@ -281,6 +301,7 @@ class ModelRunner:
                                  dtype=torch.int32).view(len(group), per_seq)
             for seq, seq_pages in zip(group, pages):
                 self._cross_pages[seq.request_id] = (seq_pages, enc_len)
+                self._cross_np[seq.request_id] = seq_pages.numpy()
             token = np.arange(enc_len)
             slots.append((pages.numpy()[:, token // bs].astype(np.int64) * bs
                           + token % bs).ravel())
@@ -303,12 +324,14 @@ class ModelRunner:
     def clear_request(self, request_id: int) -> None:
         """Return a finished request's encoder pages; drop the staged cross state."""
         pages, _ = self._cross_pages.pop(request_id, ((), 0))
+        self._cross_np.pop(request_id, None)
         self._cross_free.extend(int(p) for p in pages)
         self._cross_key = self._cross_staged = None
 
     def reset(self) -> None:
         """Return every encoder page to the pool (after an aborted batch)."""
         self._cross_pages.clear()
+        self._cross_np.clear()
         self._cross_free = list(range(self.config.num_cross_blocks))
         self._cross_key = self._cross_staged = None
 
@@ -384,12 +407,12 @@ class ModelRunner:
         key = (padded, rows.tobytes())
         if key != self._cross_key:
             request_ids = rows.tolist()
-            pages, enc_lens = zip(*(self._cross_pages[rid] for rid in request_ids))
-            pages = pages + (self._no_pages,) * (padded - n)
-            enc_lens = enc_lens + (0,) * (padded - n)
-            self._cross_staged = attention.stage_cross(self.decoder_layers, pages, enc_lens, bs,
-                                                       self.isa, buffers=self._cross_buffers,
-                                                       slots=slots)
+            pages = [self._cross_np[rid] for rid in request_ids]
+            pages += [self._no_pages_np] * (padded - n)
+            enc_lens = [self._cross_pages[rid][1] for rid in request_ids] + [0] * (padded - n)
+            self._cross_staged = attention.stage_cross(
+                self.decoder_layers, pages, enc_lens, bs, self.isa, buffers=self._cross_buffers,
+                slots=slots, group_starts=request_runs(rows, padded, hip_attn.MAX_GROUP_SIZE))
             self._cross_key = key
         set_context(
             context_lens=d["context_lens"][:padded],

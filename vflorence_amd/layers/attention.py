@@ -11,6 +11,7 @@ the CPU.
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from .. import hip_attn
@@ -95,21 +96,45 @@ def _stage_into(buffers: CrossStagingBuffers, pages, enc_lens, starts, run, slot
     h[o[2] + ng: o[2] + n] = -1  # their workgroups exit at once
     table = h[o[3]: o[3] + buffers.max_rows * buffers.max_pages].reshape(
         buffers.max_rows, buffers.max_pages)
-    for i, p in enumerate(pages):
-        table[i, : len(p)] = p.numpy() if isinstance(p, torch.Tensor) else p
-        table[i, len(p):] = 0
+    _fill_page_table(table, pages)
     base = buffers.host.data_ptr()
+    g = n if slots is None else slots
     check(lib.vfl_build_slot_descriptors(
         base + 4 * o[3], buffers.max_pages, buffers.max_pages, base + 4 * o[0], n,
-        base + 4 * o[1], base + 4 * o[2], ng, base + 4 * o[4], n if slots is None else slots,
-        buffers.desc_stride))
-    buffers.dev.copy_(buffers.host, non_blocking=True)
+        base + 4 * o[1], base + 4 * o[2], ng, base + 4 * o[4], g, buffers.desc_stride))
+    # the parts the launches read: lengths, starts, order and the n table rows, then the
+    # g slot descriptors
+    end, d0, d1 = o[3] + n * buffers.max_pages, o[4], o[4] + g * buffers.desc_stride
+    buffers.dev[:end].copy_(buffers.host[:end], non_blocking=True)
+    buffers.dev[d0:d1].copy_(buffers.host[d0:d1], non_blocking=True)
     buffers.copied.record()
     return buffers.views(n, slots)
 
 
+def _fill_page_table(table: np.ndarray, pages) -> None:
+    """Rows 0 .. len(pages) - 1 of ``table`` hold each row's pages, zero-padded: one
+    scatter of all rows' pages (a row list that repeats one page array or tensor per
+    beam converts it once)."""
+    n = len(pages)
+    arrays, seen = [], {}
+    for p in pages:
+        a = seen.get(id(p))
+        if a is None:
+            a = p if isinstance(p, np.ndarray) else (
+                p.numpy() if isinstance(p, torch.Tensor) else np.asarray(p, dtype=np.int32))
+            seen[id(p)] = a
+        arrays.append(a)
+    counts = np.fromiter(map(len, arrays), dtype=np.int64, count=n)
+    table[:n] = 0
+    total = int(counts.sum())
+    if total:
+        rows = np.repeat(np.arange(n), counts)
+        cols = np.arange(total) - np.repeat(np.cumsum(counts) - counts, counts)
+        table[rows, cols] = np.concatenate(arrays)
+
+
 def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=None,
-                slots=None):
+                slots=None, group_starts=None):
     """Point this step's sequences at their encoder K/V pages in each layer's pool.
 
     ``pages[i]`` (int32 tensor) and ``enc_lens[i]`` belong to running sequence i; beams
@@ -118,11 +143,25 @@ def stage_cross(layers, pages, enc_lens, block_size: int, isa: str, *, buffers=N
     With ``buffers`` (a ``CrossStagingBuffers``) they go to its fixed addresses
     instead of a fresh allocation, with ``slots`` launch slots (one per row when not
     given, or when the rows form more groups than that), the unused ones exiting at
-    once.
+    once.  With ``buffers``, ``pages[i]`` may also be an int32 numpy array, and a caller
+    that knows the rows' requests passes ``group_starts`` (``beam_groups``' result for
+    these rows: runs of rows sharing pages, cut at 8) instead of having the pages
+    compared.
     """
     attn = layers[0].encoder_attn
     device = attn.k_cache.device
-    starts = beam_groups(pages, enc_lens)
+    if group_starts is not None and buffers is None:
+        raise ValueError("group_starts is for staging into CrossStagingBuffers")
+    if group_starts is None:
+        starts = beam_groups(pages, enc_lens)
+    else:
+        gs = np.asarray(group_starts, dtype=np.int64)
+        steps = np.diff(gs)
+        if (gs.ndim != 1 or gs.size < 2 or gs[0] != 0 or gs[-1] != len(pages)
+                or (steps <= 0).any() or (steps > hip_attn.MAX_GROUP_SIZE).any()):
+            raise ValueError(f"group_starts must rise from 0 to {len(pages)} in runs of 1 to "
+                             f"{hip_attn.MAX_GROUP_SIZE} rows")
+        starts = gs.tolist()
     max_group = max(b - a for a, b in zip(starts, starts[1:]))
     n, ng = len(pages), len(starts) - 1
     # every (group, head) workgroup is resident at once: balance long and short groups
