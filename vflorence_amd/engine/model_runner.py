@@ -39,6 +39,7 @@ from ..layers.logits_processor import LogitsProcessor
 from ..sampling_params import SamplingParams
 from ..utils.context import set_context
 from ..utils.loader import load_model
+from .encoder_graphs import EncoderGraphs, page_cross_kv
 from .._lib import check, lib
 
 logger = logging.getLogger(__name__)
@@ -221,6 +222,9 @@ class ModelRunner:
         self._no_pages = torch.zeros(0, dtype=torch.int32)
         self._no_pages_np = self._no_pages.numpy()
         self._graph_pool = torch.cuda.graph_pool_handle() if config.cuda_graphs else None
+        # the packed encoder forward and K/V paging, captured per token bucket
+        self._encoder_graphs = (EncoderGraphs(self.model, self.decoder_layers, self.isa)
+                                if config.cuda_graphs else None)
         # the decoder step; compiled as the reference compiles it when asked
         # (vflorence/engine/model_runner.py:121-123)
         self.decode_fn = (torch.compile(self.model, dynamic=True) if config.compile
@@ -309,17 +313,15 @@ class ModelRunner:
             positions.append(np.tile(token, len(group)))
             segments.append((start, len(group), enc_len))
             start += len(group) * enc_len
-        host = torch.from_numpy(np.concatenate([*ids, *positions, *slots]))
+        ids, positions, slots = (np.concatenate(a) for a in (ids, positions, slots))
+        if self._encoder_graphs is not None and self._encoder_graphs.run(ids, positions, slots,
+                                                                         segments):
+            return
+        host = torch.from_numpy(np.concatenate([ids, positions, slots]))
         dev = host.to(self.device, non_blocking=True)
         ids_d, pos_d, slots_d = dev[:start], dev[start: 2 * start], dev[2 * start:]
-        hidden = self.model.encode_packed(ids_d, pos_d, segments)
-        for layer in self.decoder_layers:
-            attn = layer.encoder_attn
-            kv = attn.kv_proj(hidden)
-            key, value = (t.view(start, attn.num_heads, attn.head_dim)
-                          for t in kv.chunk(2, dim=-1))
-            attention.reshape_and_cache(key, value, attn.k_cache, attn.v_cache, slots_d,
-                                        isa=self.isa)
+        page_cross_kv(self.decoder_layers, self.model.encode_packed(ids_d, pos_d, segments),
+                      slots_d, self.isa)
 
     def clear_request(self, request_id: int) -> None:
         """Return a finished request's encoder pages; drop the staged cross state."""

@@ -262,25 +262,36 @@ class BartEncoderSelfAttention(_Heads):
         self.qkv_proj = nn.Linear(embed_dim, 3 * embed_dim)
         self.out_proj = nn.Linear(embed_dim, embed_dim)
 
-    def forward(self, x: torch.Tensor, segments=None) -> torch.Tensor:
-        """``x``: [B, S, d] equal-length prompts, or with ``segments`` the [T, d] tokens of
-        prompts stored back to back, where each ``(start, count, length)`` names ``count``
-        prompts of ``length`` tokens from token ``start`` on: the projections run over
-        all T tokens at once and attention per run of equal-length prompts."""
+    def attention(self, x: torch.Tensor, segments=None) -> torch.Tensor:
+        """Attention output before ``out_proj``.  ``x``: [B, S, d] equal-length prompts,
+        or with ``segments`` the [T, d] tokens of prompts stored back to back, where each
+        ``(start, count, length)`` names ``count`` prompts of ``length`` tokens from token
+        ``start`` on: the projection runs over all T tokens at once and attention per run
+        of equal-length prompts."""
         if segments is None:
             b, s, _ = x.shape
             q, k, v = (t.view(b, s, self.num_heads, self.head_dim).transpose(1, 2)
                        for t in self.qkv_proj(x).chunk(3, dim=-1))
             out = F.scaled_dot_product_attention(q, k, v, scale=self.scaling)
-            return self.out_proj(out.transpose(1, 2).reshape(b, s, self.embed_dim))
-        qkv = self.qkv_proj(x)
-        parts = []
+            return out.transpose(1, 2).reshape(b, s, self.embed_dim)
+        out = x.new_empty(x.shape[0], self.embed_dim)
+        self.attend(self.qkv_proj(x), segments, out)
+        return out
+
+    def attend(self, qkv: torch.Tensor, segments, out: torch.Tensor) -> None:
+        """Attention of each run of equal-length prompts over the packed projections
+        ``qkv`` [>= T, 3 d], written to rows ``start .. start + count * length`` of
+        ``out``; other rows are left as they are."""
         for start, count, length in segments:
+            end = start + count * length
             q, k, v = (t.view(count, length, self.num_heads, self.head_dim).transpose(1, 2)
-                       for t in qkv[start: start + count * length].chunk(3, dim=-1))
-            out = F.scaled_dot_product_attention(q, k, v, scale=self.scaling)
-            parts.append(out.transpose(1, 2).reshape(count * length, self.embed_dim))
-        return self.out_proj(parts[0] if len(parts) == 1 else torch.cat(parts))
+                       for t in qkv[start:end].chunk(3, dim=-1))
+            o = F.scaled_dot_product_attention(q, k, v, scale=self.scaling)
+            out[start:end].view(count, length, self.num_heads, self.head_dim).copy_(
+                o.transpose(1, 2))
+
+    def forward(self, x: torch.Tensor, segments=None) -> torch.Tensor:
+        return self.out_proj(self.attention(x, segments))
 
 
 class BartDecoderSelfAttention(_Heads):
@@ -349,7 +360,12 @@ class BartEncoderLayer(nn.Module):
         self.final_layer_norm = nn.LayerNorm(d)
 
     def forward(self, h: torch.Tensor, segments=None) -> torch.Tensor:
-        h = _residual_norm(h, self.self_attn(h, segments), self.self_attn_layer_norm)
+        return self.tail(h, self.self_attn.attention(h, segments))
+
+    def tail(self, h: torch.Tensor, att: torch.Tensor) -> torch.Tensor:
+        """The layer after its attention: output projection, residual + LayerNorm,
+        feed-forward, residual + LayerNorm (row by row)."""
+        h = _residual_norm(h, self.self_attn.out_proj(att), self.self_attn_layer_norm)
         return _residual_norm(h, self.fc2(self.activation_fn(self.fc1(h))), self.final_layer_norm)
 
 
@@ -436,8 +452,11 @@ class BartEncoder(nn.Module):
         self.layers = nn.ModuleList(BartEncoderLayer(config) for _ in range(config.encoder_layers))
         self.layernorm_embedding = nn.LayerNorm(d)
 
+    def embed(self, input_ids, positions):
+        return self.layernorm_embedding(self.embed_tokens(input_ids) + self.embed_positions(positions))
+
     def forward(self, input_ids, positions, segments=None):
-        h = self.layernorm_embedding(self.embed_tokens(input_ids) + self.embed_positions(positions))
+        h = self.embed(input_ids, positions)
         for layer in self.layers:
             h = layer(h, segments)
         return h
