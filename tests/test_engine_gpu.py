@@ -396,6 +396,17 @@ def test_encoder_graphs_replay_with_new_prompts_and_fall_back_past_the_buckets(s
             graphs.max_tokens = 8192
     llm.abort()
     assert_clean(llm)
+    # new pools: the captured steps and encoder graphs that wrote the old ones are dropped,
+    # and the engine decodes the fixture's tokens again
+    runner.allocate_kv_cache()
+    assert not runner._graphs and (graphs is None or not graphs._buckets)
+    fx = fixtures()["small"]
+    c = fx["cases"]["greedy"]
+    from vflorence_amd import Request
+
+    outs = llm.generate([Request(q) for q in fx["prompts"]], SamplingParams(**c["params"]))
+    assert [o.completion_token_ids for o in outs] == c["tokens"]
+    assert_clean(llm)
 
 
 def test_failed_step_releases_everything(small_engine):

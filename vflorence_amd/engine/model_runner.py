@@ -254,6 +254,11 @@ class ModelRunner:
                              for c in (layer.self_attn.k_cache, layer.self_attn.v_cache)]
         self._cache_ptrs = hip_attn.cache_pointer_table(self._self_caches)
         self._copier = hip_attn.BlockCopier(self._self_caches)
+        if hasattr(self, "_graphs"):  # a reallocation: what points at the old pools goes
+            self._graphs.clear()
+            self._cross_key = self._cross_staged = None
+            if self._encoder_graphs is not None:
+                self._encoder_graphs.clear()
         mb = 1024**2
         weights = sum(t.nbytes for t in (*self.model.parameters(), *self.model.buffers()))
         kv = sum(c.nbytes for c in self._self_caches)
