@@ -208,11 +208,13 @@ class _FakeAttention:
         return (torch.tanh(q.float()) * (1.0 + layer_idx)).to(q.dtype)
 
 
+@pytest.mark.parametrize("rows", [96, 384, 512])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_decoder_layers_with_deferred_norms_match_separate_layer_norms(monkeypatch, dtype):
+def test_decoder_layers_with_deferred_norms_match_separate_layer_norms(monkeypatch, dtype, rows):
     """Three BART-large-width decoder layers with the attention ops replaced by fixed
     functions: the deferred path (6 projection launches per layer, one LayerNorm apply at
-    the end) against the separate residual + LayerNorm kernels, within a few roundings."""
+    the end) against the separate residual + LayerNorm kernels, within a few roundings,
+    up to the projections' 512-row limit (past it the layers take the separate path)."""
     from transformers import BartConfig
 
     from vflorence_amd.layers import bart
@@ -233,18 +235,19 @@ def test_decoder_layers_with_deferred_norms_match_separate_layer_norms(monkeypat
     for m in dec.modules():
         if isinstance(m, bart.DecodeLinear):
             m.repack()
-    ids = torch.randint(0, 64, (96,), device=DEV)
-    pos = torch.randint(0, 100, (96,), device=DEV)
+    ids = torch.randint(0, 64, (rows,), device=DEV)
+    pos = torch.randint(0, 100, (rows,), device=DEV)
     with torch.no_grad():
         h0 = bart._residual_norm(dec.embed_tokens(ids), dec.embed_positions(pos),
                                  dec.layernorm_embedding)
-        assert all(layer.deferred_ready(h0, 96) for layer in dec.layers)
+        assert all(layer.deferred_ready(h0, rows) for layer in dec.layers)
+        assert not any(layer.deferred_ready(h0, 513) for layer in dec.layers)
         dec.deferred_norms = True
         got = dec(ids, pos)
         dec.deferred_norms = False
         want = dec(ids, pos)
         torch.cuda.synchronize()
-    assert got.shape == want.shape == (96, 1024)
+    assert got.shape == want.shape == (rows, 1024)
     diff = (got.float() - want.float()).abs()
     scale = want.float().abs().mean()
     tol = 0.02 if dtype == torch.bfloat16 else 0.004
