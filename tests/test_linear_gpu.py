@@ -50,7 +50,8 @@ def test_packed_layout_is_the_documented_operand_order():
 @pytest.mark.parametrize("rows,out_f,in_f", [
     (1, 1024, 1024), (7, 1024, 1024), (64, 768, 768), (256, 1024, 1024), (256, 3072, 1024),
     (100, 1000, 512), (33, 1021, 256), (300, 96, 256), (5, 64, 4096), (40, 512, 1280),
-    (17, 256, 2560), (256, 1024, 4096)])
+    (17, 256, 2560), (256, 1024, 4096), (384, 3072, 1024), (512, 1024, 4096),
+    (448, 768, 768)])
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_linear_matches_float64(dtype, rows, out_f, in_f, with_bias):
     g = torch.Generator(device=DEV).manual_seed(rows * 7 + out_f)
@@ -179,7 +180,7 @@ def unpack(packed, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rows", [1, 37, 256])
+@pytest.mark.parametrize("rows", [1, 37, 256, 400, 512])
 def test_feed_forward_pair_gelu_and_packed_activation(dtype, rows):
     """fc1 with VFL_LINEAR_GELU | VFL_LINEAR_Y_PACKED, then fc2 with VFL_LINEAR_X_PACKED:
     the packed activation holds exactly the unpacked call's rows, fc2 over it equals fc2
