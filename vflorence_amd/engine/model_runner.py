@@ -293,7 +293,9 @@ class ModelRunner:
         equal prompt length; here the groups' prompts are stored back to back and run as
         one forward (projections, LayerNorms and feed-forward over all of the step's
         tokens at once, attention per group), then one K/V scatter per layer covers every
-        token.  Pages are taken per group, in the reference's order."""
+        token; with HIP graphs on, that forward and the scatters replay from graphs
+        captured per token bucket (``EncoderGraphs``), eagerly past the largest bucket.
+        Pages are taken per group, in the reference's order."""
         groups = defaultdict(list)
         for seq in seqs:
             if seq.pixel_values is not None:
