@@ -19,9 +19,9 @@ the dominant kernel (cross-attention, timed live with HIP events on its stream),
 op-level figure for 256 ragged self-attention sequences (ctx U[1, 1024], 20k-block
 pool), cross-attention over a fragmented encoder pool, the decoder's projections on
 vfl_linear against hipBLASLt (cold weights), the whole engine's decode step (BART-large
-4 beams; Florence-2-base shapes with 3 beams and 587 encoder tokens; continuous
-batching at Florence-2-large shapes up to 512 rows), and the CPU restatement (oracle/)
-timed on the host cores.
+4 beams at 64 and 128 requests; Florence-2-base shapes with 3 beams and 587 encoder
+tokens; continuous batching at Florence-2-large shapes up to 512 rows), and the CPU
+restatement (oracle/) timed on the host cores.
 """
 
 from __future__ import annotations
@@ -784,11 +784,12 @@ def measured_traffic(c_bytes: int):
     return int(t) if t is not None else None
 
 
-def engine_decode(torch, seed: int):
+def engine_decode(torch, seed: int, requests: int = REQUESTS):
     """Decoder tokens/s through the whole engine: BART-large (12+12 layers, d_model 1024,
-    vocab 50265, synthetic weights) in bf16, 64 requests x 4 beams with encoder prompts
-    of U[256, 1024] random token ids, 128 beam-search steps (EOS suppressed by
-    min_length, so every step runs 256 rows), decode steps replayed from HIP graphs.
+    vocab 50265, synthetic weights) in bf16, ``requests`` (64) requests x 4 beams with
+    encoder prompts of U[256, 1024] random token ids, 128 beam-search steps (EOS
+    suppressed by min_length, so every step runs 4 x ``requests`` rows), decode steps
+    replayed from HIP graphs.
     Timed: the steps after the first two (encoder + first beam step + capture); each
     step includes scheduling, metadata upload, copy-on-write, the decoder forward, the
     logits rules, top-k and the beam bookkeeping."""
@@ -797,10 +798,10 @@ def engine_decode(torch, seed: int):
     from vflorence_amd import LLM, Request, SamplingParams
 
     cfg = BartConfig(forced_eos_token_id=None)
-    llm = LLM(cfg, max_num_seqs=REQUESTS * BEAMS, dtype=torch.bfloat16,
+    llm = LLM(cfg, max_num_seqs=requests * BEAMS, dtype=torch.bfloat16,
               max_decoder_len=DECODE_STEPS, max_encoder_len=MAX_ENC, cuda_graphs=True)
     g = torch.Generator().manual_seed(seed + 101)
-    lens = torch.randint(ENC_MIN, ENC_MAX + 1, (REQUESTS,), generator=g).tolist()
+    lens = torch.randint(ENC_MIN, ENC_MAX + 1, (requests,), generator=g).tolist()
     params = SamplingParams(max_tokens=DECODE_STEPS, num_beams=BEAMS,
                             min_length=DECODE_STEPS + 2, eos_token_id=[cfg.eos_token_id])
     for n in lens:
@@ -829,11 +830,11 @@ def engine_decode(torch, seed: int):
     torch.cuda.empty_cache()
     return {
         "model": "BART-large shapes, synthetic weights, bf16",
-        "requests": REQUESTS, "beams": BEAMS, "enc_len": f"U[{ENC_MIN},{ENC_MAX}]",
+        "requests": requests, "beams": BEAMS, "enc_len": f"U[{ENC_MIN},{ENC_MAX}]",
         "timed_steps": steps,
         "ms_per_step": round(el * 1e3 / steps, 3),
         "decoded_rows_per_s": round(rows_done / el, 1),
-        "request_tokens_per_s": round(REQUESTS * steps / el, 1),
+        "request_tokens_per_s": round(requests * steps / el, 1),
         "first_two_steps_s": round(first, 3),
         "copy_on_write_pairs_per_step": round(pairs / steps, 1),
         "hip_graphs": True,
@@ -1289,10 +1290,13 @@ def main():
     torch.cuda.empty_cache()
     print("[bench] decoder projections: vfl_linear against hipBLASLt, cold weights", flush=True)
     linear = decoder_linear_timing(torch)
-    decoder = florence = batching = None
+    decoder = decoder_512 = florence = batching = None
     if not args.no_engine:
         print("[bench] engine decode: BART-large bf16, 64 requests x 4 beams", flush=True)
         decoder = engine_decode(torch, args.seed)
+        print("[bench] engine decode: BART-large bf16, 128 requests x 4 beams (512 rows)",
+              flush=True)
+        decoder_512 = engine_decode(torch, args.seed, requests=2 * REQUESTS)
         print("[bench] engine decode: Florence-2-base shapes bf16, 128 requests x 3 beams",
               flush=True)
         florence = engine_decode_florence_base(torch, args.seed)
@@ -1399,6 +1403,7 @@ def main():
             "decoder_linear_256_rows_cold_weights": linear,
         },
         "decoder_tokens": decoder,
+        "decoder_tokens_512_rows": decoder_512,
         "florence2_base_3beam": florence,
         "continuous_batching_florence2_large": batching,
         "cpu_baseline": cpu,
