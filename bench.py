@@ -248,6 +248,17 @@ def capture_steps(torch, wl, grouped=True, keep_outputs=False, planned=True, fol
         with torch.cuda.graph(g, pool=pool):
             outputs.append(run())
         graphs.append(g)
+    # Every graph launched once, back to back, as the last part of building them: a
+    # graph's first launch costs ~13 us more than later ones (measured; hipGraphUpload
+    # does not remove it).  An engine replays one graph per batch shape and pays that
+    # once; this schedule holds one graph per step, so without it the timed steps would
+    # pay it for most of the graphs a short run times.  The pass also leaves the GPU
+    # busy, as a decode loop keeps it, when the caller's warmup steps start (after ~1 s
+    # of capture, a run of 20 steps timed after 5 warmup steps ran 0.500-0.503 ms per
+    # step against 0.489-0.492 ms once the GPU had run ~10 ms of steps).  Replaying a
+    # step writes the same cache values again.
+    for g in graphs:
+        g.replay()
     torch.cuda.synchronize()
     if keep_outputs:
         return graphs, keep, outputs
@@ -1210,9 +1221,9 @@ def main():
     grouped = not args.ungrouped_self
     planned = grouped and not args.table_walk
     folded = planned and not args.separate_copy
-    graphs, keep = capture_steps(torch, wl, grouped, planned=planned, fold_copies=folded)
     plans = wl["plans"]
     per_step = [step_bytes(p, wl["enc"], grouped=grouped) for p in plans]
+    graphs, keep = capture_steps(torch, wl, grouped, planned=planned, fold_copies=folded)
 
     for t in schedule_order(args.warmup):
         graphs[t].replay()

@@ -74,9 +74,6 @@ def test_benchmarked_beam_workload_matches_the_oracle():
         assert pairs[t] <= limit
     assert 40 <= np.mean(pairs[1:]) <= 56, np.mean(pairs[1:])
 
-    # host mirror of the self-attention pools before any step runs (V in logical order)
-    mirror = [[host_bits(L.self_attn.k_cache),
-               host_bits(hip_attn.v_cache_logical(L.self_attn.v_cache))] for L in wl["layers"]]
     new_kv = []
     for i in range(LAYERS):
         qkv = host_bits(wl["qkv"][i]).reshape(rows, 3, 16, 64)
@@ -86,6 +83,11 @@ def test_benchmarked_beam_workload_matches_the_oracle():
 
     graphs, keep, outputs = bench.capture_steps(torch, wl, grouped=True, keep_outputs=True)
     assert len(graphs) == len(plans)
+    # host mirror of the self-attention pools as the build left them (it launched every
+    # step's graph once), V in logical order; the replays below start from there
+    torch.cuda.synchronize()
+    mirror = [[host_bits(L.self_attn.k_cache),
+               host_bits(hip_attn.v_cache_logical(L.self_attn.v_cache))] for L in wl["layers"]]
     for t, plan in enumerate(plans):
         graphs[t].replay()
         for i in range(LAYERS):
