@@ -18,11 +18,53 @@
 namespace vfl {
 
 // ---------------------------------------------------------------------------
-// wave-wide sum (64 lanes)
+// wave-wide reductions (64 lanes) on VALU lane moves: v_permlane32/16_swap across the
+// 16-lane rows, DPP inside them.  __shfl_xor compiles to ds_bpermute, an LDS round trip
+// per step; the top-k's selection loop makes dozens of these reductions per row (256 x
+// 50265 bf16 logits, k = 8: 22.3-24.5 us per launch with ds_bpermute).
 // ---------------------------------------------------------------------------
+constexpr int DPP_QUAD_REVERSE = 0x1B;  // quad_perm [3,2,1,0]
+constexpr int DPP_ROW_ROR8 = 0x128;     // row_ror:8: lane i of a row takes lane i ^ 8
+
+template <int CTRL> __device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+// The value of lane l ^ M (M = 1, 2, 4, 8: inside a 16-lane row).  Lane l ^ 4 is the
+// quad reversal followed by the half-row mirror: (l & ~3 | 3 - l % 4) mirrored in its
+// 8 lanes is l ^ 4.
+template <int M> __device__ __forceinline__ uint32_t lane_xor(uint32_t x) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "row-local partner");
+  if constexpr (M == 1) return dpp_u<DPP_QUAD_XOR1>(x);
+  else if constexpr (M == 2) return dpp_u<DPP_QUAD_XOR2>(x);
+  else if constexpr (M == 4) return dpp_u<DPP_ROW_HALF_MIRROR>(dpp_u<DPP_QUAD_REVERSE>(x));
+  else return dpp_u<DPP_ROW_ROR8>(x);
+}
+// Lane l's value and lane (l ^ 32)'s (P = 32), or l ^ 16's (P = 16), in some order: the
+// swap pairs the two halves (rows 0-1 with 2-3), resp. rows 0 with 1 and 2 with 3.
+template <int P> __device__ __forceinline__ void lane_pair(uint32_t x, uint32_t &a, uint32_t &b) {
+  static_assert(P == 16 || P == 32, "cross-row partner");
+  if constexpr (P == 32) {
+    const auto s = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    a = s[0], b = s[1];
+  } else {
+    const auto s = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    a = s[0], b = s[1];
+  }
+}
+
+// Sum over the 64 lanes, every lane getting it: the xor butterfly with offsets 32, 16,
+// 8, 4, 2, 1, each step adding the partner's value to the lane's own (floating-point
+// addition commutes, so the bits are those of the same butterfly on __shfl_xor).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  uint32_t a, b;
+  lane_pair<32>(__float_as_uint(v), a, b);
+  v = __uint_as_float(a) + __uint_as_float(b);
+  lane_pair<16>(__float_as_uint(v), a, b);
+  v = __uint_as_float(a) + __uint_as_float(b);
+  v += __uint_as_float(lane_xor<8>(__float_as_uint(v)));
+  v += __uint_as_float(lane_xor<4>(__float_as_uint(v)));
+  v += __uint_as_float(lane_xor<2>(__float_as_uint(v)));
+  v += __uint_as_float(lane_xor<1>(__float_as_uint(v)));
   return v;
 }
 
@@ -191,16 +233,35 @@ template <int K> __device__ __forceinline__ void pop_head(float (&val)[K], int (
   val[K - 1] = -INFINITY, tok[K - 1] = INT32_MAX;
 }
 
-// Wave-wide best (score, token) among every lane's head; ties by lane.
+// (bv, bt, bl) becomes the better of itself and (ov, ot, ol): higher score, then lower
+// token, then lower lane -- a strict order over the lanes' triples.
+__device__ __forceinline__ void take_better(float &bv, int &bt, int &bl, float ov, int ot, int ol) {
+  if (better(ov, ot, bv, bt) || (ov == bv && ot == bt && ol < bl)) bv = ov, bt = ot, bl = ol;
+}
+template <int P> __device__ __forceinline__ void best_across(float &v, int &t, int &l) {
+  uint32_t v0, v1, t0, t1, l0, l1;
+  lane_pair<P>(__float_as_uint(v), v0, v1);
+  lane_pair<P>((uint32_t)t, t0, t1);
+  lane_pair<P>((uint32_t)l, l0, l1);
+  v = __uint_as_float(v0), t = (int)t0, l = (int)l0;
+  take_better(v, t, l, __uint_as_float(v1), (int)t1, (int)l1);
+}
+template <int M> __device__ __forceinline__ void best_within(float &v, int &t, int &l) {
+  take_better(v, t, l, __uint_as_float(lane_xor<M>(__float_as_uint(v))),
+              (int)lane_xor<M>((uint32_t)t), (int)lane_xor<M>((uint32_t)l));
+}
+
+// Wave-wide best (score, token) among every lane's head; ties by lane.  The best of a
+// strict order does not depend on how the butterfly pairs the lanes.
 __device__ __forceinline__ void wave_best(float v, int t, float &bv, int &bt, int &blane) {
-  int lane = threadIdx.x & 63;
-  bv = v, bt = t, blane = lane;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, 64);
-    const int ot = __shfl_xor(bt, o, 64), ol = __shfl_xor(blane, o, 64);
-    if (better(ov, ot, bv, bt) || (ov == bv && ot == bt && ol < blane)) bv = ov, bt = ot, blane = ol;
-  }
+  int l = threadIdx.x & 63;
+  best_within<1>(v, t, l);
+  best_within<2>(v, t, l);
+  best_within<4>(v, t, l);
+  best_within<8>(v, t, l);
+  best_across<16>(v, t, l);
+  best_across<32>(v, t, l);
+  bv = v, bt = t, blane = l;
 }
 
 struct TopkRules {
@@ -235,9 +296,15 @@ template <int DT> __device__ __forceinline__ float vec_elem(const uint4 &u, int 
 
 // Wave-wide maximum.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, __uint_as_float(lane_xor<1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(lane_xor<2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(lane_xor<4>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(lane_xor<8>(__float_as_uint(v))));
+  uint32_t a, b;
+  lane_pair<16>(__float_as_uint(v), a, b);
+  v = fmaxf(__uint_as_float(a), __uint_as_float(b));
+  lane_pair<32>(__float_as_uint(v), a, b);
+  return fmaxf(__uint_as_float(a), __uint_as_float(b));
 }
 
 // Row top-k in two reads of the row (the second mostly from L2):
