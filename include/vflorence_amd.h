@@ -351,6 +351,25 @@ int vfl_add_layer_norm(const void *x, int64_t x_stride, const void *residual,
                        void *stream);
 
 /*
+ * The decoder's input embedding in one launch, replacing the lookups and LayerNorm of
+ * vflorence/models/bart.py:260-264 (embed_tokens :24-39, embed_positions :12-21):
+ *   t = token_table[ids[r]] * token_scale   (rounded to the element type; none at 1)
+ *   p = position_table[positions[r] + position_offset]        (BART: offset 2)
+ *   out[r] = LayerNorm(p + t) * weight + bias
+ * with vfl_add_layer_norm's arithmetic (the sum rounded to the element type, fp32
+ * statistics).  ids and positions are DEVICE int64 arrays of `rows` entries; a row whose
+ * token or position index falls outside its table (token_rows, position_rows) is written
+ * as NaN instead of reading past the table.  Same dim, alignment and stride rules as
+ * vfl_add_layer_norm for the tables and out.
+ */
+int vfl_embed_layer_norm(const int64_t *ids, const int64_t *positions, int64_t rows,
+                         const void *token_table, int64_t token_rows, int64_t token_stride,
+                         float token_scale, const void *position_table, int64_t position_rows,
+                         int64_t position_stride, int64_t position_offset, const void *weight,
+                         const void *bias, void *out, int64_t out_stride, int dim, float eps,
+                         int dtype, void *stream);
+
+/*
  * Replaces the device work of ModelRunner._sample / _beam_search
  * (vflorence/engine/model_runner.py:355-398) and LogitsProcessor
  * (vflorence/layers/logits_processor.py:24-51) for the rules that need no token
@@ -367,7 +386,10 @@ int vfl_add_layer_norm(const void *x, int64_t x_stride, const void *residual,
  * n_eos EOS, n_suppress suppressed, n_begin begin-suppressed, n_bos forced-BOS and
  * n_forced_eos forced-EOS token ids.  1 <= k <= 16; lengths may be NULL only without
  * rule tokens.  Repetition penalty and n-gram bans (which read the history) are not
- * covered: their callers apply them before, on the logits.
+ * covered: their callers apply them before, on the logits.  scores and ids may be
+ * device memory or pinned host memory (hipHostMalloc): the kernel stores straight into
+ * either, so a caller that needs the result on the host synchronizes the stream and
+ * reads it, with no copy launch.
  */
 int vfl_logprob_topk(const void *logits, int64_t row_stride, int64_t rows, int vocab, int dtype,
                      const int64_t *lengths, const int32_t *rule_tokens, int min_length,

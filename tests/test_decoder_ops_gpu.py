@@ -129,3 +129,70 @@ def test_logprob_topk_on_16bit_logits_breaks_ties_by_token(dtype):
     # greedy: the first maximum, as torch.argmax returns it
     _, top1 = ops().logprob_topk(logits, 1, log_softmax=False)
     assert torch.equal(top1[:, 0], logits.float().argmax(dim=-1))
+
+
+@pytest.mark.parametrize("k,log_softmax", [(8, True), (1, False)])
+def test_logprob_topk_writes_pinned_host_outputs(k, log_softmax):
+    """The kernel stores into pinned host tensors directly: after a stream
+    synchronization they hold what the device-output call returns, and a second call
+    into the same tensors overwrites every entry."""
+    g = torch.Generator(device=DEV).manual_seed(11)
+    outs = (torch.full((64, k), float("nan"), dtype=torch.float32, pin_memory=True),
+            torch.full((64, k), -7, dtype=torch.int64, pin_memory=True))
+    for step in range(2):
+        logits = (torch.randn(64, 50432, device=DEV, generator=g) * 3).to(torch.bfloat16)
+        logits = logits[:, :50265]
+        want_v, want_i = ops().logprob_topk(logits, k, log_softmax=log_softmax)
+        got_v, got_i = ops().logprob_topk(logits, k, log_softmax=log_softmax, out=outs)
+        assert got_v is outs[0] and got_i is outs[1]
+        torch.cuda.current_stream().synchronize()
+        assert torch.equal(got_v, want_v.cpu()) and torch.equal(got_i, want_i.cpu()), step
+    with pytest.raises(ValueError):
+        ops().logprob_topk(logits, k, log_softmax=log_softmax,
+                           out=(torch.empty(64, k), torch.empty(64, k, dtype=torch.int64)))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("scale", [1.0, 32.0])
+def test_embed_layer_norm_equals_lookups_then_add_layer_norm(dtype, scale):
+    """One launch for the decoder's embeddings: bit for bit what the two lookups (the
+    token row scaled and stored in the element type) and the residual + LayerNorm kernel
+    give, over ids and positions that hit the tables' first and last rows."""
+    g = torch.Generator(device=DEV).manual_seed(3)
+    vocab, max_pos, dim, rows, off = 1000, 130, 1024, 77, 2
+    tok = torch.randn(vocab, dim, device=DEV, generator=g).to(dtype)
+    pos = torch.randn(max_pos + off, dim, device=DEV, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(dim, device=DEV, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(dim, device=DEV, generator=g)).to(dtype)
+    ids = torch.randint(0, vocab, (rows,), device=DEV, generator=g)
+    positions = torch.randint(0, max_pos, (rows,), device=DEV, generator=g)
+    ids[:2] = torch.tensor([0, vocab - 1], device=DEV)
+    positions[:2] = torch.tensor([0, max_pos - 1], device=DEV)
+    got = ops().embed_layer_norm(ids, positions, tok, scale, pos, off, w, b, 1e-5)
+    t = F.embedding(ids, tok)
+    if scale != 1.0:
+        t = t * scale
+    want = ops().add_layer_norm(F.embedding(positions + off, pos), t, w, b, 1e-5)
+    assert got.dtype == dtype and got.shape == (rows, dim)
+    assert torch.equal(got, want)
+
+
+def test_embed_layer_norm_marks_rows_with_indices_outside_the_tables():
+    g = torch.Generator(device=DEV).manual_seed(4)
+    tok = torch.randn(50, 64, device=DEV, generator=g).to(torch.bfloat16)
+    pos = torch.randn(12, 64, device=DEV, generator=g).to(torch.bfloat16)
+    w = torch.ones(64, device=DEV, dtype=torch.bfloat16)
+    b = torch.zeros(64, device=DEV, dtype=torch.bfloat16)
+    ids = torch.tensor([3, 50, -1, 7, 8], device=DEV)
+    positions = torch.tensor([0, 1, 2, 10, -3], device=DEV)  # + 2: 12 and -1 are outside
+    got = ops().embed_layer_norm(ids, positions, tok, 1.0, pos, 2, w, b, 1e-5)
+    bad = torch.tensor([False, True, True, True, True], device=DEV)
+    assert torch.isnan(got[bad]).all()
+    assert torch.isfinite(got[~bad]).all()
+    want = ops().add_layer_norm(pos[2:3], tok[3:4], w, b, 1e-5)
+    assert torch.equal(got[:1], want)
+    with pytest.raises(ValueError):
+        ops().embed_layer_norm(ids.int(), positions, tok, 1.0, pos, 2, w, b, 1e-5)
+    with pytest.raises(RuntimeError):
+        ops().embed_layer_norm(ids.cpu(), positions.cpu(), tok.cpu(), 1.0, pos.cpu(), 2, w.cpu(),
+                               b.cpu(), 1e-5)

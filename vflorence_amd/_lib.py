@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "vfl_copy_blocks",
     "vfl_copy_blocks_noalloc",
     "vfl_add_layer_norm",
+    "vfl_embed_layer_norm",
     "vfl_logprob_topk",
     "vfl_linear_packed_elems",
     "vfl_pack_linear_weight",
@@ -109,6 +110,11 @@ _SIGNATURES = {
     "vfl_add_layer_norm": (
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _f32, _i32, _vp],
+    ),
+    "vfl_embed_layer_norm": (
+        ctypes.c_int,
+        [_vp, _vp, _i64, _vp, _i64, _i64, _f32, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i32,
+         _f32, _i32, _vp],
     ),
     "vfl_logprob_topk": (
         ctypes.c_int,

@@ -220,13 +220,24 @@ constexpr int DPP_ROW_MIRROR = 0x140;
 // lane of a group ends with the group's sum.  Within a 16-lane row the partners come
 // from DPP (no LDS traffic): after the quad sums, half-row mirroring pairs each
 // quad with the other quad of its half-row, and row mirroring pairs the halves.
+// Across rows, v_permlane16_swap pairs rows 0-1 and 2-3 and v_permlane32_swap the two
+// halves (VALU moves too); each pair's lanes add the same two values, as lane l and
+// lane l ^ 16 (l ^ 32) of an xor butterfly would.
 template <int N> __device__ __forceinline__ float group_sum(float x) {
   if constexpr (N >= 2) x += dpp<DPP_QUAD_XOR1>(x);
   if constexpr (N >= 4) x += dpp<DPP_QUAD_XOR2>(x);
   if constexpr (N >= 8) x += dpp<DPP_ROW_HALF_MIRROR>(x);
   if constexpr (N >= 16) x += dpp<DPP_ROW_MIRROR>(x);
-  if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
-  if constexpr (N >= 64) x += __shfl_xor(x, 32, 64);
+  if constexpr (N >= 32) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  }
+  if constexpr (N >= 64) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  }
   return x;
 }
 

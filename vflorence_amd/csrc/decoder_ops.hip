@@ -118,18 +118,40 @@ template <> __device__ __forceinline__ float round_to_elem<VFL_FLOAT16>(float v)
 // 256 rows x 1024): 2 rows per workgroup 2.45 ms per step, 4 rows 2.47-2.48, 1 row 2.48.
 constexpr int LN_ROWS = 2;
 
-template <int DT, int NV>  // NV: 4-element vectors per lane (dim <= 256 * NV)
+// Rows of x and residual taken from tables: row r reads x row x_rows[r] + x_offset and
+// residual row r_rows[r] + r_offset, the residual row times r_scale rounded to the
+// element type first when r_scale != 1 (what a scaled embedding lookup stores).  A row
+// whose index falls outside its table comes out NaN.
+struct RowGather {
+  const int64_t *x_rows, *r_rows;
+  int64_t x_offset, r_offset, x_count, r_count;
+  float r_scale;
+};
+
+template <int DT, int NV, bool GATHER>  // NV: 4-element vectors per lane (dim <= 256 * NV)
 __global__ __launch_bounds__(64 * LN_ROWS) void add_layer_norm_kernel(
     const typename Elem<DT>::T *x, int64_t x_stride, const typename Elem<DT>::T *residual,
     int64_t r_stride, const typename Elem<DT>::T *__restrict__ weight,
     const typename Elem<DT>::T *__restrict__ bias, typename Elem<DT>::T *out, int64_t out_stride,
-    int64_t rows, int dim, float eps) {
+    int64_t rows, int dim, float eps, RowGather g) {
   // out may alias x or residual: each lane reads its elements before the reductions
   // and writes the same elements after them.
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * LN_ROWS + (threadIdx.x >> 6);
   if (row >= rows) return;  // wave-uniform
   const int nvec = dim >> 2;
+  int64_t xr = row, rr = row;
+  if constexpr (GATHER) {
+    xr = g.x_rows[row] + g.x_offset;
+    rr = g.r_rows[row] + g.r_offset;
+    if (xr < 0 || xr >= g.x_count || rr < 0 || rr >= g.r_count) {  // wave-uniform
+      for (int i = lane; i < nvec; i += 64) {
+        const float nan4[4] = {NAN, NAN, NAN, NAN};
+        store4<DT>(out + row * out_stride + i * 4, nan4);
+      }
+      return;
+    }
+  }
   float v[NV][4], w[NV][4], b[NV][4];
   float sum = 0.f;
 #pragma unroll
@@ -137,10 +159,16 @@ __global__ __launch_bounds__(64 * LN_ROWS) void add_layer_norm_kernel(
     const int vi = lane + 64 * k;
     if (vi < nvec) {
       float a[4], c[4];
-      load4<DT>(x + row * x_stride + vi * 4, a);
-      load4<DT>(residual + row * r_stride + vi * 4, c);
+      load4<DT>(x + xr * x_stride + vi * 4, a);
+      load4<DT>(residual + rr * r_stride + vi * 4, c);
       load4<DT>(weight + vi * 4, w[k]);
       load4<DT>(bias + vi * 4, b[k]);
+      if constexpr (GATHER) {
+        if (g.r_scale != 1.f) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) c[e] = round_to_elem<DT>(c[e] * g.r_scale);
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[k][e] = round_to_elem<DT>(a[e] + c[e]);
@@ -176,17 +204,17 @@ __global__ __launch_bounds__(64 * LN_ROWS) void add_layer_norm_kernel(
   }
 }
 
-template <int DT>
+template <int DT, bool GATHER>
 static int launch_add_layer_norm(const void *x, int64_t xs, const void *r, int64_t rs,
                                  const void *w, const void *b, void *out, int64_t os, int64_t rows,
-                                 int dim, float eps, hipStream_t stream) {
+                                 int dim, float eps, const RowGather &g, hipStream_t stream) {
   using T = typename Elem<DT>::T;
   const int nvec = dim / 4;
   const dim3 grid((unsigned)((rows + LN_ROWS - 1) / LN_ROWS)), block(64 * LN_ROWS);
 #define VFL_LN(NV)                                                                             \
-  add_layer_norm_kernel<DT, NV><<<grid, block, 0, stream>>>(                                   \
+  add_layer_norm_kernel<DT, NV, GATHER><<<grid, block, 0, stream>>>(                           \
       (const T *)x, xs, (const T *)r, rs, (const T *)w, (const T *)b, (T *)out, os, rows, dim, \
-      eps)
+      eps, g)
   if (nvec <= 64)
     VFL_LN(1);
   else if (nvec <= 128)
@@ -198,7 +226,7 @@ static int launch_add_layer_norm(const void *x, int64_t xs, const void *r, int64
   else
     VFL_LN(16);
 #undef VFL_LN
-  return launch_status("add_layer_norm");
+  return launch_status(GATHER ? "embed_layer_norm" : "add_layer_norm");
 }
 
 // ---------------------------------------------------------------------------
@@ -554,43 +582,90 @@ using namespace vfl;
 
 static bool aligned(const void *p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
 
-extern "C" int vfl_add_layer_norm(const void *x, int64_t x_stride, const void *residual,
-                                  int64_t residual_stride, const void *weight, const void *bias,
-                                  void *out, int64_t out_stride, int64_t rows, int dim, float eps,
-                                  int dtype, void *stream) {
-  clear_error();
+// Shared argument checks of the residual + LayerNorm entry points.
+static int check_layer_norm(const char *who, int64_t rows, int dim, int dtype, const void *x,
+                            int64_t x_stride, const void *residual, int64_t residual_stride,
+                            const void *weight, const void *bias, const void *out,
+                            int64_t out_stride) {
   if (dtype != VFL_FLOAT32 && dtype != VFL_BFLOAT16 && dtype != VFL_FLOAT16) {
-    set_error("add_layer_norm: unsupported dtype code %d", dtype);
+    set_error("%s: unsupported dtype code %d", who, dtype);
     return VFL_E_INVALID;
   }
   if (rows < 0 || rows > 2147483647LL || dim <= 0 || dim % 4 || dim > 4096) {
-    set_error("add_layer_norm: dim %d must be a positive multiple of 4 up to 4096 (rows %lld)",
-              dim, (long long)rows);
+    set_error("%s: dim %d must be a positive multiple of 4 up to 4096 (rows %lld)", who, dim,
+              (long long)rows);
     return VFL_E_INVALID;
   }
   if (!x || !residual || !weight || !bias || !out) {
-    set_error("add_layer_norm: null pointer argument");
+    set_error("%s: null pointer argument", who);
     return VFL_E_INVALID;
   }
   const int vb = 4 * elem_bytes(dtype);
   if (x_stride % 4 || residual_stride % 4 || out_stride % 4 || !aligned(x, vb) ||
       !aligned(residual, vb) || !aligned(weight, vb) || !aligned(bias, vb) || !aligned(out, vb) ||
       x_stride < dim || residual_stride < dim || out_stride < dim) {
-    set_error("add_layer_norm: rows must be %d-byte aligned with strides that are multiples of 4 "
+    set_error("%s: rows must be %d-byte aligned with strides that are multiples of 4 "
               "elements and at least dim",
-              vb);
+              who, vb);
+    return VFL_E_INVALID;
+  }
+  return VFL_OK;
+}
+
+template <bool GATHER>
+static int launch_layer_norm(int dtype, const void *x, int64_t xs, const void *r, int64_t rs,
+                             const void *w, const void *b, void *out, int64_t os, int64_t rows,
+                             int dim, float eps, const RowGather &g, hipStream_t s) {
+  if (dtype == VFL_FLOAT32)
+    return launch_add_layer_norm<VFL_FLOAT32, GATHER>(x, xs, r, rs, w, b, out, os, rows, dim,
+                                                      eps, g, s);
+  if (dtype == VFL_BFLOAT16)
+    return launch_add_layer_norm<VFL_BFLOAT16, GATHER>(x, xs, r, rs, w, b, out, os, rows, dim,
+                                                       eps, g, s);
+  return launch_add_layer_norm<VFL_FLOAT16, GATHER>(x, xs, r, rs, w, b, out, os, rows, dim, eps,
+                                                    g, s);
+}
+
+extern "C" int vfl_add_layer_norm(const void *x, int64_t x_stride, const void *residual,
+                                  int64_t residual_stride, const void *weight, const void *bias,
+                                  void *out, int64_t out_stride, int64_t rows, int dim, float eps,
+                                  int dtype, void *stream) {
+  clear_error();
+  const int st = check_layer_norm("add_layer_norm", rows, dim, dtype, x, x_stride, residual,
+                                  residual_stride, weight, bias, out, out_stride);
+  if (st != VFL_OK) return st;
+  if (rows == 0) return VFL_OK;
+  return launch_layer_norm<false>(dtype, x, x_stride, residual, residual_stride, weight, bias,
+                                  out, out_stride, rows, dim, eps, RowGather{},
+                                  (hipStream_t)stream);
+}
+
+extern "C" int vfl_embed_layer_norm(const int64_t *ids, const int64_t *positions, int64_t rows,
+                                    const void *token_table, int64_t token_rows,
+                                    int64_t token_stride, float token_scale,
+                                    const void *position_table, int64_t position_rows,
+                                    int64_t position_stride, int64_t position_offset,
+                                    const void *weight, const void *bias, void *out,
+                                    int64_t out_stride, int dim, float eps, int dtype,
+                                    void *stream) {
+  clear_error();
+  const int st = check_layer_norm("embed_layer_norm", rows, dim, dtype, position_table,
+                                  position_stride, token_table, token_stride, weight, bias, out,
+                                  out_stride);
+  if (st != VFL_OK) return st;
+  if (!ids || !positions || token_rows <= 0 || position_rows <= 0) {
+    set_error("embed_layer_norm: null index array or empty table (token rows %lld, position "
+              "rows %lld)",
+              (long long)token_rows, (long long)position_rows);
     return VFL_E_INVALID;
   }
   if (rows == 0) return VFL_OK;
-  hipStream_t s = (hipStream_t)stream;
-  if (dtype == VFL_FLOAT32)
-    return launch_add_layer_norm<VFL_FLOAT32>(x, x_stride, residual, residual_stride, weight, bias,
-                                              out, out_stride, rows, dim, eps, s);
-  if (dtype == VFL_BFLOAT16)
-    return launch_add_layer_norm<VFL_BFLOAT16>(x, x_stride, residual, residual_stride, weight,
-                                               bias, out, out_stride, rows, dim, eps, s);
-  return launch_add_layer_norm<VFL_FLOAT16>(x, x_stride, residual, residual_stride, weight, bias,
-                                            out, out_stride, rows, dim, eps, s);
+  // x: the position rows, residual: the (scaled) token rows -- the operand order of
+  // add_layer_norm(position embedding, token embedding)
+  const RowGather g{positions, ids, position_offset, 0, position_rows, token_rows, token_scale};
+  return launch_layer_norm<true>(dtype, position_table, position_stride, token_table,
+                                 token_stride, weight, bias, out, out_stride, rows, dim, eps, g,
+                                 (hipStream_t)stream);
 }
 
 extern "C" int vfl_logprob_topk(const void *logits, int64_t row_stride, int64_t rows, int vocab,

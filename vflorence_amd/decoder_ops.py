@@ -71,6 +71,44 @@ def _(x, residual, weight, bias, eps):
     return torch.empty_like(x, memory_format=torch.contiguous_format)
 
 
+@torch.library.custom_op("vflorence_amd::embed_layer_norm", mutates_args=())
+def embed_layer_norm(ids: torch.Tensor, positions: torch.Tensor, token_table: torch.Tensor,
+                     token_scale: float, position_table: torch.Tensor, position_offset: int,
+                     weight: torch.Tensor, bias: torch.Tensor, eps: float) -> torch.Tensor:
+    """``LayerNorm(position_table[positions + position_offset] + token_table[ids] *
+    token_scale) * weight + bias`` for int64 ``ids`` / ``positions`` [rows]: the decoder's
+    embeddings and their LayerNorm in one launch, with ``add_layer_norm``'s arithmetic on
+    the two looked-up rows (the scaled token row rounded to the element type first).  A
+    row whose index lies outside its table comes out NaN."""
+    dev = _require_gpu(ids, positions, token_table, position_table, weight, bias)
+    dim = token_table.shape[-1]
+    if (token_table.dim() != 2 or position_table.dim() != 2 or position_table.shape[1] != dim
+            or weight.shape != (dim,) or bias.shape != (dim,)):
+        raise ValueError("embed_layer_norm: tables must be [rows, dim]; weight / bias [dim]")
+    if ids.dtype != torch.int64 or positions.dtype != torch.int64 or ids.dim() != 1 \
+            or positions.shape != ids.shape:
+        raise ValueError("embed_layer_norm: ids and positions must be int64 [rows]")
+    if len({token_table.dtype, position_table.dtype, weight.dtype, bias.dtype}) != 1:
+        raise ValueError("embed_layer_norm: tables, weight and bias must share one dtype")
+    tok = token_table if token_table.stride(-1) == 1 else token_table.contiguous()
+    pos = position_table if position_table.stride(-1) == 1 else position_table.contiguous()
+    ids, positions = ids.contiguous(), positions.contiguous()
+    rows = ids.shape[0]
+    out = torch.empty(rows, dim, dtype=tok.dtype, device=dev)
+    check(lib.vfl_embed_layer_norm(
+        ids.data_ptr(), positions.data_ptr(), rows, tok.data_ptr(), tok.shape[0], tok.stride(0),
+        token_scale, pos.data_ptr(), pos.shape[0], pos.stride(0), position_offset,
+        weight.contiguous().data_ptr(), bias.contiguous().data_ptr(), out.data_ptr(),
+        out.stride(0), dim, eps, _dtype_code(tok.dtype), _stream(dev)))
+    return out
+
+
+@embed_layer_norm.register_fake
+def _(ids, positions, token_table, token_scale, position_table, position_offset, weight, bias,
+      eps):
+    return token_table.new_empty(ids.shape[0], token_table.shape[-1])
+
+
 def linear_fits(rows: int, weight: torch.Tensor, *, max_in: int | None = LINEAR_MAX_IN,
                 max_out: int | None = LINEAR_MAX_OUT) -> bool:
     """Whether ``linear`` serves ``rows`` rows times ``weight``: a contiguous, 16-byte
@@ -368,9 +406,12 @@ class TopkRules:
 
 
 def logprob_topk(logits: torch.Tensor, k: int, *, log_softmax: bool,
-                 lengths: torch.Tensor | None = None, rules: TopkRules | None = None):
+                 lengths: torch.Tensor | None = None, rules: TopkRules | None = None,
+                 out: tuple[torch.Tensor, torch.Tensor] | None = None):
     """Per row: (log-softmax), generation rules, and the k best scores with their token
-    ids, best first (ties: lower token id).  Returns (float32 [rows, k], int64 [rows, k])."""
+    ids, best first (ties: lower token id).  Returns (float32 [rows, k], int64 [rows, k]):
+    new device tensors, or ``out`` filled in -- which may be pinned host tensors, written
+    by the kernel itself (valid on the host once the stream has been synchronized)."""
     dev = _require_gpu(logits)
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be [rows, vocab] with contiguous rows")
@@ -383,8 +424,17 @@ def logprob_topk(logits: torch.Tensor, k: int, *, log_softmax: bool,
         raise ValueError("the rules need per-row lengths")
     if lengths is not None and (lengths.dtype != torch.int64 or lengths.shape != (rows,)):
         raise ValueError("lengths must be int64 [rows]")
-    scores = torch.empty(rows, k, dtype=torch.float32, device=dev)
-    ids = torch.empty(rows, k, dtype=torch.int64, device=dev)
+    if out is None:
+        scores = torch.empty(rows, k, dtype=torch.float32, device=dev)
+        ids = torch.empty(rows, k, dtype=torch.int64, device=dev)
+    else:
+        scores, ids = out
+        for t, dt in ((scores, torch.float32), (ids, torch.int64)):
+            if t.dtype != dt or t.shape != (rows, k) or not t.is_contiguous():
+                raise ValueError(f"out tensors must be contiguous {dt} [{rows}, {k}]")
+            if not (t.device == logits.device or (t.device.type == "cpu" and t.is_pinned())):
+                raise ValueError("out tensors must be on the logits' device or in pinned "
+                                 "host memory")
     check(lib.vfl_logprob_topk(
         logits.data_ptr(), logits.stride(0), rows, vocab, _dtype_code(logits.dtype),
         None if lengths is None else lengths.data_ptr(),

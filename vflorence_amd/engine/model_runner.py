@@ -133,6 +133,16 @@ def _to_host(*tensors: torch.Tensor) -> list[torch.Tensor]:
     return out
 
 
+def _pinned(shape: tuple, dtype: torch.dtype) -> torch.Tensor:
+    """A pinned host tensor kept per shape and dtype, for a kernel to write its result
+    into (callers use it before asking for the same shape again)."""
+    key = ("out", tuple(shape), dtype)
+    o = _HOST_STAGING.get(key)
+    if o is None:
+        o = _HOST_STAGING[key] = torch.empty(shape, dtype=dtype, pin_memory=True)
+    return o
+
+
 def launch_slots(padded: int, below: int, beams: int, max_group: int) -> int:
     """Row-group slots an attention launch over a bucket of ``padded`` rows needs when
     its real rows are whole requests of ``beams`` rows each (more than ``below`` rows:
@@ -472,14 +482,17 @@ class ModelRunner:
         rules = processor.topk_rules() if logits.is_cuda else None
         keep = max(2, 1 + len(sp.eos_ids())) * sp.num_beams
         if rules is not None and (sp.num_beams == 1 or keep <= decoder_ops.MAX_K):
-            # one kernel: log-softmax (beam search), the rules, the per-row top-k
+            # one kernel: log-softmax (beam search), the rules, the per-row top-k, its
+            # result stored by the kernel straight into pinned host memory (no copy
+            # launches at the end of the step)
+            k = 1 if sp.num_beams == 1 else min(keep, logits.shape[-1])
+            rows = logits.shape[0]
+            out = (_pinned((rows, k), torch.float32), _pinned((rows, k), torch.int64))
+            top, ids = decoder_ops.logprob_topk(logits, k, log_softmax=sp.num_beams > 1,
+                                                lengths=lengths, rules=rules, out=out)
+            torch.cuda.current_stream().synchronize()
             if sp.num_beams == 1:
-                _, ids = decoder_ops.logprob_topk(logits, 1, log_softmax=False, lengths=lengths,
-                                                  rules=rules)
-                return _to_host(ids[:, 0])[0].numpy()
-            top, ids = decoder_ops.logprob_topk(logits, min(keep, logits.shape[-1]),
-                                                log_softmax=True, lengths=lengths, rules=rules)
-            top, ids = _to_host(top.float(), ids)
+                return ids[:, 0].numpy()
             return top.numpy(), ids.numpy()
         scores = logits.float()
         if sp.num_beams > 1:

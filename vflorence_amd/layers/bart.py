@@ -483,9 +483,24 @@ class BartDecoder(nn.Module):
             layer.encoder_attn.q_proj.set_input_norm(layer.self_attn_layer_norm)
             layer.fc1.set_input_norm(layer.encoder_attn_layer_norm)
 
+    def embed(self, input_ids, positions):
+        """``layernorm_embedding(embed_tokens(ids) + embed_positions(positions))``
+        (vflorence/models/bart.py:260-264): on the GPU one launch that looks up both rows
+        and normalizes their sum (vflorence_amd::embed_layer_norm), the same arithmetic as
+        the lookups followed by the residual + LayerNorm kernel."""
+        tok, pos, ln = self.embed_tokens, self.embed_positions, self.layernorm_embedding
+        d = tok.weight.shape[1]
+        if (input_ids.is_cuda and input_ids.dim() == 1 and input_ids.dtype == torch.int64
+                and positions.dtype == torch.int64 and d % 4 == 0 and d <= 4096
+                and tok.weight.dtype == pos.weight.dtype == ln.weight.dtype):
+            from ..decoder_ops import embed_layer_norm
+
+            return embed_layer_norm(input_ids, positions, tok.weight, float(tok.embed_scale),
+                                    pos.weight, pos.OFFSET, ln.weight, ln.bias, ln.eps)
+        return _residual_norm(tok(input_ids), pos(positions), ln)
+
     def forward(self, input_ids, positions):
-        h = _residual_norm(self.embed_tokens(input_ids), self.embed_positions(positions),
-                           self.layernorm_embedding)
+        h = self.embed(input_ids, positions)
         rows = h.shape[0]
         if (h.is_cuda and h.dim() == 2 and h.dtype in (torch.bfloat16, torch.float16)
                 and self.deferred_norms):
