@@ -72,6 +72,7 @@ class _StepBuffers:
         self.h = self._views(self.host)
         self.d = self._views(self.dev)
         self.np = {k: v.numpy() for k, v in self.h.items()}
+        self.ptr = {k: v.data_ptr() for k, v in self.h.items()}  # host staging addresses
 
     def _views(self, buf):
         r, w = self.rows, self.width
@@ -91,21 +92,19 @@ class _StepBuffers:
         the number of groups."""
         gs = self.np["group_start"]
         groups = int(np.searchsorted(gs[: padded + 1], padded))
-        h = self.h
+        p = self.ptr
         check(lib.vfl_build_group_plan(
-            h["tables"].data_ptr(), self.width, self.width, h["context_lens"].data_ptr(),
-            padded, h["group_start"].data_ptr(), None, groups, block_size, num_blocks,
-            h["plan"].data_ptr(), self.rows, self.plan_stride))
+            p["tables"], self.width, self.width, p["context_lens"], padded, p["group_start"],
+            None, groups, block_size, num_blocks, p["plan"], self.rows, self.plan_stride))
         self._plan_words = 4 + groups * self.plan_stride
         return groups
 
     def fold_copies(self, num_pairs: int, num_blocks: int) -> bool:
         """Fold the packed copy-on-write pairs into the plan just built (the fused
         self-attention launches then copy the blocks); False when they cannot be."""
-        h = self.h
-        rc = lib.vfl_fold_plan_copies(h["plan"].data_ptr(), self.rows, self.plan_stride,
-                                      h["copy_src"].data_ptr(), h["copy_dst"].data_ptr(),
-                                      num_pairs, num_blocks)
+        p = self.ptr
+        rc = lib.vfl_fold_plan_copies(p["plan"], self.rows, self.plan_stride, p["copy_src"],
+                                      p["copy_dst"], num_pairs, num_blocks)
         return rc == 0
 
     def upload(self, grouped: bool = False) -> None:
