@@ -233,6 +233,7 @@ class ModelRunner:
         self._buffers = _StepBuffers(config.max_num_seqs, width, self.device)
         self._query_start_loc = torch.arange(config.max_num_seqs + 1, dtype=torch.int32,
                                              device=self.device)
+        self._qsl_views: dict[int, torch.Tensor] = {}  # its first padded + 1 entries
         self._cross_buffers = attention.CrossStagingBuffers(
             config.max_num_seqs, math.ceil(config.max_encoder_len / self.block_size), self.device)
         # decode steps captured per batch size (rows), replayed while the shapes repeat
@@ -450,11 +451,14 @@ class ModelRunner:
                 slots=slots, group_starts=request_runs(rows, padded, hip_attn.MAX_GROUP_SIZE))
             self._cross_key = key
         context_lens, tables, slot_mapping, input_ids, positions = buf.row_views(padded)
+        qsl = self._qsl_views.get(padded)
+        if qsl is None:
+            qsl = self._qsl_views[padded] = self._query_start_loc[: padded + 1]
         set_context(
             context_lens=context_lens,
             block_tables=tables,
             slot_mapping=slot_mapping,
-            query_start_loc=self._query_start_loc[: padded + 1],
+            query_start_loc=qsl,
             self_metadata=self_metadata,
             isa=self.isa,
             cross_staged=self._cross_staged,
