@@ -67,8 +67,9 @@ class _StepBuffers:
         words = self.plan_offset + 4 + rows * self.plan_stride
         self.host = torch.zeros(words, dtype=torch.int32, pin_memory=True)
         self.dev = torch.zeros(words, dtype=torch.int32, device=device)
-        self.copied = torch.cuda.Event()
-        self.copied.record()
+        # an upload the stream may not have finished: the staging must not be rewritten
+        # before a synchronization (every step ends with one, in its sampling)
+        self.in_flight = False
         self.h = self._views(self.host)
         self.d = self._views(self.dev)
         self.np = {k: v.numpy() for k, v in self.h.items()}
@@ -127,7 +128,7 @@ class _StepBuffers:
         if v is None:
             v = self._upload_views[words] = (self.dev[:words], self.host[:words])
         v[0].copy_(v[1], non_blocking=True)
-        self.copied.record()
+        self.in_flight = True  # (a flag, not an event: recording one costs ~4 us)
 
 
 _HOST_STAGING: dict[tuple, torch.Tensor] = {}
@@ -393,7 +394,9 @@ class ModelRunner:
                                                max(width, buf.width), self.device)
             self._graphs.clear()  # they read the old buffers
             self._self_metadata.clear()
-        buf.copied.synchronize()  # the previous step's upload has left the staging
+        if buf.in_flight:  # the previous upload must have left the staging
+            torch.cuda.current_stream(self.device).synchronize()
+            buf.in_flight = False
         h = buf.np
         # Beams of a request share their prefix blocks (copy-on-write forks): their
         # self-attention runs as row groups that read each shared block once; the group
@@ -550,7 +553,9 @@ class ModelRunner:
         finally:
             set_context()
         n = batch.num_rows  # the rows past n are padding
-        return self._sample(batch, logits[:n], self._buffers.d["lengths"][:n])
+        out = self._sample(batch, logits[:n], self._buffers.d["lengths"][:n])
+        self._buffers.in_flight = False  # sampling synchronized the stream
+        return out
 
     def _forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         """The decoder step, eager or replayed from a HIP graph of this batch size.
