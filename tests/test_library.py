@@ -234,6 +234,29 @@ def test_linear_validates_before_launch():
     assert pack(ptr=16 * 1000 + 8) == -1
 
 
+def test_embed_layer_norm_validates_before_launch():
+    """vfl_embed_layer_norm refuses bad sizes, null or misaligned pointers and empty tables
+    with an error code and message, before touching memory or the GPU."""
+    from vflorence_amd._lib import lib
+
+    a = 16 * 1000  # a 16-byte aligned stand-in address (never dereferenced)
+
+    def call(ids=a, pos=a, rows=4, tok=a, tok_rows=50, pos_t=a, pos_rows=12, dim=64,
+             stride=64, dtype=1, out=a):
+        return lib.vfl_embed_layer_norm(ids, pos, rows, tok, tok_rows, stride, 1.0, pos_t,
+                                        pos_rows, stride, 2, a, a, out, stride, dim, 1e-5,
+                                        dtype, None)
+
+    assert call(dtype=7) == -1 and b"dtype" in lib.vfl_last_error()
+    assert call(dim=66) == -1 and call(dim=8192) == -1   # a multiple of 4, at most 4096
+    assert call(stride=32) == -1                          # stride shorter than a row
+    assert call(tok=a + 4) == -1 and b"aligned" in lib.vfl_last_error()  # 4 bf16 = 8 bytes
+    assert call(out=None) == -1 and b"null" in lib.vfl_last_error()
+    assert call(ids=None) == -1 and call(pos=None) == -1
+    assert call(tok_rows=0) == -1 and call(pos_rows=0) == -1
+    assert call(rows=0) == 0                              # nothing to do, nothing read
+
+
 def test_cpu_tensors_are_rejected():
     import torch
 
